@@ -1,0 +1,221 @@
+"""Headline benchmark: boosting rounds/sec of pack-parallel tree growth on one MI355X.
+
+Workload (the north-star era panel): 2,400,000 rows x 2,376
+uint8 features quantised to 5 levels, 574 contiguous eras, pack_size 8, max_depth 6,
+per-depth feature fraction 0.1 (238 features), lr 0.01, lambda_dro 0.5, min_samples_leaf 20.
+Inputs are synthetic and generated directly in HBM (column-major bins); one step is one full
+boosting round (gradient, 6 depths of histogram -> DES score -> decide -> partition, pack
+aggregation, decision read-back and host tree build), the same span as the reference's
+round_seconds (booster.py:495, 654).
+
+Also reported: the histogram kernel's achieved HBM GB/s (algorithmic bytes / average launch
+time from HIP events on the fit's stream) against the 8 TB/s peak, and the CPU oracle
+(restated reference CPU frontier, C/OpenMP) timed on a bounded row sample on the host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "boosting rounds/sec (B=8,D=6, 2.4M×2376) on 1 GPU; hist-build HBM GB/s"
+
+CONFIGS = {
+    3: dict(rows=2_400_000, features=2376, eras=574, bins=5, pack_size=8, max_depth=6,
+            frac=0.1, lr=0.01, lambda_dro=0.5, lambda_l2=1e-6, msl=20),
+    2: dict(rows=200_000, features=100, eras=50, bins=128, pack_size=8, max_depth=5,
+            frac=1.0, lr=0.1, lambda_dro=0.0, lambda_l2=1e-6, msl=20),
+}
+
+
+def era_offsets(n: int, e: int) -> np.ndarray:
+    sizes = np.array([len(a) for a in np.array_split(np.arange(n), e)], dtype=np.int64)
+    off = np.zeros(e + 1, dtype=np.int64)
+    np.cumsum(sizes, out=off[1:])
+    return off.astype(np.int32)
+
+
+def make_device_data(c: dict, seed: int = 42):
+    """Config-3 style panel in HBM: uniform 5-level bins, quantised sparse-linear target with
+    era-specific sign flips on 10 of its 50 features."""
+    import torch
+
+    N, F, E, nb = c["rows"], c["features"], c["eras"], c["bins"]
+    ld = (N + 15) // 16 * 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    bins = torch.randint(0, nb, (F, ld), dtype=torch.uint8, device="cuda", generator=g)
+    cpu = torch.Generator().manual_seed(seed)
+    sel = torch.randperm(F, generator=cpu)[:50]
+    w = torch.randn(50, generator=cpu)
+    off = era_offsets(N, E)
+    era_id = torch.from_numpy(np.repeat(np.arange(E), np.diff(off))).cuda()
+    flips = torch.where(torch.rand(E, 10, generator=cpu) < 0.5, -1.0, 1.0).cuda()
+    lin = torch.zeros(N, device="cuda")
+    center = (nb - 1) / 2.0
+    for j in range(50):
+        col = bins[int(sel[j]), :N].float() - center
+        s = flips[era_id, j] if j < 10 else 1.0
+        lin += float(w[j]) * col * s
+    lin += torch.randn(N, device="cuda", generator=g) * lin.std() * 0.5
+    q = torch.quantile(lin[:: max(1, N // 200_000)], torch.tensor([0.2, 0.4, 0.6, 0.8], device="cuda"))
+    y = torch.bucketize(lin, q).float() / 4.0
+    return bins, y, off
+
+
+def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None) -> dict:
+    """Oracle (restated reference CPU frontier + fit loop) on a bounded row sample."""
+    from oracle import oracle as ref
+
+    N, F, E, nb = c["rows"], c["features"], c["eras"], c["bins"]
+    n_s = sample_rows or max(E * 50, N // 20)
+    rng = np.random.default_rng(0)
+    bins = rng.integers(0, nb, size=(n_s, F), dtype=np.uint8)
+    y = (rng.integers(0, 5, size=n_s) / 4.0).astype(np.float32)
+    codes = np.repeat(np.arange(E), np.diff(era_offsets(n_s, E)))
+    gen = __import__("torch").Generator().manual_seed(42)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 6 and (len(times) < 2 or time.perf_counter() - t_start < budget_s):
+        r = ref.fit(bins, y, codes, num_rounds=1, pack_size=c["pack_size"], max_depth=c["max_depth"],
+                    learning_rate=c["lr"], lambda_l2=c["lambda_l2"], lambda_dro=c["lambda_dro"],
+                    min_samples_leaf=c["msl"], max_bins=nb, layer_feature_fraction=c["frac"], rng=gen)
+        times.append(r.round_seconds[0])
+    steady = times[1:] if len(times) > 1 else times
+    sec = float(np.mean(steady))
+    return {
+        "value": (n_s / N) / sec,
+        "unit": "rounds/s",
+        "cores": int(ref.lib().oracle_num_threads()),
+        "kind": "port",
+        "sample": (f"{n_s} rows x {F} features (row-major int8), {E} eras, full {c['max_depth']}-depth "
+                   f"rounds; mean of {len(steady)} rounds = {sec:.3f} s, scaled by rows {n_s}/{N}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--rows", type=int, default=0, help="override row count (quick runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md for how the path would shard).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from packboost_amd import PackBoostConfig
+    from packboost_amd.engine import DeviceFit, tree_arrays_from_log
+
+    c = dict(CONFIGS[args.config])
+    if args.rows:
+        c["rows"] = args.rows
+    torch.cuda.set_device(0)
+    bins, y, off = make_device_data(c)
+    N = c["rows"]
+    cfg = PackBoostConfig(pack_size=c["pack_size"], max_depth=c["max_depth"], learning_rate=c["lr"],
+                          lambda_l2=c["lambda_l2"], lambda_dro=c["lambda_dro"],
+                          min_samples_leaf=c["msl"], max_bins=c["bins"],
+                          layer_feature_fraction=c["frac"], random_state=42, prebinned=True)
+    fit = DeviceFit(bins, N, y, off, cfg)
+    rng = torch.Generator().manual_seed(42)
+    print(f"[bench] config {args.config}: N={N} F={c['features']} E={c['eras']} K={fit.K} "
+          f"warmup={args.warmup} steps={args.steps}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        log = fit.run_round(rng)
+        tree_arrays_from_log(log, cfg, N)
+    torch.cuda.synchronize()
+    events: list = []
+    logs = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        log = fit.run_round(rng, events)
+        tree_arrays_from_log(log, cfg, N)
+        logs.append(log)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    # histogram roofline: algorithmic bytes per launch = rows of active nodes x K bin bytes
+    # + rows x 6 (grad f32 + node id u16) + written planes U x E x K x nb x 8
+    K, E, nb = fit.K, fit.E, fit.nb
+    phase_ms: dict[str, float] = {}
+    hist_bytes = 0.0
+    hist_ms = 0.0
+    n_hist = 0
+    for (phase, d, a, b), log in zip(events, [l for l in logs for _ in range(4 * fit.D)]):
+        ms = a.elapsed_time(b)
+        phase_ms[phase] = phase_ms.get(phase, 0.0) + ms
+        if phase == "hist":
+            u = int(log.u_active[d])
+            if u == 0:
+                continue
+            base = (1 << d) - 1
+            rows = int(log.decisions[base: base + u]["node_count"].astype(np.int64).sum())
+            hist_bytes += rows * K + rows * 6 + u * E * K * nb * 8
+            hist_ms += ms
+            n_hist += 1
+    achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
+    rounds_per_s = args.steps / elapsed
+    out = {
+        "metric": METRIC,
+        "value": round(rounds_per_s, 4),
+        "unit": "rounds/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (generated in HBM: uniform 5-level bins, quantised sparse-linear target)",
+        "config": {
+            "workload": (f"config{args.config}: {N} rows x {c['features']} features, {c['eras']} eras, "
+                         f"{c['bins']} bins, B={c['pack_size']}, D={c['max_depth']}, K={K}/depth"),
+            "rows": N, "features": c["features"], "eras": c["eras"], "max_bins": c["bins"],
+            "pack_size": c["pack_size"], "max_depth": c["max_depth"], "features_per_depth": K,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "hist_era_kernel",
+            "avg_launch_ms": round(hist_ms / max(n_hist, 1), 4),
+            "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
+        },
+        "phase_ms_per_round": {k: round(v / args.steps, 4) for k, v in phase_ms.items()},
+        "cpu_baseline": None,
+    }
+    fit.close()
+    del bins
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle on a row sample", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(c, args.cpu_budget)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

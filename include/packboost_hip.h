@@ -1,0 +1,223 @@
+/*
+ * packboost_hip.h — C ABI of libpackboost_hip.so, the MI355X (gfx950) backend for
+ * PackBoost's pack-parallel, layer-wise tree growth and pack prediction.
+ *
+ * Conventions
+ *   - Every entry point returns an int status: PB_OK (0) or a negative PB_ERR_* code.
+ *     pb_last_error() returns a thread-local message for the last failure on the
+ *     calling thread. HIP failures are reported as "HIP error: ..." so a caller that
+ *     pattern-matches the reference's "CUDA error" fallback can match either spelling.
+ *   - All pointers named *_dev are device pointers allocated by the caller; the
+ *     library never frees caller memory. Persistent scratch belongs to pb_ctx.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is
+ *     enqueued asynchronously; no entry point synchronises the device unless stated.
+ *   - Row-indexed device arrays (grad, node ids, ...) must hold `rows_padded`
+ *     (= N rounded up to a multiple of 16) elements; the pad rows must carry
+ *     node id PB_INACTIVE and grad 0. Bins are column-major uint8 [F][ld] with
+ *     ld % 16 == 0, ld >= N, 16-byte aligned base, and rows sorted era-major so
+ *     era e occupies rows [era_off[e], era_off[e+1]).
+ *
+ * The reference binds its native path through pybind11 (packboost/backends/bindings.cpp:11-24)
+ * and the Python shim packboost/backends/__init__.py:9-163. Each entry point below names
+ * the reference interface it replaces.
+ */
+#ifndef PACKBOOST_HIP_H
+#define PACKBOOST_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PB_OK 0
+#define PB_ERR_INVALID (-1)     /* bad argument / shape / id (reference: std::invalid_argument) */
+#define PB_ERR_RANGE (-2)       /* index out of range (reference: std::out_of_range) */
+#define PB_ERR_HIP (-3)         /* HIP runtime failure (reference: "CUDA error: ...") */
+#define PB_ERR_UNSUPPORTED (-4) /* configuration this build does not handle */
+#define PB_ERR_NOMEM (-5)
+
+#define PB_INACTIVE 0xFFFFu     /* node id of a row that is in no active frontier node */
+#define PB_MAX_DEPTH 16
+
+typedef struct pb_ctx pb_ctx;
+
+/* Shape of one fit. Replaces the implicit shapes the reference reads from its tensors
+ * (frontier_cpu.cpp:131-140, frontier_cuda.cu:576-632). */
+typedef struct {
+    int64_t num_rows;      /* N */
+    int64_t ld;            /* byte stride between feature columns of bins (>= N, %16 == 0) */
+    int32_t num_features;  /* F */
+    int32_t num_eras;      /* E (>= 1) */
+    int32_t max_bins;      /* nb, 2..255 */
+    int32_t max_depth;     /* D, 1..PB_MAX_DEPTH */
+    int32_t max_feats;     /* largest feature subset per depth, K */
+    int32_t min_samples_leaf;
+} pb_dims;
+
+/* Split-scoring hyper-parameters; the reference passes them one by one
+ * (frontier_cpu.cpp:116-123) as C++ float after pybind's double->float cast, while
+ * leaf values use the Python double (booster.py:545-546). They are carried here as
+ * double; the scorer rounds each to float exactly as that cast does.
+ * cut_selection: 0 = "even", 1 = "mass". */
+typedef struct {
+    double lambda_l2;
+    double lambda_dro;
+    double direction_weight;
+    double era_alpha;
+    int32_t min_samples_leaf;
+    int32_t k_cuts;
+    int32_t cut_selection;
+    int32_t reserved;
+} pb_split_params;
+
+/* One entry per active frontier node and depth: the reference's SplitDecision
+ * (booster.py:205-217) without row lists, plus the node's tree ids. */
+typedef struct {
+    int32_t node_id;      /* TreeBuilder id of the node */
+    int32_t split;        /* 1: split, 0: became a leaf (no valid candidate) */
+    int32_t feature;
+    int32_t threshold;
+    float score;
+    float left_grad;
+    float left_hess;
+    float right_grad;
+    float right_hess;
+    int32_t left_count;
+    int32_t right_count;
+    int32_t left_id;      /* TreeBuilder ids of the children (split only) */
+    int32_t right_id;
+    float node_grad;      /* sum of grad over the node's rows (float32) */
+    int32_t node_count;   /* rows in the node */
+    int32_t reserved;
+} pb_decision;
+
+/* Candidate record (one per wavefront winner, or per lane when dumped for tests). */
+typedef struct {
+    float score;
+    int32_t left_total;
+    float left_grad;
+    int32_t feature;
+    int32_t threshold;
+    int32_t valid;
+    int32_t reserved[2];
+} pb_candidate;
+
+/* ---- library ---------------------------------------------------------------------- */
+const char* pb_last_error(void);
+int32_t pb_version(void);
+/* Reference: _cuda_available (bindings.cpp:15-22 / backends/__init__.py:95-113). 1 if a gfx950 device is usable. */
+int32_t pb_device_available(void);
+
+/* ---- context ---------------------------------------------------------------------- */
+/* Allocates the persistent scratch for one fit (frontier state, decision tables,
+ * candidate buffers). era_off_host: int32 [E+1], era_off[0] = 0, era_off[E] = N.
+ * Replaces the per-call context build of frontier_cpu.cpp:142-209. */
+int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out);
+int pb_ctx_destroy(pb_ctx* ctx);
+/* Bytes of the two histogram planes (counts int32, grad float32) pb_hist_build writes
+ * for a depth with up to `max_nodes` active nodes: E * max_nodes * K * nb * 4 each. */
+int64_t pb_hist_plane_elems(const pb_ctx* ctx, int32_t max_nodes);
+/* Largest active-node count the frontier can reach at `depth`. */
+int32_t pb_max_nodes(const pb_ctx* ctx, int32_t depth);
+/* Device pointer of the era offsets (int32 [E+1]) the context holds. */
+const int32_t* pb_era_offsets_dev(const pb_ctx* ctx);
+
+/* ---- round driver ------------------------------------------------------------------ */
+/* grad = preds - y (booster.py:2149-2151, squared loss; hess == 1, booster.py:2153-2154);
+ * resets the per-round frontier: every row in root node 0 (active iff N >= 2*msl,
+ * booster.py:794-796), tree size 1. Also records max|grad| for the histogram's
+ * fixed-point scale. */
+int pb_round_begin(pb_ctx* ctx, const float* preds_dev, const float* y_dev, float* grad_dev,
+                   uint16_t* nid_dev, uint16_t* tnode_dev, void* stream);
+
+/* Kernel 1 — histogram build. Replaces the per-feature histogram + scan of
+ * find_best_splits_batched_cpu (frontier_cpu.cpp:261-321) and the histogram part of
+ * cuda_find_best_splits_kernel (frontier_cuda.cu:441-498). For every active node u,
+ * era e, sampled feature k and bin b writes, into [E][max_nodes][K][nb] planes:
+ *   cnt[e][u][k][b] = rows with bin <= b (b < nb-1), total rows at b = nb-1
+ *   grad[e][u][k][b] = float32 running sum over bins of the per-bin grad sums.
+ * feats_dev: int32 [K] feature ids; `depth` selects the frontier's active-node count. */
+int pb_hist_build(pb_ctx* ctx, const uint8_t* bins_dev, const float* grad_dev,
+                  const uint16_t* nid_dev, const int32_t* feats_dev, int32_t K, int32_t depth,
+                  int32_t max_nodes, int32_t* hist_cnt_dev, float* hist_grad_dev, void* stream);
+
+/* Kernel 2 — DES split scoring + argmax. Replaces the scoring/tie-break loop of
+ * frontier_cpu.cpp:342-444 (and frontier_cuda.cu:500-571 + booster.py:1451-1467).
+ * Reads the planes written by pb_hist_build, scores every (node, feature, threshold)
+ * by era-weighted Welford mean - lambda_dro * std (+ direction term), and keeps the
+ * best candidate per node. cand_all_dev (optional, may be NULL) receives one record
+ * per (node, feature, threshold) lane: [max_nodes][K][T]. */
+int pb_des_score(pb_ctx* ctx, const int32_t* hist_cnt_dev, const float* hist_grad_dev,
+                 const int32_t* feats_dev, int32_t K, int32_t depth, int32_t max_nodes,
+                 const pb_split_params* params, pb_candidate* cand_all_dev, void* stream);
+
+/* Applies the per-node winners of the last pb_des_score: builds the decisions of this
+ * depth (booster.py:527-563: split -> children ids (len, len+1), child values
+ * -G/(H+lambda); no split -> leaf value -G/(H+lambda)), assigns the next frontier
+ * (children with >= 2*msl rows, booster.py:516, 794-796) and writes the depth's
+ * decisions to decisions_dev + (2^depth - 1) (pb_decision [2^D - 1] per round).
+ * values_dev: float32 [2^(D+1)] leaf value per TreeBuilder node id. */
+int pb_decide(pb_ctx* ctx, int32_t depth, int32_t max_nodes, const pb_split_params* params,
+              pb_decision* decisions_dev, float* values_dev, void* stream);
+
+/* Kernel 3 — partition. Replaces the stable per-era left/right row split of
+ * frontier_cpu.cpp:446-497 and partition_frontier_cuda (frontier_cuda.cu:719-851):
+ * every row of a split node moves to child 2j+(bin > thr) (TreeBuilder ids) and to its
+ * slot in the next frontier (PB_INACTIVE if the child is below capacity); rows of a
+ * node that did not split leave the frontier. */
+int pb_partition(pb_ctx* ctx, const uint8_t* bins_dev, int32_t depth, uint16_t* nid_dev,
+                 uint16_t* tnode_dev, void* stream);
+
+/* Pack aggregation (booster.py:581-599): pack_sum[r] = sum over the pack's `pack_size`
+ * identical trees of float32(value[leaf(r)]) in tree order; preds += float32(lr) * pack_sum. */
+int pb_round_end(pb_ctx* ctx, const uint16_t* tnode_dev, const float* values_dev,
+                 int32_t pack_size, float learning_rate, float* preds_dev, void* stream);
+
+/* Teacher-forces the frontier of `depth`: `num_active` active slots whose TreeBuilder ids are
+ * node_ids_host (NULL: 0..num_active-1) and a tree size of `tree_size`. Lets a caller run one
+ * depth on its own row -> slot assignment (nid); the reference takes that assignment as the
+ * per-node era row lists of find_best_splits_batched_cpu (frontier_cpu.cpp:111-124). */
+int pb_frontier_set(pb_ctx* ctx, int32_t depth, int32_t num_active, const int32_t* node_ids_host,
+                    int32_t tree_size, void* stream);
+
+/* Copies the frontier's per-depth active-node counts (int32 [PB_MAX_DEPTH+1]) and the
+ * tree size to host memory; synchronises `stream`. */
+int pb_frontier_counts(pb_ctx* ctx, int32_t* u_active_host, int32_t* tree_size_host, void* stream);
+
+/* ---- prediction --------------------------------------------------------------------- */
+/* Kernel 4 — batched pack prediction. Replaces predict_pack_cuda (frontier_cuda.cu:925-1068):
+ * out[r] = tree_weight * sum_t value(leaf_t(r)) over the B trees of one packed forest
+ * (the SoA layout of booster.py:730-783: feature, threshold, left_abs, right_abs int32,
+ * value float32, is_leaf uint8, offsets int32 [B+1]). Traversal: left iff bin <= threshold.
+ * bins_dev: column-major uint8 [F][ld], N rows. out_dev is overwritten (not accumulated).
+ * leaf_dev (optional, may be NULL): int32 [B][N] absolute leaf index per tree and row. */
+int pb_predict_pack(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
+                    const int32_t* feature_dev, const int32_t* threshold_dev,
+                    const int32_t* left_abs_dev, const int32_t* right_abs_dev,
+                    const float* value_dev, const uint8_t* is_leaf_dev,
+                    const int32_t* offsets_dev, int32_t B, int32_t total_nodes,
+                    float tree_weight, float* out_dev, int32_t* leaf_dev, void* stream);
+
+/* Whole forest in PackBoost.predict's CPU order (booster.py:709-712): out[r] = sum over the
+ * T trees in order of float32(tree_weight * value(leaf_t(r))), one float32 rounding per
+ * product and per add. Same SoA layout as pb_predict_pack with offsets int32 [T+1]. */
+int pb_predict_forest(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
+                      const int32_t* feature_dev, const int32_t* threshold_dev,
+                      const int32_t* left_abs_dev, const int32_t* right_abs_dev,
+                      const float* value_dev, const uint8_t* is_leaf_dev,
+                      const int32_t* offsets_dev, int32_t T, int32_t total_nodes,
+                      float tree_weight, float* out_dev, void* stream);
+
+/* Single tree. Replaces predict_bins_cuda (frontier_cuda.cu:193-233, 853-920):
+ * out[r] = value(leaf(r)) with child indices relative to the tree. */
+int pb_predict_bins(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
+                    const int32_t* feature_dev, const int32_t* threshold_dev,
+                    const int32_t* left_dev, const int32_t* right_dev,
+                    const float* value_dev, const uint8_t* is_leaf_dev, int32_t num_nodes,
+                    float* out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PACKBOOST_HIP_H */

@@ -1,0 +1,429 @@
+"""PackBoost: pack-parallel gradient boosting with Directional Era Splitting on MI355X.
+
+Public surface and model format follow the reference's packboost/booster.py:
+  * TreeNode / Tree / TreeBuilder (booster.py:25-190) — same fields and child numbering;
+  * PackBoost(config).fit(X, y, era, *, num_rounds, feature_names, eval_sets, round_callback),
+    .predict(X), .predict_packwise(X, block_size_trees), .trees, .round_metrics,
+    ._depth_logs, ._tree_weight, ._binner (booster.py:289-726).
+The split finder, partition, pack aggregation and prediction run as HIP kernels on the
+device (engine.DeviceFit); there is no CPU compute path.
+"""
+
+from __future__ import annotations
+
+import json
+import logging
+import os
+from dataclasses import dataclass, field
+from time import perf_counter
+from typing import Callable, Iterable, List, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from . import backends as native_backends
+from .backends import _hip
+from .config import PackBoostConfig
+from .data import (BinningResult, apply_bins, encode_eras, era_major_order,
+                   feature_names_or_default, preprocess_features)
+from .engine import (DeviceFit, column_major_bins, depth_log_from_round, padded_rows,
+                     subset_size, tree_arrays_from_log)
+
+
+# ------------------------------------------------------------------ tree structures
+@dataclass(slots=True)
+class TreeNode:
+    feature: int = -1
+    threshold: int = 0
+    left: int = -1
+    right: int = -1
+    value: float = 0.0
+    is_leaf: bool = True
+
+
+@dataclass(slots=True)
+class Tree:
+    nodes: List[TreeNode]
+    _compiled: dict = field(init=False, repr=False, default_factory=dict)
+
+    def _ensure_compiled(self, device: torch.device) -> dict[str, torch.Tensor]:
+        key = str(device)
+        c = self._compiled.get(key)
+        if c is None:
+            c = {
+                "feature": torch.tensor([n.feature for n in self.nodes], dtype=torch.int32, device=device),
+                "threshold": torch.tensor([n.threshold for n in self.nodes], dtype=torch.int32, device=device),
+                "left": torch.tensor([n.left for n in self.nodes], dtype=torch.int32, device=device),
+                "right": torch.tensor([n.right for n in self.nodes], dtype=torch.int32, device=device),
+                "value": torch.tensor([n.value for n in self.nodes], dtype=torch.float32, device=device),
+                "is_leaf": torch.tensor([n.is_leaf for n in self.nodes], dtype=torch.bool, device=device),
+            }
+            self._compiled[key] = c
+        return c
+
+    def predict_bins(self, bins: torch.Tensor) -> torch.Tensor:
+        """Leaf value per row of integer bins [N, F] (left iff bin <= threshold), on the GPU."""
+        N = int(bins.shape[0])
+        device = _device_of(bins)
+        if N == 0:
+            return torch.empty(0, dtype=torch.float32, device=bins.device)
+        bins_fm = _to_column_major(bins, device)
+        c = self._ensure_compiled(device)
+        out = torch.empty(N, dtype=torch.float32, device=device)
+        lib = _hip.load()
+        _hip.check(lib.pb_predict_bins(
+            bins_fm.data_ptr(), N, bins_fm.shape[1], bins_fm.shape[0], c["feature"].data_ptr(),
+            c["threshold"].data_ptr(), c["left"].data_ptr(), c["right"].data_ptr(),
+            c["value"].data_ptr(), c["is_leaf"].to(torch.uint8).data_ptr(), len(self.nodes),
+            out.data_ptr(), _hip.stream_ptr()), "pb_predict_bins")
+        return out.to(bins.device)
+
+
+class TreeBuilder:
+    def __init__(self) -> None:
+        self.nodes: List[TreeNode] = [TreeNode()]
+
+    def set_leaf(self, node_id: int, value: float) -> None:
+        n = self.nodes[node_id]
+        n.value = float(value); n.is_leaf = True
+        n.feature = -1; n.threshold = 0; n.left = -1; n.right = -1
+
+    def split(self, node_id: int, feature: int, threshold: int) -> Tuple[int, int]:
+        n = self.nodes[node_id]
+        n.feature = int(feature); n.threshold = int(threshold); n.is_leaf = False
+        l = len(self.nodes); r = l + 1
+        n.left = l; n.right = r
+        self.nodes.append(TreeNode()); self.nodes.append(TreeNode())
+        return l, r
+
+    def build(self) -> Tree:
+        return Tree(nodes=self.nodes)
+
+
+def _tree_from_arrays(a: dict[str, np.ndarray]) -> Tree:
+    nodes = [TreeNode(int(f), int(t), int(l), int(r), float(v), bool(lf))
+             for f, t, l, r, v, lf in zip(a["feature"], a["threshold"], a["left"], a["right"],
+                                          a["value"], a["is_leaf"])]
+    return Tree(nodes=nodes)
+
+
+def _device_of(x) -> torch.device:
+    if isinstance(x, torch.Tensor) and x.is_cuda:
+        return x.device
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _to_column_major(bins, device: torch.device) -> torch.Tensor:
+    """Row-major integer bins [N, F] (numpy or torch) -> contiguous uint8 [F, ld] on device."""
+    if isinstance(bins, torch.Tensor):
+        t = bins
+    else:
+        t = torch.from_numpy(np.ascontiguousarray(bins))
+    if t.dtype not in (torch.uint8, torch.int8):
+        t = t.to(torch.uint8)
+    N, F = t.shape
+    ld = padded_rows(int(N))
+    out = torch.zeros((int(F), ld), dtype=torch.uint8, device=device)
+    out[:, :N] = t.to(device).view(torch.uint8).t()
+    return out
+
+
+def _require_backend(device: torch.device) -> None:
+    if device.type != "cuda":
+        raise RuntimeError(
+            "packboost_amd runs on the MI355X HIP backend only; use PackBoostConfig(device='cuda')")
+    if not torch.cuda.is_available():
+        raise RuntimeError("HIP error: no GPU device is visible to torch")
+    _hip.load()
+
+
+# ------------------------------------------------------------------ booster
+class PackBoost:
+    """Pack-parallel gradient booster with DES scoring (squared loss)."""
+
+    def __init__(self, config: PackBoostConfig) -> None:
+        self.config = config
+        self._device = torch.device(config.device)
+        self._rng = torch.Generator(device="cpu")
+        if config.random_state is not None:
+            self._rng.manual_seed(int(config.random_state))
+        mode = (os.getenv("PACKBOOST_HIST_MODE") or config.histogram_mode).lower()
+        if mode not in {"rebuild", "subtract", "auto"}:
+            raise ValueError(f"Unsupported histogram_mode: {mode}")
+        if config.cut_selection not in ("even", "mass"):
+            raise ValueError(f"Unsupported cut_selection: {config.cut_selection}")
+        self._histogram_mode = mode
+        self._logger = logging.getLogger(__name__)
+        self._depth_logs: list[dict[str, object]] = []
+        self._binner: BinningResult | None = None
+        self._rounds: list[dict[str, np.ndarray]] = []   # one tree's arrays per round
+        self._trees_cache: list[Tree] | None = None
+        self._era_unique: np.ndarray | None = None
+        self._feature_names: list[str] | None = None
+        self._tree_weight: float | None = None
+        self._trained_pack_size: int | None = None
+        self._round_metrics: list[dict[str, float]] = []
+        self._packed_forest: list[dict[str, torch.Tensor]] = []
+        self._num_features: int | None = None
+        self._use_native_cuda = self._device.type == "cuda" and native_backends.cuda_available()
+
+    # ---------------------------------------------------------------- public
+    @property
+    def trees(self) -> Sequence[Tree]:
+        if self._trees_cache is None:
+            B = int(self._trained_pack_size or self.config.pack_size)
+            out: list[Tree] = []
+            for arrs in self._rounds:
+                for _ in range(B):
+                    out.append(_tree_from_arrays(arrs))
+            self._trees_cache = out
+        return self._trees_cache
+
+    @property
+    def round_metrics(self) -> Sequence[dict[str, float]]:
+        return self._round_metrics
+
+    def fit(self, X, y, era: Iterable[int] | None, *, num_rounds: int,
+            feature_names: Sequence[str] | None = None,
+            eval_sets: Sequence[tuple] | None = None,
+            round_callback: Callable[[int, dict[str, float]], None] | None = None) -> "PackBoost":
+        """Squared-loss boosting with pack-synchronous growth and DES (booster.py:375-656)."""
+        _require_backend(self._device)
+        cfg = self.config
+        y_np = np.asarray(y.detach().cpu().numpy() if isinstance(y, torch.Tensor) else y,
+                          dtype=np.float32)
+        if y_np.ndim != 1:
+            raise ValueError("y must be 1-D")
+        if isinstance(X, torch.Tensor):
+            N, F = int(X.shape[0]), int(X.shape[1])
+        else:
+            X_arr = np.asarray(X.to_numpy() if hasattr(X, "to_numpy") else X)
+            N, F = X_arr.shape
+        if N != y_np.shape[0]:
+            raise ValueError("X and y row mismatch")
+        codes, uniq = encode_eras(era, N)
+        self._era_unique = uniq
+        E = int(uniq.shape[0])
+        self._feature_names = feature_names_or_default(feature_names, F)
+        self._num_features = F
+
+        if isinstance(X, torch.Tensor):
+            if X.dtype.is_floating_point:
+                raise ValueError("torch inputs must be integer bins (prebinned)")
+            self._binner = BinningResult(bins=np.empty((0, F), np.uint8), bin_edges=None, prebinned=True)
+            bins_src = X
+        else:
+            self._binner = preprocess_features(X_arr, cfg.max_bins, assume_prebinned=bool(cfg.prebinned))
+            bins_src = self._binner.bins
+        perm, offsets = era_major_order(codes, E)
+        device = self._device if self._device.index is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        bins_fm = column_major_bins(bins_src, perm, device)
+        if N and int(bins_fm[:, :N].max().item()) >= cfg.max_bins:
+            raise ValueError("bins must lie in [0, max_bins)")
+        y_dev = torch.from_numpy(y_np if perm is None else y_np[perm]).to(device)
+        self._perm = perm
+        self._depth_logs = []
+        self._round_metrics = []
+        self._rounds = []
+        self._trees_cache = None
+        self._packed_forest = []
+        self._tree_weight = None
+        self._trained_pack_size = None
+
+        fitter = DeviceFit(bins_fm, N, y_dev, offsets, cfg)
+        self._fitter = fitter
+        k = subset_size(cfg, F)
+        era_ids_dev = torch.from_numpy(np.repeat(np.arange(E), np.diff(offsets))).to(device)
+        eval_states = self._prepare_eval(eval_sets, device)
+        eval_every = _eval_every()
+        try:
+            for round_idx in range(num_rounds):
+                t0 = perf_counter()
+                log = fitter.run_round(self._rng)
+                arrs = tree_arrays_from_log(log, cfg, N)
+                self._rounds.append(arrs)
+                self._trees_cache = None
+                self._tree_weight = float(cfg.learning_rate)
+                self._trained_pack_size = int(cfg.pack_size)
+                for d in range(int(cfg.max_depth)):
+                    if int(log.u_active[d]) <= 0:
+                        break
+                    dl = depth_log_from_round(log, d, cfg, k, self._histogram_mode)
+                    self._depth_logs.append(dl)
+                    if self._logger.isEnabledFor(logging.INFO):
+                        self._logger.info(json.dumps(dl))
+                if eval_states and eval_every > 0 and (
+                        (round_idx + 1) % eval_every == 0 or round_idx + 1 == num_rounds):
+                    self._update_eval(eval_states)
+                round_time = perf_counter() - t0
+                metrics = {
+                    "round": round_idx + 1,
+                    "train_corr": _era_corr_device(era_ids_dev, fitter.y[:N], fitter.preds[:N], E),
+                    "trees_per_second": (cfg.pack_size / round_time) if round_time > 0 else float("inf"),
+                    "round_seconds": round_time,
+                }
+                for st in eval_states:
+                    metrics[f"{st['name']}_corr"] = _era_corr_device(
+                        st["era_ids"], st["y"], st["preds"], st["num_eras"])
+                self._round_metrics.append(metrics)
+                if round_callback is not None:
+                    round_callback(round_idx + 1, metrics)
+        finally:
+            torch.cuda.synchronize(device)
+        self._train_preds = fitter.preds[:N].clone()
+        fitter.close()
+        self._fitter = None
+        return self
+
+    def predict(self, X) -> np.ndarray:
+        """Sum over all trees in order of float32(tree_weight * leaf value) (booster.py:709-712)."""
+        if self._binner is None:
+            raise RuntimeError("Model must be fitted before predict()")
+        _require_backend(self._device)
+        if self._trained_pack_size is not None and int(self.config.pack_size) != self._trained_pack_size:
+            raise RuntimeError("pack_size differs from training; keep it constant.")
+        if isinstance(X, torch.Tensor):
+            bins = X
+            N = int(X.shape[0])
+        else:
+            bins = apply_bins(X, self._binner.bin_edges, self.config.max_bins)
+            N = bins.shape[0]
+        if not self._rounds:
+            return np.zeros(N, dtype=np.float32)
+        if self._tree_weight is None:
+            raise RuntimeError("Missing _tree_weight; call fit() first.")
+        device = _device_of(bins)
+        bins_fm = _to_column_major(bins, device)
+        out = self._predict_device(bins_fm, N, device)
+        return out.cpu().numpy()
+
+    def predict_packwise(self, X, block_size_trees: int = 8) -> np.ndarray:
+        if block_size_trees <= 0:
+            raise ValueError("block_size_trees must be positive")
+        if self._binner is None:
+            raise RuntimeError("Model must be fitted before predict_packwise()")
+        return self.predict(X)
+
+    # ---------------------------------------------------------------- internals
+    def _forest_device(self, device: torch.device) -> dict[str, torch.Tensor]:
+        key = (str(device), len(self._rounds))
+        cached = getattr(self, "_forest_cache", None)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        forest = pack_forest(self._rounds, int(self._trained_pack_size or self.config.pack_size), device)
+        self._forest_cache = (key, forest)
+        return forest
+
+    def _predict_device(self, bins_fm: torch.Tensor, N: int, device: torch.device) -> torch.Tensor:
+        f = self._forest_device(device)
+        out = torch.empty(N, dtype=torch.float32, device=device)
+        lib = _hip.load()
+        _hip.check(lib.pb_predict_forest(
+            bins_fm.data_ptr(), N, bins_fm.shape[1], bins_fm.shape[0], f["feature"].data_ptr(),
+            f["threshold"].data_ptr(), f["left_abs"].data_ptr(), f["right_abs"].data_ptr(),
+            f["value"].data_ptr(), f["is_leaf"].data_ptr(), f["offsets"].data_ptr(),
+            int(f["offsets"].numel() - 1), int(f["value"].numel()),
+            float(self._tree_weight), out.data_ptr(), _hip.stream_ptr()), "pb_predict_forest")
+        return out
+
+    def _prepare_eval(self, eval_sets, device) -> list[dict]:
+        states = []
+        for item in eval_sets or ():
+            name, X_eval, y_eval, era_eval = item
+            if y_eval is None:
+                raise ValueError(f"eval set '{name}' requires y values for correlation logging")
+            if self.config.prebinned or self._binner.bin_edges is None:
+                b = apply_bins(X_eval, None, self.config.max_bins)
+            else:
+                b = apply_bins(X_eval, self._binner.bin_edges, self.config.max_bins)
+            n = b.shape[0]
+            codes, uniq = encode_eras(era_eval, n)
+            states.append({
+                "name": name, "bins_fm": _to_column_major(b, device), "n": n,
+                "y": torch.from_numpy(np.asarray(y_eval, dtype=np.float32)).to(device),
+                "era_ids": torch.from_numpy(codes.astype(np.int64)).to(device),
+                "num_eras": int(uniq.shape[0]),
+                "preds": torch.zeros(n, dtype=torch.float32, device=device),
+            })
+        return states
+
+    def _update_eval(self, states: list[dict]) -> None:
+        # Like the reference (booster.py:236-274) the eval predictions are recomputed over
+        # every tree so far, in tree order, so they equal predict() on the same rows.
+        B = int(self.config.pack_size)
+        lib = _hip.load()
+        for st in states:
+            f = pack_forest(self._rounds, B, st["preds"].device)
+            out = torch.empty_like(st["preds"])
+            _hip.check(lib.pb_predict_forest(
+                st["bins_fm"].data_ptr(), st["n"], st["bins_fm"].shape[1], st["bins_fm"].shape[0],
+                f["feature"].data_ptr(), f["threshold"].data_ptr(), f["left_abs"].data_ptr(),
+                f["right_abs"].data_ptr(), f["value"].data_ptr(), f["is_leaf"].data_ptr(),
+                f["offsets"].data_ptr(), int(f["offsets"].numel() - 1), int(f["value"].numel()),
+                float(self._tree_weight), out.data_ptr(), _hip.stream_ptr()), "pb_predict_forest")
+            st["preds"] = out
+
+
+def pack_forest(rounds: Sequence[dict[str, np.ndarray]], pack_size: int,
+                device: torch.device) -> dict[str, torch.Tensor]:
+    """Packed SoA of every tree (booster.py:730-783 layout, children as absolute indices)."""
+    feats, thrs, lefts, rights, vals, leafs, offs = [], [], [], [], [], [], [0]
+    for a in rounds:
+        n = a["feature"].shape[0]
+        for _ in range(pack_size):
+            base = offs[-1]
+            feats.append(a["feature"].astype(np.int32))
+            thrs.append(a["threshold"].astype(np.int32))
+            lf = a["is_leaf"]
+            lefts.append(np.where(lf | (a["left"] < 0), -1, a["left"] + base).astype(np.int32))
+            rights.append(np.where(lf | (a["right"] < 0), -1, a["right"] + base).astype(np.int32))
+            vals.append(a["value"].astype(np.float32))
+            leafs.append(lf.astype(np.uint8))
+            offs.append(base + n)
+    cat = np.concatenate
+    return {
+        "feature": torch.from_numpy(cat(feats)).to(device),
+        "threshold": torch.from_numpy(cat(thrs)).to(device),
+        "left_abs": torch.from_numpy(cat(lefts)).to(device),
+        "right_abs": torch.from_numpy(cat(rights)).to(device),
+        "value": torch.from_numpy(cat(vals)).to(device),
+        "is_leaf": torch.from_numpy(cat(leafs)).to(device),
+        "offsets": torch.tensor(offs, dtype=torch.int32, device=device),
+    }
+
+
+def _eval_every() -> int:
+    try:
+        return int(os.getenv("PACKBOOST_EVAL_EVERY", "1"))
+    except ValueError:
+        return 1
+
+
+def _era_corr_device(era_ids: torch.Tensor, y: torch.Tensor, p: torch.Tensor, num_eras: int) -> float:
+    """Mean over eras of the Pearson correlation of y and preds (booster.py:909-929).
+
+    Eras with < 2 rows or a (near-)constant side are skipped; NaN if none remain.
+    """
+    yd = y.double()
+    pd_ = p.double()
+    ones = torch.ones_like(yd)
+
+    def seg(v):
+        return torch.zeros(num_eras, dtype=torch.float64, device=v.device).index_add_(0, era_ids, v)
+
+    n = seg(ones)
+    sy, sp = seg(yd), seg(pd_)
+    syy, spp, syp = seg(yd * yd), seg(pd_ * pd_), seg(yd * pd_)
+    nn = n.clamp_min(1)
+    my, mp = sy / nn, sp / nn
+    vy = (syy / nn - my * my).clamp_min(0)
+    vp = (spp / nn - mp * mp).clamp_min(0)
+    cov = syp / nn - my * mp
+    sy_, sp_ = vy.sqrt(), vp.sqrt()
+    ok = (n >= 2) & (sy_ > 1e-12) & (sp_ > 1e-12)
+    if not bool(ok.any()):
+        return float("nan")
+    corr = cov[ok] / (sy_[ok] * sp_[ok])
+    corr = corr[torch.isfinite(corr)]
+    return float(corr.mean().item()) if corr.numel() else float("nan")

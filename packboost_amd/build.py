@@ -1,0 +1,76 @@
+"""Builds libpackboost_hip.so (gfx950) in-tree with hipcc.
+
+Every HIP source is compiled with:
+  -ffp-contract=off      no FMA contraction: the DES scorer and the pack aggregation issue
+                         the reference's float32 operations one rounding at a time;
+  -packed-fp32-ops off   no packed-FP32 VALU instructions (gfx950 code is plain FP32 VALU).
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+LIB_NAME = "libpackboost_hip.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+SOURCES = ["hist.hip", "score.hip", "partition.hip", "predict.hip", "capi.cpp"]
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    cand = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(cand).exists():
+        raise RuntimeError("hipcc not found (ROCm toolchain required to build the HIP backend)")
+    return cand
+
+
+def compile_flags() -> list[str]:
+    return [
+        "-x", "hip",
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-ffp-contract=off",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall",
+        "-Wno-unused-function",
+        "-I", str(PKG_DIR.parent / "include"),
+    ]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compiles every source for gfx950 and links the shared library. Always rebuilds."""
+    cc = hipcc()
+    out_dir = PKG_DIR / "_build"
+    out_dir.mkdir(exist_ok=True)
+
+    def one(src: str) -> Path:
+        obj = out_dir / (Path(src).stem + ".o")
+        cmd = [cc, *compile_flags(), "-c", str(CSRC / src), "-o", str(obj)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")
+        if verbose and res.stderr.strip():
+            print(res.stderr, file=sys.stderr)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(one, SOURCES))
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

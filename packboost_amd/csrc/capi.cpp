@@ -1,0 +1,450 @@
+// C-ABI host layer of libpackboost_hip.so: argument validation (mirroring the reference's
+// std::invalid_argument / std::out_of_range checks, frontier_cpu.cpp:125-135,176-178,263-265),
+// launch-shape selection for the kernels, the per-fit context, and error reporting.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "pb_internal.h"
+
+struct pb_ctx {
+    pb_dims d;
+    int64_t rows_padded;
+    int32_t max_era_rows;
+    int32_t umax;   // largest active-node count of any depth
+    int32_t wmax;   // wavefront winners per node for K features x all thresholds
+    int32_t device;
+    int32_t* era_off_dev;
+    pb::Frontier* st;
+    pb::SplitRule* rules;
+    pb::NodeTotal* ntot;
+    pb_candidate* cand_w;
+    int32_t* ids[2];
+    int32_t* thr_tab;
+    int32_t last_w;
+    int64_t lds_budget;
+    int32_t force_copies;
+    int32_t force_ftile;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+    g_err = std::string("HIP error: ") + hipGetErrorString(e) + " (" + where + ")";
+    return PB_ERR_HIP;
+}
+
+#define PB_HIP(call, where)                          \
+    do {                                             \
+        hipError_t e_ = (call);                      \
+        if (e_ != hipSuccess) return hip_fail(e_, where); \
+    } while (0)
+
+int64_t env_int(const char* name, int64_t dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    return std::strtoll(v, nullptr, 10);
+}
+
+int32_t max_nodes_at(const pb_ctx* c, int32_t depth) {
+    int64_t cap = int64_t(1) << std::min(depth, 30);
+    if (c->d.min_samples_leaf > 0) {
+        const int64_t by_rows = c->d.num_rows / (2 * (int64_t)c->d.min_samples_leaf);
+        cap = std::min(cap, std::max<int64_t>(1, by_rows));
+    }
+    cap = std::min<int64_t>(cap, 65534);
+    return (int32_t)cap;
+}
+
+int32_t thresholds_per_feature(const pb_ctx* c, const pb_split_params* p) {
+    const int full = std::max(1, c->d.max_bins - 1);
+    if (p->k_cuts > 0 && p->k_cuts < full) return std::max(1, std::min(p->k_cuts, full));
+    return full;
+}
+
+template <typename T>
+int dev_alloc(T** p, size_t n, const char* what) {
+    *p = nullptr;
+    if (n == 0) n = 1;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(p), n * sizeof(T));
+    if (e != hipSuccess) return hip_fail(e, what);
+    return PB_OK;
+}
+
+void free_ctx(pb_ctx* c) {
+    if (!c) return;
+    (void)hipFree(c->era_off_dev);
+    (void)hipFree(c->st);
+    (void)hipFree(c->rules);
+    (void)hipFree(c->ntot);
+    (void)hipFree(c->cand_w);
+    (void)hipFree(c->ids[0]);
+    (void)hipFree(c->ids[1]);
+    (void)hipFree(c->thr_tab);
+    delete c;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pb_last_error(void) { return g_err.c_str(); }
+
+int32_t pb_version(void) { return 100; }  // 0.1.0
+
+int32_t pb_device_available(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+    return std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+}
+
+int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out) {
+    if (!dims || !era_off_host || !out) return fail(PB_ERR_INVALID, "pb_ctx_create: null argument");
+    *out = nullptr;
+    const pb_dims& d = *dims;
+    if (d.num_rows < 1) return fail(PB_ERR_INVALID, "num_rows must be >= 1");
+    if (d.num_rows > (int64_t(1) << 30)) return fail(PB_ERR_UNSUPPORTED, "num_rows above 2^30");
+    if (d.ld < d.num_rows || d.ld % 16 != 0)
+        return fail(PB_ERR_INVALID, "ld must be >= num_rows and a multiple of 16");
+    if (d.num_features < 1) return fail(PB_ERR_INVALID, "num_features must be >= 1");
+    if (d.num_eras < 1) return fail(PB_ERR_INVALID, "num_eras must be >= 1");
+    if (d.max_bins < 2 || d.max_bins > 255) return fail(PB_ERR_INVALID, "max_bins must be in [2, 255]");
+    if (d.max_depth < 1 || d.max_depth > 15) return fail(PB_ERR_UNSUPPORTED, "max_depth must be in [1, 15]");
+    if (d.max_feats < 1 || d.max_feats > d.num_features)
+        return fail(PB_ERR_INVALID, "max_feats must be in [1, num_features]");
+    if (d.min_samples_leaf < 0) return fail(PB_ERR_INVALID, "min_samples_leaf must be >= 0");
+    if (era_off_host[0] != 0 || era_off_host[d.num_eras] != d.num_rows)
+        return fail(PB_ERR_INVALID, "era offsets must start at 0 and end at num_rows");
+    int32_t max_era = 0;
+    for (int e = 0; e < d.num_eras; ++e) {
+        const int32_t len = era_off_host[e + 1] - era_off_host[e];
+        if (len < 0) return fail(PB_ERR_INVALID, "era offsets must be non-decreasing");
+        max_era = std::max(max_era, len);
+    }
+
+    pb_ctx* c = new pb_ctx();
+    std::memset(c, 0, sizeof(*c));
+    c->d = d;
+    c->rows_padded = (d.num_rows + 15) / 16 * 16;
+    c->max_era_rows = max_era;
+    (void)hipGetDevice(&c->device);
+    c->umax = 1;
+    for (int dd = 0; dd < d.max_depth; ++dd) c->umax = std::max(c->umax, max_nodes_at(c, dd));
+    const int tmax = std::max(1, d.max_bins - 1);
+    c->wmax = (int32_t)(((int64_t)d.max_feats * tmax + pb::kWave - 1) / pb::kWave);
+    c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 64 * 1024);
+    c->force_copies = (int32_t)env_int("PB_HIST_COPIES", 0);
+    c->force_ftile = (int32_t)env_int("PB_HIST_FTILE", 0);
+
+    int rc = PB_OK;
+    if ((rc = dev_alloc(&c->era_off_dev, d.num_eras + 1, "alloc era offsets")) ||
+        (rc = dev_alloc(&c->st, 1, "alloc frontier")) ||
+        (rc = dev_alloc(&c->rules, c->umax, "alloc split rules")) ||
+        (rc = dev_alloc(&c->ntot, c->umax, "alloc node totals")) ||
+        (rc = dev_alloc(&c->cand_w, (size_t)c->umax * c->wmax, "alloc candidates")) ||
+        (rc = dev_alloc(&c->ids[0], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
+        (rc = dev_alloc(&c->ids[1], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
+        (rc = dev_alloc(&c->thr_tab, (size_t)d.max_feats * tmax, "alloc threshold table"))) {
+        free_ctx(c);
+        return rc;
+    }
+    hipError_t e = hipMemcpy(c->era_off_dev, era_off_host, sizeof(int32_t) * (d.num_eras + 1),
+                             hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        free_ctx(c);
+        return hip_fail(e, "copy era offsets");
+    }
+    e = hipMemset(c->st, 0, sizeof(pb::Frontier));
+    if (e != hipSuccess) {
+        free_ctx(c);
+        return hip_fail(e, "clear frontier");
+    }
+    *out = c;
+    return PB_OK;
+}
+
+int pb_ctx_destroy(pb_ctx* ctx) {
+    free_ctx(ctx);
+    return PB_OK;
+}
+
+int64_t pb_hist_plane_elems(const pb_ctx* c, int32_t max_nodes) {
+    if (!c) return -1;
+    return (int64_t)c->d.num_eras * max_nodes * c->d.max_feats * c->d.max_bins;
+}
+
+int32_t pb_max_nodes(const pb_ctx* c, int32_t depth) {
+    if (!c || depth < 0) return -1;
+    return max_nodes_at(c, depth);
+}
+
+const int32_t* pb_era_offsets_dev(const pb_ctx* c) { return c ? c->era_off_dev : nullptr; }
+
+int pb_round_begin(pb_ctx* c, const float* preds, const float* y, float* grad, uint16_t* nid,
+                   uint16_t* tnode, void* stream) {
+    if (!c || !preds || !y || !grad || !nid || !tnode)
+        return fail(PB_ERR_INVALID, "pb_round_begin: null argument");
+    const int64_t N = c->d.num_rows;
+    const int32_t root_active = (N >= 2 * (int64_t)c->d.min_samples_leaf) ? 1 : 0;
+    PB_HIP(pb::launch_round_begin(preds, y, grad, nid, tnode, N, c->rows_padded, root_active, c->st,
+                                  c->ids[0], (hipStream_t)stream),
+           "round_begin launch");
+    return PB_OK;
+}
+
+int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint16_t* nid,
+                  const int32_t* feats, int32_t K, int32_t depth, int32_t max_nodes,
+                  int32_t* hist_cnt, float* hist_grad, void* stream) {
+    if (!c || !bins || !grad || !nid || !feats || !hist_cnt || !hist_grad)
+        return fail(PB_ERR_INVALID, "pb_hist_build: null argument");
+    if (K < 1 || K > c->d.max_feats) return fail(PB_ERR_INVALID, "pb_hist_build: K out of range");
+    if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_hist_build: depth out of range");
+    if (max_nodes < max_nodes_at(c, depth))
+        return fail(PB_ERR_INVALID, "pb_hist_build: max_nodes below the frontier bound of this depth");
+    if ((reinterpret_cast<uintptr_t>(bins) & 15) || (reinterpret_cast<uintptr_t>(grad) & 15) ||
+        (reinterpret_cast<uintptr_t>(nid) & 7))
+        return fail(PB_ERR_INVALID, "pb_hist_build: bins/grad must be 16-byte and nid 8-byte aligned");
+    if (c->max_era_rows > pb::kMaxEraRowsDirect)
+        return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: eras above 65535 rows are not supported yet");
+
+    const int nb = c->d.max_bins;
+    const int64_t cells = (int64_t)max_nodes * nb;
+    const int64_t budget = std::max<int64_t>(c->lds_budget, 8 * 1024);
+    int clog2 = 4;  // 16 copies: conflict-free 64-bit atomics
+    if (c->force_copies > 0) {
+        clog2 = 0;
+        while ((1 << (clog2 + 1)) <= c->force_copies && clog2 < 4) ++clog2;
+    } else {
+        const int64_t want_feats = std::min<int64_t>(K, 8);
+        while (clog2 > 0 && cells * (int64_t(1) << clog2) * 8 * want_feats > budget) --clog2;
+    }
+    const int64_t per_feat = cells * (int64_t(1) << clog2) * 8;
+    int64_t ft = budget / per_feat;
+    if (c->force_ftile > 0) ft = c->force_ftile;
+    ft = std::min<int64_t>(ft, std::min<int64_t>(K, 16));
+    if (ft < 1)
+        return fail(PB_ERR_UNSUPPORTED,
+                    "pb_hist_build: one feature's node x bin histogram exceeds the LDS budget");
+    int ftile = 1;
+    while (ftile * 2 <= ft) ftile *= 2;
+    const size_t lds_bytes = (size_t)(ftile * per_feat);
+    if (lds_bytes > 160 * 1024) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: LDS above 160 KiB");
+
+    pb::HistArgs a;
+    a.bins = bins;
+    a.ld = c->d.ld;
+    a.grad = grad;
+    a.nid = nid;
+    a.era_off = c->era_off_dev;
+    a.E = c->d.num_eras;
+    a.feats = feats;
+    a.K = K;
+    a.ntiles = (K + ftile - 1) / ftile;
+    a.ftile = ftile;
+    a.U = max_nodes;
+    a.nb = nb;
+    a.clog2 = clog2;
+    a.st = c->st;
+    a.depth = depth;
+    a.out_cnt = hist_cnt;
+    a.out_g = hist_grad;
+    const int eras8 = (a.E + 7) / 8 * 8;
+    const int64_t grid = (int64_t)eras8 * a.ntiles;
+    if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: grid too large");
+    PB_HIP(pb::launch_hist(a, (int)grid, lds_bytes, (hipStream_t)stream), "hist launch");
+    return PB_OK;
+}
+
+int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, const int32_t* feats,
+                 int32_t K, int32_t depth, int32_t max_nodes, const pb_split_params* p,
+                 pb_candidate* cand_all, void* stream) {
+    if (!c || !hist_cnt || !hist_grad || !feats || !p)
+        return fail(PB_ERR_INVALID, "pb_des_score: null argument");
+    if (K < 1 || K > c->d.max_feats) return fail(PB_ERR_INVALID, "pb_des_score: K out of range");
+    if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_des_score: depth out of range");
+    if (max_nodes < max_nodes_at(c, depth))
+        return fail(PB_ERR_INVALID, "pb_des_score: max_nodes below the frontier bound of this depth");
+    const int nb = c->d.max_bins;
+    const int T = thresholds_per_feature(c, p);
+    const int full = std::max(1, nb - 1);
+    const int32_t* thr_tab = nullptr;
+    if (p->k_cuts > 0 && p->k_cuts < full) {
+        PB_HIP(pb::launch_kcuts(hist_cnt, c->d.num_eras, max_nodes, K, nb, p->k_cuts,
+                                p->cut_selection == 1 ? 1 : 0, c->st, depth, c->thr_tab,
+                                (hipStream_t)stream),
+               "kcuts launch");
+        thr_tab = c->thr_tab;
+    }
+    const int64_t KT = (int64_t)K * T;
+    const int64_t KTpad = (KT + pb::kWave - 1) / pb::kWave * pb::kWave;
+    const int64_t lanes = KTpad * max_nodes_at(c, depth);
+    const int64_t grid = (lanes + pb::kBlock - 1) / pb::kBlock;
+    if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_des_score: grid too large");
+    pb::ScoreArgs a;
+    a.cnt = hist_cnt;
+    a.g = hist_grad;
+    a.E = c->d.num_eras;
+    a.U = max_nodes;
+    a.K = K;
+    a.nb = nb;
+    a.T = T;
+    a.feats = feats;
+    a.thr_tab = thr_tab;
+    a.lambda_l2 = (float)p->lambda_l2;
+    a.lambda_dro = (float)p->lambda_dro;
+    a.dir_w = (float)p->direction_weight;
+    a.era_alpha = (float)p->era_alpha;
+    a.msl = p->min_samples_leaf;
+    a.st = c->st;
+    a.depth = depth;
+    a.cand_w = c->cand_w;
+    a.cand_all = cand_all;
+    a.ntot = c->ntot;
+    c->last_w = (int32_t)(KTpad / pb::kWave);
+    PB_HIP(pb::launch_score(a, (int)grid, (hipStream_t)stream), "score launch");
+    return PB_OK;
+}
+
+int pb_decide(pb_ctx* c, int32_t depth, int32_t max_nodes, const pb_split_params* p,
+              pb_decision* dec, float* values, void* stream) {
+    if (!c || !p || !dec || !values) return fail(PB_ERR_INVALID, "pb_decide: null argument");
+    if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_decide: depth out of range");
+    if (c->last_w <= 0) return fail(PB_ERR_INVALID, "pb_decide: call pb_des_score first");
+    (void)max_nodes;
+    PB_HIP(pb::launch_decide(c->cand_w, c->last_w, c->ntot, c->st, depth, p->min_samples_leaf,
+                             p->lambda_l2, c->ids[depth & 1], c->ids[(depth + 1) & 1], c->rules,
+                             dec, values, (hipStream_t)stream),
+           "decide launch");
+    return PB_OK;
+}
+
+int pb_partition(pb_ctx* c, const uint8_t* bins, int32_t depth, uint16_t* nid, uint16_t* tnode,
+                 void* stream) {
+    if (!c || !bins || !nid || !tnode) return fail(PB_ERR_INVALID, "pb_partition: null argument");
+    if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_partition: depth out of range");
+    if ((reinterpret_cast<uintptr_t>(nid) & 3) || (reinterpret_cast<uintptr_t>(tnode) & 3))
+        return fail(PB_ERR_INVALID, "pb_partition: nid/tnode must be 4-byte aligned");
+    PB_HIP(pb::launch_partition(bins, c->d.ld, c->rows_padded, c->rules, c->st, depth, nid, tnode,
+                                (hipStream_t)stream),
+           "partition launch");
+    return PB_OK;
+}
+
+int pb_round_end(pb_ctx* c, const uint16_t* tnode, const float* values, int32_t pack_size,
+                 float lr, float* preds, void* stream) {
+    if (!c || !tnode || !values || !preds) return fail(PB_ERR_INVALID, "pb_round_end: null argument");
+    if (pack_size < 1) return fail(PB_ERR_INVALID, "pb_round_end: pack_size must be >= 1");
+    PB_HIP(pb::launch_round_end(tnode, values, pack_size, lr, preds, c->d.num_rows,
+                                (hipStream_t)stream),
+           "round_end launch");
+    return PB_OK;
+}
+
+int pb_frontier_set(pb_ctx* c, int32_t depth, int32_t num_active, const int32_t* node_ids_host,
+                    int32_t tree_size, void* stream) {
+    if (!c) return fail(PB_ERR_INVALID, "pb_frontier_set: null context");
+    if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_frontier_set: depth out of range");
+    if (num_active < 0 || num_active > max_nodes_at(c, depth))
+        return fail(PB_ERR_RANGE, "pb_frontier_set: num_active above the frontier bound of this depth");
+    if (tree_size < 1 || tree_size > (1 << (c->d.max_depth + 1)))
+        return fail(PB_ERR_RANGE, "pb_frontier_set: tree_size out of range");
+    std::vector<int32_t> ids(std::max(num_active, 1));
+    for (int i = 0; i < num_active; ++i) {
+        ids[i] = node_ids_host ? node_ids_host[i] : i;
+        if (ids[i] < 0 || ids[i] >= tree_size) return fail(PB_ERR_RANGE, "pb_frontier_set: node id out of range");
+    }
+    hipStream_t s = (hipStream_t)stream;
+    PB_HIP(hipStreamSynchronize(s), "frontier_set sync");
+    pb::Frontier f;
+    PB_HIP(hipMemcpy(&f, c->st, sizeof(f), hipMemcpyDeviceToHost), "frontier_set read");
+    f.u_active[depth] = num_active;
+    for (int dd = depth + 1; dd <= PB_MAX_DEPTH; ++dd) f.u_active[dd] = 0;
+    f.tree_size = tree_size;
+    PB_HIP(hipMemcpy(c->st, &f, sizeof(f), hipMemcpyHostToDevice), "frontier_set write");
+    if (num_active > 0)
+        PB_HIP(hipMemcpy(c->ids[depth & 1], ids.data(), sizeof(int32_t) * num_active,
+                         hipMemcpyHostToDevice),
+               "frontier_set ids");
+    return PB_OK;
+}
+
+int pb_frontier_counts(pb_ctx* c, int32_t* u_active_host, int32_t* tree_size_host, void* stream) {
+    if (!c || !u_active_host || !tree_size_host)
+        return fail(PB_ERR_INVALID, "pb_frontier_counts: null argument");
+    pb::Frontier f;
+    PB_HIP(hipMemcpyAsync(&f, c->st, sizeof(f), hipMemcpyDeviceToHost, (hipStream_t)stream),
+           "frontier copy");
+    PB_HIP(hipStreamSynchronize((hipStream_t)stream), "frontier sync");
+    std::memcpy(u_active_host, f.u_active, sizeof(f.u_active));
+    *tree_size_host = f.tree_size;
+    return PB_OK;
+}
+
+int pb_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const int32_t* feature,
+                    const int32_t* threshold, const int32_t* left_abs, const int32_t* right_abs,
+                    const float* value, const uint8_t* is_leaf, const int32_t* offsets, int32_t B,
+                    int32_t total_nodes, float tree_weight, float* out, int32_t* leaf,
+                    void* stream) {
+    if (N < 0 || ld < N || F < 1 || B < 0 || total_nodes < 0)
+        return fail(PB_ERR_INVALID, "pb_predict_pack: bad shape");
+    if (N == 0) return PB_OK;
+    if (!bins || !feature || !threshold || !left_abs || !right_abs || !value || !is_leaf ||
+        !offsets || !out)
+        return fail(PB_ERR_INVALID, "pb_predict_pack: null argument");
+    PB_HIP(pb::launch_predict_pack(bins, N, ld, F, feature, threshold, left_abs, right_abs, value,
+                                   is_leaf, offsets, B, total_nodes, tree_weight, 0, out, leaf,
+                                   (hipStream_t)stream),
+           "predict_pack launch");
+    return PB_OK;
+}
+
+int pb_predict_forest(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                      const int32_t* feature, const int32_t* threshold, const int32_t* left_abs,
+                      const int32_t* right_abs, const float* value, const uint8_t* is_leaf,
+                      const int32_t* offsets, int32_t T, int32_t total_nodes, float tree_weight,
+                      float* out, void* stream) {
+    if (N < 0 || ld < N || F < 1 || T < 0 || total_nodes < 0)
+        return fail(PB_ERR_INVALID, "pb_predict_forest: bad shape");
+    if (N == 0) return PB_OK;
+    if (!bins || !feature || !threshold || !left_abs || !right_abs || !value || !is_leaf ||
+        !offsets || !out)
+        return fail(PB_ERR_INVALID, "pb_predict_forest: null argument");
+    PB_HIP(pb::launch_predict_pack(bins, N, ld, F, feature, threshold, left_abs, right_abs, value,
+                                   is_leaf, offsets, T, total_nodes, tree_weight, 1, out, nullptr,
+                                   (hipStream_t)stream),
+           "predict_forest launch");
+    return PB_OK;
+}
+
+int pb_predict_bins(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const int32_t* feature,
+                    const int32_t* threshold, const int32_t* left, const int32_t* right,
+                    const float* value, const uint8_t* is_leaf, int32_t num_nodes, float* out,
+                    void* stream) {
+    if (N < 0 || ld < N || F < 1 || num_nodes < 0)
+        return fail(PB_ERR_INVALID, "pb_predict_bins: bad shape");
+    if (N == 0) return PB_OK;
+    if (!bins || !feature || !threshold || !left || !right || !value || !is_leaf || !out)
+        return fail(PB_ERR_INVALID, "pb_predict_bins: null argument");
+    PB_HIP(pb::launch_predict_bins(bins, N, ld, F, feature, threshold, left, right, value, is_leaf,
+                                   num_nodes, out, (hipStream_t)stream),
+           "predict_bins launch");
+    return PB_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,154 @@
+// Kernel 3 — row-to-node partition, plus the round's gradient and pack-aggregation passes.
+//
+// The reference keeps per-node, per-era row lists and splits them stably into left/right
+// lists (frontier_cpu.cpp:446-497; partition_frontier_cuda, frontier_cuda.cu:719-851).
+// Here every row carries two uint16 ids instead: `nid`, its slot in the active frontier of
+// the current depth (PB_INACTIVE once its node stopped growing), and `tnode`, the
+// TreeBuilder id of the node it sits in. Row order never changes, so the per-era order the
+// reference's lists preserve is implicit, and the partition is one coalesced pass:
+//   child = left_id + (bin[feature][row] > threshold)  (left iff bin <= threshold)
+// All B trees of a pack share one frontier (they are identical, booster.py:503-519 +
+// shard dedup at booster.py:1048-1062), so one id pair per row covers the whole pack.
+#include "pb_internal.h"
+
+namespace pb {
+namespace {
+
+constexpr int kMaxRulesLds = 2048;
+
+__global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __restrict__ bins,
+                                                       int64_t ld, int64_t rows_padded,
+                                                       const SplitRule* __restrict__ rules,
+                                                       const Frontier* st, int32_t depth,
+                                                       uint16_t* __restrict__ nid,
+                                                       uint16_t* __restrict__ tnode) {
+    __shared__ SplitRule s_rules[kMaxRulesLds];
+    const int Ua = st->u_active[depth];
+    if (Ua <= 0) return;
+    const bool in_lds = Ua <= kMaxRulesLds;
+    if (in_lds) {
+        for (int u = threadIdx.x; u < Ua; u += kBlock) s_rules[u] = rules[u];
+        __syncthreads();
+    }
+    const int64_t stride = (int64_t)gridDim.x * kBlock * 2;
+    for (int64_t r = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 2; r < rows_padded; r += stride) {
+        const uint32_t nn = *reinterpret_cast<const uint32_t*>(nid + r);
+        const uint32_t tt = *reinterpret_cast<const uint32_t*>(tnode + r);
+        uint32_t n2[2] = {nn & 0xffffu, nn >> 16};
+        uint32_t t2[2] = {tt & 0xffffu, tt >> 16};
+        bool changed = false;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t u = n2[j];
+            if (u >= (uint32_t)Ua) continue;  // PB_INACTIVE or stale
+            const SplitRule rr = in_lds ? s_rules[u] : rules[u];
+            changed = true;
+            if (rr.feature < 0) {
+                n2[j] = PB_INACTIVE;
+                continue;
+            }
+            const uint32_t bin = bins[(int64_t)rr.feature * ld + r + j];
+            const uint32_t side = bin > (uint32_t)rr.threshold ? 1u : 0u;
+            t2[j] = (uint32_t)rr.left_id + side;
+            n2[j] = rr.next_slot[side];
+        }
+        if (changed) {
+            *reinterpret_cast<uint32_t*>(nid + r) = n2[0] | (n2[1] << 16);
+            *reinterpret_cast<uint32_t*>(tnode + r) = t2[0] | (t2[1] << 16);
+        }
+    }
+}
+
+__global__ void reset_kernel(Frontier* st, int32_t root_active, int32_t* cur_ids) {
+    if (threadIdx.x == 0) {
+        for (int d = 0; d <= PB_MAX_DEPTH; ++d) st->u_active[d] = 0;
+        st->u_active[0] = root_active;
+        st->tree_size = 1;
+        st->gmax_bits = 0u;
+        cur_ids[0] = 0;
+    }
+}
+
+// grad = preds - y (booster.py:2149-2151); hess == 1 is implicit (counts). Every row starts in
+// the root; the pad rows [N, rows_padded) are parked with grad 0 and PB_INACTIVE.
+__global__ __launch_bounds__(kBlock) void round_begin_kernel(const float* __restrict__ preds,
+                                                         const float* __restrict__ y,
+                                                         float* __restrict__ grad,
+                                                         uint16_t* __restrict__ nid,
+                                                         uint16_t* __restrict__ tnode, int64_t N,
+                                                         int64_t rows_padded, int32_t root_active,
+                                                         Frontier* st) {
+    float amax = 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x; r < rows_padded; r += stride) {
+        float g = 0.0f;
+        if (r < N) {
+            g = preds[r] - y[r];
+            amax = fmaxf(amax, fabsf(g));
+        }
+        grad[r] = g;
+        nid[r] = (r < N && root_active) ? (uint16_t)0 : (uint16_t)PB_INACTIVE;
+        tnode[r] = 0;
+    }
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+    if ((threadIdx.x & (kWave - 1)) == 0 && amax > 0.0f)
+        atomicMax(&st->gmax_bits, __float_as_uint(amax));  // non-negative floats order as uints
+}
+
+// pack_sum[r] = sum_{t<B} value[leaf(r)] in float32, tree order (booster.py:586-598, the
+// B trees are identical); preds += float32(lr) * pack_sum as two rounded float32 ops
+// (torch: tmp = lr * pack_sum; preds += tmp).
+__global__ __launch_bounds__(kBlock) void round_end_kernel(const uint16_t* __restrict__ tnode,
+                                                       const float* __restrict__ values,
+                                                       int32_t B, float lr,
+                                                       float* __restrict__ preds, int64_t N) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x; r < N; r += stride) {
+        const float v = values[tnode[r]];
+        float s = 0.0f;
+        for (int t = 0; t < B; ++t) s = s + v;
+        const float tmp = lr * s;
+        preds[r] = preds[r] + tmp;
+    }
+}
+
+int grid_for(int64_t work, int per_block, int cap) {
+    int64_t g = (work + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (int)g;
+}
+
+}  // namespace
+
+hipError_t launch_partition(const uint8_t* bins, int64_t ld, int64_t rows_padded,
+                            const SplitRule* rules, const Frontier* st, int32_t depth,
+                            uint16_t* nid, uint16_t* tnode, hipStream_t s) {
+    const int grid = grid_for(rows_padded / 2, kBlock, 8192);
+    hipLaunchKernelGGL(partition_kernel, dim3(grid), dim3(kBlock), 0, s, bins, ld, rows_padded,
+                       rules, st, depth, nid, tnode);
+    return hipGetLastError();
+}
+
+hipError_t launch_round_begin(const float* preds, const float* y, float* grad, uint16_t* nid,
+                              uint16_t* tnode, int64_t N, int64_t rows_padded, int32_t root_active,
+                              Frontier* st, int32_t* cur_ids, hipStream_t s) {
+    hipLaunchKernelGGL(reset_kernel, dim3(1), dim3(64), 0, s, st, root_active, cur_ids);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int grid = grid_for(rows_padded, kBlock, 8192);
+    hipLaunchKernelGGL(round_begin_kernel, dim3(grid), dim3(kBlock), 0, s, preds, y, grad, nid,
+                       tnode, N, rows_padded, root_active, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
+                            float lr, float* preds, int64_t N, hipStream_t s) {
+    const int grid = grid_for(N, kBlock, 8192);
+    hipLaunchKernelGGL(round_end_kernel, dim3(grid), dim3(kBlock), 0, s, tnode, values, pack_size,
+                       lr, preds, N);
+    return hipGetLastError();
+}
+
+}  // namespace pb

@@ -1,0 +1,112 @@
+// Internal declarations shared by the HIP kernels and the C-ABI host layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/packboost_hip.h"
+
+namespace pb {
+
+constexpr int kWave = 64;          // CDNA wavefront width
+constexpr int kBlock = 256;        // threads per workgroup for the row kernels
+constexpr int kCountBits = 16;     // low bits of a histogram word hold the row count
+constexpr int kMaxEraRowsDirect = (1 << kCountBits) - 1;
+constexpr int kGradScaleLog2 = 30; // |grad| * scale < 2^30 -> fixed point fits int32 per row
+
+// Frontier state of the round in flight; lives in device memory and is only written
+// by kernels, so a whole round is enqueued without host round trips.
+struct Frontier {
+    int32_t u_active[PB_MAX_DEPTH + 1];  // active nodes per depth
+    int32_t tree_size;                   // next TreeBuilder id
+    uint32_t gmax_bits;                  // float bits of max |grad| this round
+    int32_t reserved[6];
+};
+
+// Per active node of the current depth, read by the partition kernel.
+struct SplitRule {
+    int32_t feature;    // -1: node did not split
+    int32_t threshold;
+    int32_t left_id;    // TreeBuilder id of the left child (right = left + 1)
+    uint16_t next_slot[2];  // slot in the next frontier (PB_INACTIVE if not active)
+};
+
+struct NodeTotal {
+    int32_t count;
+    float grad;
+};
+
+struct HistArgs {
+    const uint8_t* bins;
+    int64_t ld;
+    const float* grad;
+    const uint16_t* nid;
+    const int32_t* era_off;
+    int32_t E;
+    const int32_t* feats;
+    int32_t K;
+    int32_t ntiles;
+    int32_t ftile;
+    int32_t U;      // node stride of the output planes (max nodes)
+    int32_t nb;
+    int32_t clog2;  // log2 of LDS histogram copies
+    const Frontier* st;
+    int32_t depth;
+    int32_t* out_cnt;
+    float* out_g;
+};
+
+struct ScoreArgs {
+    const int32_t* cnt;
+    const float* g;
+    int32_t E;
+    int32_t U;
+    int32_t K;
+    int32_t nb;
+    int32_t T;             // thresholds per feature
+    const int32_t* feats;
+    const int32_t* thr_tab;  // [K][T] or null for the full sweep 0..nb-2
+    float lambda_l2;
+    float lambda_dro;
+    float dir_w;
+    float era_alpha;
+    int32_t msl;
+    const Frontier* st;
+    int32_t depth;
+    pb_candidate* cand_w;    // [U][W] wavefront winners
+    pb_candidate* cand_all;  // optional [U][K][T]
+    NodeTotal* ntot;         // [U]
+};
+
+// Launchers (defined in the .hip files; all return hipError_t of the launch).
+hipError_t launch_hist(const HistArgs& a, int grid, size_t lds_bytes, hipStream_t s);
+hipError_t launch_score(const ScoreArgs& a, int grid, hipStream_t s);
+hipError_t launch_kcuts(const int32_t* cnt, int32_t E, int32_t U, int32_t K, int32_t nb,
+                        int32_t k, int32_t mass, const Frontier* st, int32_t depth,
+                        int32_t* thr_tab, hipStream_t s);
+hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal* ntot,
+                         Frontier* st, int32_t depth, int32_t msl, double lambda_l2,
+                         const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
+                         pb_decision* dec, float* values, hipStream_t s);
+hipError_t launch_partition(const uint8_t* bins, int64_t ld, int64_t rows_padded,
+                            const SplitRule* rules, const Frontier* st, int32_t depth,
+                            uint16_t* nid, uint16_t* tnode, hipStream_t s);
+hipError_t launch_round_begin(const float* preds, const float* y, float* grad, uint16_t* nid,
+                              uint16_t* tnode, int64_t N, int64_t rows_padded, int32_t root_active,
+                              Frontier* st, int32_t* cur_ids, hipStream_t s);
+hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
+                            float lr, float* preds, int64_t N, hipStream_t s);
+hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                               const int32_t* feature, const int32_t* threshold,
+                               const int32_t* left_abs, const int32_t* right_abs,
+                               const float* value, const uint8_t* is_leaf,
+                               const int32_t* offsets, int32_t B, int32_t total_nodes,
+                               float tree_weight, int32_t sequential, float* out, int32_t* leaf,
+                               hipStream_t s);
+hipError_t launch_predict_bins(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                               const int32_t* feature, const int32_t* threshold,
+                               const int32_t* left, const int32_t* right, const float* value,
+                               const uint8_t* is_leaf, int32_t num_nodes, float* out,
+                               hipStream_t s);
+
+}  // namespace pb

@@ -1,0 +1,333 @@
+"""Device-resident training rounds on the HIP backend.
+
+`DeviceFit` owns the per-fit device state (column-major uint8 bins, targets, predictions,
+per-row frontier ids, histogram planes, decision log) and runs one boosting round as a
+sequence of asynchronous kernel launches on the caller's stream:
+
+    round_begin                         grad = preds - y, every row in the root
+    for depth in 0..D-1:
+        hist_build -> des_score -> decide -> partition
+    round_end                           preds += lr * pack_sum
+
+The only host round trip per round is the final copy of the decision log (a few KB), from
+which the host rebuilds the round's trees. Feature subsets are drawn on the host from the
+fit's CPU generator before the round; the generator is rewound afterwards to the state the
+reference would have after its actual number of draws (it draws only while a depth still
+has active nodes, booster.py:516-519).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .backends import _hip
+from .config import PackBoostConfig
+
+
+def padded_rows(n: int) -> int:
+    return (n + 15) // 16 * 16
+
+
+def split_params(cfg: PackBoostConfig) -> _hip.PbSplitParams:
+    p = _hip.PbSplitParams()
+    p.lambda_l2 = float(cfg.lambda_l2)
+    p.lambda_dro = float(cfg.lambda_dro)
+    p.direction_weight = float(cfg.direction_weight)
+    p.era_alpha = max(0.0, float(cfg.era_alpha))
+    p.min_samples_leaf = int(cfg.min_samples_leaf)
+    p.k_cuts = int(cfg.k_cuts)
+    p.cut_selection = 1 if str(cfg.cut_selection) == "mass" else 0
+    p.reserved = 0
+    return p
+
+
+def subset_size(cfg: PackBoostConfig, num_features: int) -> int:
+    """k = max(1, round(frac * F)), capped at F (booster.py:787-792)."""
+    k = max(1, int(round(float(cfg.layer_feature_fraction) * num_features)))
+    return min(k, num_features)
+
+
+@dataclass
+class RoundLog:
+    """Decisions of one round, as the host reads them back."""
+
+    u_active: np.ndarray      # int32 [D+1] active unique nodes per depth
+    tree_size: int            # nodes of each tree of the round
+    decisions: np.ndarray     # DECISION_DTYPE [2^D - 1], depth d at offset 2^d - 1
+    root_grad: float          # float32 sum of grad over all rows (root value numerator)
+    depths_drawn: int         # feature subsets the reference would have drawn
+
+
+class DeviceFit:
+    """One fit's device state and round driver (all B trees of a pack share one frontier)."""
+
+    def __init__(self, bins_fm: torch.Tensor, num_rows: int, y: torch.Tensor,
+                 era_offsets: np.ndarray, cfg: PackBoostConfig, *,
+                 stream: torch.cuda.Stream | None = None) -> None:
+        lib = _hip.load()
+        if bins_fm.dtype != torch.uint8 or bins_fm.dim() != 2 or not bins_fm.is_cuda:
+            raise ValueError("bins_fm must be a CUDA uint8 tensor [F, ld]")
+        if not bins_fm.is_contiguous():
+            raise ValueError("bins_fm must be contiguous")
+        F, ld = bins_fm.shape
+        N = int(num_rows)
+        if ld < N or ld % 16 != 0 or bins_fm.data_ptr() % 16 != 0:
+            raise ValueError("bins_fm row stride must be >= N and a multiple of 16")
+        self.lib = lib
+        self.cfg = cfg
+        self.device = bins_fm.device
+        self.stream = stream if stream is not None else torch.cuda.current_stream(self.device)
+        self.N, self.F, self.ld = N, int(F), int(ld)
+        self.E = int(len(era_offsets) - 1)
+        self.D = int(cfg.max_depth)
+        self.K = subset_size(cfg, self.F)
+        self.nb = int(cfg.max_bins)
+        self.B = int(cfg.pack_size)
+        self.lr = float(cfg.learning_rate)
+        self.params = split_params(cfg)
+        self.bins = bins_fm
+        self.rows_padded = padded_rows(N)
+        dev = self.device
+
+        dims = _hip.PbDims(num_rows=N, ld=self.ld, num_features=self.F, num_eras=self.E,
+                           max_bins=self.nb, max_depth=self.D, max_feats=self.K,
+                           min_samples_leaf=int(cfg.min_samples_leaf))
+        offs = np.ascontiguousarray(era_offsets, dtype=np.int32)
+        self._offs = offs
+        ctx = ctypes.c_void_p()
+        _hip.check(lib.pb_ctx_create(ctypes.byref(dims), offs.ctypes.data, ctypes.byref(ctx)),
+                   "pb_ctx_create")
+        self.ctx = ctx
+
+        def rows(dtype):
+            return torch.zeros(self.rows_padded, dtype=dtype, device=dev)
+
+        self.y = rows(torch.float32)
+        self.y[:N].copy_(y.to(device=dev, dtype=torch.float32).reshape(-1))
+        self.preds = rows(torch.float32)
+        self.grad = rows(torch.float32)
+        self.nid = rows(torch.int16)    # uint16 ids carried in int16 storage
+        self.tnode = rows(torch.int16)
+        self.max_nodes = [int(lib.pb_max_nodes(ctx, d)) for d in range(self.D)]
+        plane = max(int(lib.pb_hist_plane_elems(ctx, m)) for m in self.max_nodes)
+        self.hist_cnt = torch.empty(plane, dtype=torch.int32, device=dev)
+        self.hist_g = torch.empty(plane, dtype=torch.float32, device=dev)
+        self.values = torch.zeros(1 << (self.D + 1), dtype=torch.float32, device=dev)
+        n_dec = (1 << self.D) - 1
+        self.dec_dev = torch.zeros(n_dec * _hip.DECISION_DTYPE.itemsize, dtype=torch.uint8, device=dev)
+        self.dec_host = torch.empty_like(self.dec_dev, device="cpu").pin_memory()
+        self.feats_dev = torch.zeros((self.D, self.K), dtype=torch.int32, device=dev)
+        self.feats_host = torch.zeros((self.D, self.K), dtype=torch.int32).pin_memory()
+        self.root_grad_dev = torch.zeros(1, dtype=torch.float32, device=dev)
+
+    # ------------------------------------------------------------------ lifecycle
+    def close(self) -> None:
+        if getattr(self, "ctx", None) is not None and self.ctx.value:
+            torch.cuda.synchronize(self.device)
+            self.lib.pb_ctx_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self) -> None:  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------ rounds
+    def draw_subsets(self, rng: torch.Generator) -> tuple[np.ndarray, list]:
+        """Draws the subsets of every depth, keeping the generator state before each draw."""
+        states = []
+        subs = np.empty((self.D, self.K), dtype=np.int32)
+        for d in range(self.D):
+            states.append(rng.get_state())
+            subs[d] = torch.randperm(self.F, generator=rng)[: self.K].numpy().astype(np.int32)
+        states.append(rng.get_state())
+        return subs, states
+
+    def enqueue_round(self, subsets: np.ndarray, events: list | None = None) -> None:
+        """Enqueues one full round on the stream (no host synchronisation).
+
+        events: optional list that receives (phase, depth, start, end) timing events
+        recorded on the fit's stream around every kernel phase.
+        """
+        lib, ctx, s = self.lib, self.ctx, _hip.stream_ptr(self.stream)
+        chk = _hip.check
+        self.feats_host.numpy()[...] = subsets
+        with torch.cuda.stream(self.stream):
+            self.feats_dev.copy_(self.feats_host, non_blocking=True)
+        chk(lib.pb_round_begin(ctx, self.preds.data_ptr(), self.y.data_ptr(), self.grad.data_ptr(),
+                               self.nid.data_ptr(), self.tnode.data_ptr(), s), "pb_round_begin")
+        p = ctypes.byref(self.params)
+        def mark():
+            if events is None:
+                return None
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record(self.stream)
+            return ev
+
+        for d in range(self.D):
+            fptr = self.feats_dev[d].data_ptr()
+            m = self.max_nodes[d]
+            t0 = mark()
+            chk(lib.pb_hist_build(ctx, self.bins.data_ptr(), self.grad.data_ptr(),
+                                  self.nid.data_ptr(), fptr, self.K, d, m,
+                                  self.hist_cnt.data_ptr(), self.hist_g.data_ptr(), s),
+                "pb_hist_build")
+            t1 = mark()
+            chk(lib.pb_des_score(ctx, self.hist_cnt.data_ptr(), self.hist_g.data_ptr(), fptr,
+                                 self.K, d, m, p, None, s), "pb_des_score")
+            t2 = mark()
+            chk(lib.pb_decide(ctx, d, m, p, self.dec_dev.data_ptr(), self.values.data_ptr(), s),
+                "pb_decide")
+            t3 = mark()
+            chk(lib.pb_partition(ctx, self.bins.data_ptr(), d, self.nid.data_ptr(),
+                                 self.tnode.data_ptr(), s), "pb_partition")
+            t4 = mark()
+            if events is not None:
+                events += [("hist", d, t0, t1), ("score", d, t1, t2), ("decide", d, t2, t3),
+                           ("partition", d, t3, t4)]
+        self._root_value_if_inactive()
+        chk(lib.pb_round_end(ctx, self.tnode.data_ptr(), self.values.data_ptr(), self.B,
+                             ctypes.c_float(self.lr), self.preds.data_ptr(), s), "pb_round_end")
+
+    def _root_value_if_inactive(self) -> None:
+        # Root below capacity (N < 2*msl): the tree is a single leaf -G/(N+lambda)
+        # (booster.py:503-513). The decision kernels never run for it.
+        if self.N >= 2 * int(self.cfg.min_samples_leaf):
+            return
+        with torch.cuda.stream(self.stream):
+            g = self.grad[: self.N].sum()
+            self.root_grad_dev.copy_(g.reshape(1))
+            h = float(self.N)
+            self.values[0:1].copy_((-g.double() / (h + float(self.cfg.lambda_l2))).float().reshape(1))
+
+    def read_round(self, depths_states: list | None = None) -> RoundLog:
+        """Synchronises the stream and returns the round's decision log."""
+        with torch.cuda.stream(self.stream):
+            self.dec_host.copy_(self.dec_dev, non_blocking=True)
+        u = np.zeros(_hip.PB_MAX_DEPTH + 1, dtype=np.int32)
+        ts = ctypes.c_int32(0)
+        _hip.check(self.lib.pb_frontier_counts(self.ctx, u.ctypes.data, ctypes.byref(ts),
+                                               _hip.stream_ptr(self.stream)), "pb_frontier_counts")
+        dec = np.frombuffer(self.dec_host.numpy().tobytes(), dtype=_hip.DECISION_DTYPE).copy()
+        drawn = int(np.count_nonzero(u[: self.D] > 0))
+        if u[0] > 0:
+            root_grad = float(dec[0]["node_grad"])
+        else:
+            root_grad = float(self.root_grad_dev.cpu()[0])
+        return RoundLog(u_active=u[: self.D + 1].copy(), tree_size=int(ts.value), decisions=dec,
+                        root_grad=root_grad, depths_drawn=drawn)
+
+    def run_round(self, rng: torch.Generator, events: list | None = None) -> RoundLog:
+        subs, states = self.draw_subsets(rng)
+        self.enqueue_round(subs, events)
+        log = self.read_round()
+        if log.depths_drawn < self.D:
+            rng.set_state(states[log.depths_drawn])
+        return log
+
+
+def tree_arrays_from_log(log: RoundLog, cfg: PackBoostConfig, num_rows: int) -> dict[str, np.ndarray]:
+    """Rebuilds one tree of the round (TreeBuilder semantics, booster.py:172-190, 499-563).
+
+    Values are Python-double results of -G/(H + lambda) on the float32 sums, as the reference
+    stores them in TreeNode.value.
+    """
+    lam = float(cfg.lambda_l2)
+    n = max(1, int(log.tree_size))
+    feature = np.full(n, -1, dtype=np.int64)
+    threshold = np.zeros(n, dtype=np.int64)
+    left = np.full(n, -1, dtype=np.int64)
+    right = np.full(n, -1, dtype=np.int64)
+    value = np.zeros(n, dtype=np.float64)
+    is_leaf = np.ones(n, dtype=bool)
+    # root leaf value at round start: -sum(g) / (sum(h) + lambda), h == 1 per row
+    if num_rows > 0:
+        value[0] = -float(np.float32(log.root_grad)) / (float(np.float32(num_rows)) + lam)
+    D = int(cfg.max_depth)
+    for d in range(D):
+        ua = int(log.u_active[d])
+        if ua <= 0:
+            break
+        recs = log.decisions[(1 << d) - 1: (1 << d) - 1 + ua]
+        for r in recs:
+            nid = int(r["node_id"])
+            if int(r["split"]):
+                feature[nid] = int(r["feature"])
+                threshold[nid] = int(r["threshold"])
+                is_leaf[nid] = False
+                li, ri = int(r["left_id"]), int(r["right_id"])
+                left[nid], right[nid] = li, ri
+                value[li] = -float(r["left_grad"]) / (float(r["left_hess"]) + lam)
+                value[ri] = -float(r["right_grad"]) / (float(r["right_hess"]) + lam)
+            else:
+                cnt = int(r["node_count"])
+                value[nid] = 0.0 if cnt == 0 else -float(r["node_grad"]) / (float(np.float32(cnt)) + lam)
+                feature[nid], threshold[nid], left[nid], right[nid] = -1, 0, -1, -1
+                is_leaf[nid] = True
+    return {"feature": feature, "threshold": threshold, "left": left, "right": right,
+            "value": value, "is_leaf": is_leaf}
+
+
+def depth_log_from_round(log: RoundLog, d: int, cfg: PackBoostConfig, k: int,
+                         histogram_mode: str) -> dict:
+    """Per-depth instrumentation in the reference's key set (booster.py:220-270, 565-579)."""
+    ua = int(log.u_active[d])
+    recs = log.decisions[(1 << d) - 1: (1 << d) - 1 + ua]
+    rows = int(recs["node_count"].astype(np.int64).sum()) if ua else 0
+    B = int(cfg.pack_size)
+    rebuild = histogram_mode == "rebuild"
+    out = {
+        "nodes_processed": ua, "nodes_skipped": 0, "rows_total": rows,
+        "feature_blocks": 1 if ua else 0, "bincount_calls": 2 if ua else 0,
+        "hist_ms": 0.0, "scan_ms": 0.0, "score_ms": 0.0, "partition_ms": 0.0,
+        "nodes_subtract_ok": 0 if rebuild else ua, "nodes_rebuild": ua if rebuild else 0,
+        "nodes_subtract_fallback": 0, "nodes_collapsed": (B - 1) * ua,
+        "feature_block_size": k, "depth": d, "feature_subset_size": k, "pack_size": B,
+        "layer_feature_fraction": float(cfg.layer_feature_fraction),
+        "histogram_mode": histogram_mode, "seed": cfg.random_state,
+        "torch_threads": torch.get_num_threads(),
+    }
+    return out
+
+
+def column_major_bins(bins_rowmajor: np.ndarray | torch.Tensor, perm: np.ndarray | None,
+                      device: torch.device, chunk_rows: int = 1 << 18) -> torch.Tensor:
+    """Row-major bins [N, F] -> device uint8 [F, ld] with rows permuted era-major.
+
+    Transposes on the device in row chunks so host memory holds only the input.
+    """
+    if isinstance(bins_rowmajor, torch.Tensor):
+        src = bins_rowmajor
+        N, F = src.shape
+    else:
+        src = np.asarray(bins_rowmajor)
+        N, F = src.shape
+    ld = padded_rows(N)
+    out = torch.zeros((F, ld), dtype=torch.uint8, device=device)
+    perm_t = None
+    if perm is not None:
+        perm_t = torch.as_tensor(perm, dtype=torch.int64)
+    for r0 in range(0, N, chunk_rows):
+        r1 = min(N, r0 + chunk_rows)
+        if perm_t is None:
+            part = src[r0:r1]
+        else:
+            idx = perm_t[r0:r1]
+            part = src[idx.numpy()] if isinstance(src, np.ndarray) else src[idx.to(src.device)]
+        t = torch.as_tensor(part).to(device=device).view(torch.uint8)
+        out[:, r0:r1] = t.t()
+    return out
+
+
+def bins_max(bins_fm: torch.Tensor, N: int) -> int:
+    return int(bins_fm[:, :N].max().item()) if N > 0 else 0
+
+
+def clamp_log2(x: float) -> int:
+    return int(math.ceil(math.log2(max(1.0, x))))

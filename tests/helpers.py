@@ -1,0 +1,187 @@
+"""Shared builders for the parity tests: seeded problems, the oracle's view of one depth and
+the GPU's view of the same depth through the C ABI."""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+PB_INACTIVE = 0xFFFF
+
+
+def make_problem(seed: int, N: int, F: int, E: int, nb: int, U: int, *, inactive_frac: float = 0.1,
+                 ragged: bool = True, empty_era: bool = False, grad_scale: float = 1.0) -> dict:
+    """Random bins/grad, an era-major layout and a row -> active-slot assignment."""
+    rng = np.random.default_rng(seed)
+    if ragged:
+        w = rng.uniform(0.3, 1.7, size=E)
+        if empty_era and E > 2:
+            w[E // 2] = 0.0
+        sizes = np.floor(w / w.sum() * N).astype(np.int64)
+        sizes[-1] += N - sizes.sum()
+    else:
+        sizes = np.full(E, N // E, dtype=np.int64)
+        sizes[-1] += N - sizes.sum()
+    offs = np.zeros(E + 1, dtype=np.int64)
+    np.cumsum(sizes, out=offs[1:])
+    era = np.repeat(np.arange(E), sizes)
+    bins = rng.integers(0, nb, size=(N, F), dtype=np.uint8)
+    grad = (rng.standard_normal(N) * grad_scale).astype(np.float32)
+    nid = rng.integers(0, U, size=N).astype(np.int64)
+    if inactive_frac > 0:
+        nid[rng.random(N) < inactive_frac] = PB_INACTIVE
+    return {"bins": bins, "grad": grad, "nid": nid.astype(np.uint16), "era": era,
+            "era_off": offs.astype(np.int32), "N": N, "F": F, "E": E, "nb": nb, "U": U}
+
+
+def node_era_rows(p: dict) -> list[list[np.ndarray]]:
+    nid, era = p["nid"].astype(np.int64), p["era"]
+    out = []
+    for u in range(p["U"]):
+        m = nid == u
+        out.append([np.nonzero(m & (era == e))[0].astype(np.int64) for e in range(p["E"])])
+    return out
+
+
+def depth_for(U: int) -> int:
+    d = 0
+    while (1 << d) < U:
+        d += 1
+    return d
+
+
+class GpuDepth:
+    """Runs hist -> score -> decide -> partition for one teacher-forced depth."""
+
+    def __init__(self, hip, p: dict, K: int, *, msl: int, depth: int | None = None,
+                 max_depth: int | None = None):
+        import torch
+
+        self.torch = torch
+        self.hip = hip
+        self.lib = hip.load()
+        self.p = p
+        N, F, E, nb = p["N"], p["F"], p["E"], p["nb"]
+        self.depth = depth_for(p["U"]) if depth is None else depth
+        D = max(self.depth + 1, max_depth or 0)
+        self.ld = (N + 15) // 16 * 16
+        dims = hip.PbDims(num_rows=N, ld=self.ld, num_features=F, num_eras=E, max_bins=nb,
+                          max_depth=D, max_feats=K, min_samples_leaf=msl)
+        self.offs = np.ascontiguousarray(p["era_off"], dtype=np.int32)
+        ctx = ctypes.c_void_p()
+        hip.check(self.lib.pb_ctx_create(ctypes.byref(dims), self.offs.ctypes.data, ctypes.byref(ctx)),
+                  "pb_ctx_create")
+        self.ctx = ctx
+        dev = torch.device("cuda")
+        bfm = np.zeros((F, self.ld), dtype=np.uint8)
+        bfm[:, :N] = p["bins"].T
+        self.bins = torch.from_numpy(bfm).to(dev)
+        rp = self.ld
+        self.grad = torch.zeros(rp, dtype=torch.float32, device=dev)
+        preds = torch.zeros(rp, dtype=torch.float32, device=dev)
+        preds[:N] = torch.from_numpy(p["grad"]).to(dev)
+        y = torch.zeros(rp, dtype=torch.float32, device=dev)
+        self.nid = torch.zeros(rp, dtype=torch.int16, device=dev)
+        self.tnode = torch.zeros(rp, dtype=torch.int16, device=dev)
+        s = hip.stream_ptr()
+        hip.check(self.lib.pb_round_begin(ctx, preds.data_ptr(), y.data_ptr(), self.grad.data_ptr(),
+                                          self.nid.data_ptr(), self.tnode.data_ptr(), s), "round_begin")
+        nid = np.full(rp, PB_INACTIVE, dtype=np.uint16)
+        nid[:N] = p["nid"]
+        self.nid.copy_(torch.from_numpy(nid.view(np.int16)).to(dev))
+        d = self.depth
+        base = (1 << d) - 1
+        ids = (base + np.arange(p["U"])).astype(np.int32)
+        self.node_ids = ids
+        tn = np.zeros(rp, dtype=np.uint16)
+        act = nid[:N] != PB_INACTIVE
+        tn[:N][act] = ids[nid[:N][act]]
+        self.tnode.copy_(torch.from_numpy(tn.view(np.int16)).to(dev))
+        hip.check(self.lib.pb_frontier_set(ctx, d, p["U"], ids.ctypes.data, (1 << (d + 1)) - 1, s),
+                  "pb_frontier_set")
+        self.max_nodes = int(self.lib.pb_max_nodes(ctx, d))
+        assert self.max_nodes >= p["U"]
+        plane = int(self.lib.pb_hist_plane_elems(ctx, self.max_nodes))
+        self.cnt = torch.zeros(plane, dtype=torch.int32, device=dev)
+        self.g = torch.zeros(plane, dtype=torch.float32, device=dev)
+        self.K = K
+        self.values = torch.zeros(1 << (D + 1), dtype=torch.float32, device=dev)
+        self.dec = torch.zeros(((1 << D) - 1) * 64, dtype=torch.uint8, device=dev)
+
+    def planes(self):
+        p = self.p
+        shape = (p["E"], self.max_nodes, self.K, p["nb"])
+        n = int(np.prod(shape))
+        c = self.cnt[:n].cpu().numpy().reshape(shape)[:, : p["U"]]
+        g = self.g[:n].cpu().numpy().reshape(shape)[:, : p["U"]]
+        return c, g
+
+    def load_planes(self, cnt: np.ndarray, g: np.ndarray) -> None:
+        """Writes [E][U][K][nb] planes into the device buffers (node stride max_nodes)."""
+        torch = self.torch
+        E, U, K, nb = cnt.shape
+        fc = np.zeros((E, self.max_nodes, K, nb), np.int32)
+        fg = np.zeros((E, self.max_nodes, K, nb), np.float32)
+        fc[:, :U], fg[:, :U] = cnt, g
+        self.cnt[: fc.size].copy_(torch.from_numpy(fc.reshape(-1)))
+        self.g[: fg.size].copy_(torch.from_numpy(fg.reshape(-1)))
+
+    def hist(self, feats: np.ndarray) -> None:
+        self.feats = self.torch.from_numpy(np.ascontiguousarray(feats, np.int32)).to("cuda")
+        self.hip.check(self.lib.pb_hist_build(
+            self.ctx, self.bins.data_ptr(), self.grad.data_ptr(), self.nid.data_ptr(),
+            self.feats.data_ptr(), self.K, self.depth, self.max_nodes, self.cnt.data_ptr(),
+            self.g.data_ptr(), self.hip.stream_ptr()), "pb_hist_build")
+
+    def score(self, feats: np.ndarray, params, T: int):
+        torch = self.torch
+        self.feats = torch.from_numpy(np.ascontiguousarray(feats, np.int32)).to("cuda")
+        n = self.max_nodes * self.K * T
+        self.cand_all = torch.zeros(n * 32, dtype=torch.uint8, device="cuda")
+        self.hip.check(self.lib.pb_des_score(
+            self.ctx, self.cnt.data_ptr(), self.g.data_ptr(), self.feats.data_ptr(), self.K,
+            self.depth, self.max_nodes, ctypes.byref(params), self.cand_all.data_ptr(),
+            self.hip.stream_ptr()), "pb_des_score")
+        raw = self.cand_all.cpu().numpy().tobytes()
+        c = np.frombuffer(raw, dtype=self.hip.CANDIDATE_DTYPE).reshape(self.max_nodes, self.K, T)
+        return c[: self.p["U"]]
+
+    def decide(self, params):
+        self.hip.check(self.lib.pb_decide(self.ctx, self.depth, self.max_nodes, ctypes.byref(params),
+                                          self.dec.data_ptr(), self.values.data_ptr(),
+                                          self.hip.stream_ptr()), "pb_decide")
+        raw = self.dec.cpu().numpy().tobytes()
+        d = np.frombuffer(raw, dtype=self.hip.DECISION_DTYPE)
+        base = (1 << self.depth) - 1
+        return d[base: base + self.p["U"]].copy()
+
+    def partition(self):
+        self.hip.check(self.lib.pb_partition(self.ctx, self.bins.data_ptr(), self.depth,
+                                             self.nid.data_ptr(), self.tnode.data_ptr(),
+                                             self.hip.stream_ptr()), "pb_partition")
+        N = self.p["N"]
+        nid = self.nid.cpu().numpy().view(np.uint16)[:N].copy()
+        tn = self.tnode.cpu().numpy().view(np.uint16)[:N].copy()
+        return nid, tn
+
+    def frontier(self):
+        u = np.zeros(17, np.int32)
+        ts = ctypes.c_int32(0)
+        self.hip.check(self.lib.pb_frontier_counts(self.ctx, u.ctypes.data, ctypes.byref(ts),
+                                                   self.hip.stream_ptr()), "pb_frontier_counts")
+        return u, int(ts.value)
+
+    def close(self):
+        self.torch.cuda.synchronize()
+        self.lib.pb_ctx_destroy(self.ctx)
+
+
+def split_params(hip, *, lambda_l2=1e-6, lambda_dro=0.0, direction_weight=0.0, era_alpha=0.0,
+                 msl=20, k_cuts=0, cut_selection="mass"):
+    p = hip.PbSplitParams()
+    p.lambda_l2, p.lambda_dro, p.direction_weight, p.era_alpha = (
+        float(lambda_l2), float(lambda_dro), float(direction_weight), float(era_alpha))
+    p.min_samples_leaf, p.k_cuts = int(msl), int(k_cuts)
+    p.cut_selection = 1 if cut_selection == "mass" else 0
+    return p

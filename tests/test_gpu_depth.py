@@ -1,0 +1,137 @@
+"""Teacher-forced parity of one depth (kernels 1-3) against the CPU oracle.
+
+Inputs: seeded random bins/grad/era layouts and a row -> node assignment. The oracle is the
+restated reference split finder (frontier_cpu.cpp:111-515). Bars:
+  * counts and node assignments bit-exact;
+  * grad planes within 1e-5 of the per-cell absolute grad mass (sum |g| over the cell's rows);
+  * scorer fed the oracle's planes: every candidate's score / left count / left grad /
+    validity bit-identical, and the chosen (feature, threshold) identical;
+  * scorer on the GPU's own planes: same choice unless the oracle's scores of the two
+    choices are within 1e-6 (a tie).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.helpers import GpuDepth, make_problem, node_era_rows, split_params
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # seed, N, F, E, nb, U, K, msl, lambda_l2, lambda_dro, dir_w, era_alpha
+    (1, 4000, 12, 6, 5, 1, 12, 20, 1e-6, 0.5, 0.0, 0.0),
+    (2, 6000, 20, 9, 16, 4, 9, 10, 1.0, 0.5, 0.0, 0.0),
+    (3, 9000, 30, 17, 128, 8, 16, 5, 1e-6, 0.1, 0.2, 1.5),
+    (4, 3000, 8, 3, 2, 2, 8, 1, 0.5, 0.0, 0.0, 0.0),
+    (5, 20000, 40, 40, 5, 32, 24, 20, 1e-6, 0.5, 0.0, 0.0),
+    (6, 5000, 10, 5, 255, 3, 10, 3, 1.0, 1.0, 0.0, 2.5),
+]
+
+
+def _abs_mass(p, U):
+    """sum |g| per (era, node) — the scale of any grad cell of that (era, node)."""
+    nid = p["nid"].astype(np.int64)
+    m = np.zeros((p["E"], U))
+    act = nid < U
+    np.add.at(m, (p["era"][act], nid[act]), np.abs(p["grad"][act].astype(np.float64)))
+    return m
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"case{c[0]}" for c in CASES])
+def test_depth_parity(hip, oracle_mod, case):
+    seed, N, F, E, nb, U, K, msl, lam, dro, dw, alpha = case
+    print(f"[depth parity] seed={seed} N={N} F={F} E={E} nb={nb} U={U} K={K}", flush=True)
+    p = make_problem(seed, N, F, E, nb, U, empty_era=(seed % 2 == 0))
+    rng = np.random.default_rng(seed + 100)
+    feats = rng.permutation(F)[:K].astype(np.int32)
+    kw = dict(lambda_l2=lam, lambda_dro=dro, direction_weight=dw, era_alpha=alpha,
+              min_samples_leaf=msl)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb,
+                                 want_planes=True, want_cands=True, **kw)
+    g = GpuDepth(hip, p, K, msl=msl)
+    try:
+        g.hist(feats)
+        cnt, gp = g.planes()
+        rc, rg = ref.planes
+        np.testing.assert_array_equal(cnt, rc)
+        mass = _abs_mass(p, U)[:, :, None, None]
+        err = np.abs(gp.astype(np.float64) - rg.astype(np.float64))
+        assert np.all(err <= 1e-5 * np.maximum(mass, 1.0)), float((err / np.maximum(mass, 1.0)).max())
+
+        params = split_params(hip, lambda_l2=lam, lambda_dro=dro, direction_weight=dw,
+                              era_alpha=alpha, msl=msl)
+        T = nb - 1
+        # (a) scorer on the GPU's own histogram -> decisions
+        own = g.score(feats, params, T)
+        dec = g.decide(params)
+        # (b) scorer fed the oracle planes: bit-exact candidates
+        g.load_planes(rc, rg)
+        c = g.score(feats, params, T)
+        rs, rl, rlg, rv = ref.cands
+        np.testing.assert_array_equal(c["valid"].astype(bool), rv.astype(bool))
+        v = rv.astype(bool)
+        np.testing.assert_array_equal(c["score"][v].view(np.uint32), rs[v].view(np.uint32))
+        np.testing.assert_array_equal(c["left_total"][v], rl[v])
+        np.testing.assert_array_equal(c["left_grad"][v].view(np.uint32), rlg[v].view(np.uint32))
+
+        for u in range(U):
+            if ref.feature[u] < 0:
+                assert dec["split"][u] == 0
+                continue
+            assert dec["split"][u] == 1
+            if (dec["feature"][u], dec["threshold"][u]) != (ref.feature[u], ref.threshold[u]):
+                k = int(np.nonzero(feats == dec["feature"][u])[0][0])
+                s_gpu_choice = rs[u, k, dec["threshold"][u]]
+                assert abs(float(s_gpu_choice) - float(ref.score[u])) <= 1e-6 * max(1.0, abs(float(ref.score[u]))), \
+                    f"node {u}: not a tie"
+                continue
+            assert dec["left_count"][u] == ref.left_count[u]
+            assert dec["right_count"][u] == ref.right_count[u]
+            assert abs(float(dec["left_grad"][u]) - float(ref.left_grad[u])) <= 1e-5 * max(1.0, float(np.abs(p["grad"]).sum()))
+
+        # partition with the GPU's decisions vs the restated rule bin <= thr -> left
+        nid_after, tn_after = g.partition()
+        u_next, tsize = g.frontier()
+        nid0 = p["nid"].astype(np.int64)
+        exp_tn = np.zeros(N, np.int64)
+        exp_nid = np.full(N, 0xFFFF, np.int64)
+        act = nid0 < U
+        exp_tn[act] = g.node_ids[nid0[act]]
+        slot = 0
+        for u in range(U):
+            rows = np.nonzero(nid0 == u)[0]
+            if not dec["split"][u]:
+                continue
+            side = (p["bins"][rows, dec["feature"][u]] > dec["threshold"][u]).astype(np.int64)
+            exp_tn[rows] = dec["left_id"][u] + side
+            cnts = [int(np.sum(side == 0)), int(np.sum(side == 1))]
+            assert cnts[0] == dec["left_count"][u] and cnts[1] == dec["right_count"][u]
+            for s_ in (0, 1):
+                if cnts[s_] >= 2 * msl:
+                    exp_nid[rows[side == s_]] = slot
+                    slot += 1
+        np.testing.assert_array_equal(tn_after.astype(np.int64), exp_tn)
+        np.testing.assert_array_equal(nid_after.astype(np.int64), exp_nid)
+        assert u_next[g.depth + 1] == slot
+    finally:
+        g.close()
+
+
+def test_hist_extreme_grad_scale(hip, oracle_mod):
+    """Fixed-point grad sums hold up for tiny and huge gradient magnitudes."""
+    for scale in (1e-20, 1e20):
+        p = make_problem(11, 3000, 6, 4, 7, 2, grad_scale=scale)
+        feats = np.arange(6, dtype=np.int32)
+        ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, 7, want_planes=True)
+        g = GpuDepth(hip, p, 6, msl=1)
+        try:
+            g.hist(feats)
+            cnt, gp = g.planes()
+            np.testing.assert_array_equal(cnt, ref.planes[0])
+            mass = _abs_mass(p, 2)[:, :, None, None]
+            err = np.abs(gp.astype(np.float64) - ref.planes[1].astype(np.float64))
+            assert np.all(err <= 1e-5 * mass + 1e-30 * scale)
+        finally:
+            g.close()
