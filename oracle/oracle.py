@@ -201,7 +201,7 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
         min_samples_leaf: int = 20, max_bins: int = 63, k_cuts: int = 0,
         cut_selection: str = "mass", layer_feature_fraction: float = 1.0, era_alpha: float = 0.0,
         random_state: int | None = None, rng: torch.Generator | None = None,
-        stop_after_depths: int | None = None) -> FitResult:
+        stop_after_depths: int | None = None, trace: list | None = None) -> FitResult:
     """PackBoost.fit on the native CPU path, restated (booster.py:375-599)."""
     import time
 
@@ -247,6 +247,10 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
             res = split_batch(bins, grad, [er for _, er in active], feat_subset, max_bins, k_cuts,
                               cut_selection, lambda_l2, lambda_dro, direction_weight, era_alpha, msl)
             split_ms += float(res.timings.sum())
+            if trace is not None:
+                trace.append({"round": len(rounds), "depth": depth, "node_ids": [n for n, _ in active],
+                              "feats": feat_subset, "nodes_era_rows": [er for _, er in active],
+                              "grad": grad, "result": res})
             nxt = []
             pos = 0
             for m, (nid, er) in enumerate(active):

@@ -33,14 +33,27 @@ struct Cand {
     int valid;
 };
 
+// a beats b: valid first, then higher score, then (exact score tie) larger left count, larger
+// feature id, larger threshold. Written without early returns: with early returns the gfx950
+// backend of this toolchain emitted a winner update that kept the old feature/threshold on
+// the tie path (the IR was right, the machine code was not), so both the comparison and the
+// update below are plain boolean algebra and per-field selects.
 __device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
-    if (!a.valid) return false;
-    if (!b.valid) return true;
-    if (a.score > b.score) return true;
-    if (a.score < b.score) return false;
-    if (a.lt != b.lt) return a.lt > b.lt;
-    if (a.f != b.f) return a.f > b.f;
-    return a.thr > b.thr;
+    const bool a_ok = a.valid != 0;
+    const bool b_ok = b.valid != 0;
+    const bool s_gt = a.score > b.score;
+    const bool s_eq = a.score == b.score;
+    const bool tie_win = (a.lt > b.lt) | ((a.lt == b.lt) & ((a.f > b.f) | ((a.f == b.f) & (a.thr > b.thr))));
+    return a_ok & ((!b_ok) | s_gt | (s_eq & tie_win));
+}
+
+__device__ __forceinline__ void take_if(bool take, const Cand& c, Cand& best) {
+    best.score = take ? c.score : best.score;
+    best.lt = take ? c.lt : best.lt;
+    best.lg = take ? c.lg : best.lg;
+    best.f = take ? c.f : best.f;
+    best.thr = take ? c.thr : best.thr;
+    best.valid = take ? c.valid : best.valid;
 }
 
 __device__ __forceinline__ Cand shfl_xor_cand(const Cand& c, int m) {
@@ -161,7 +174,7 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) {
         const Cand o = shfl_xor_cand(c, m);
-        if (better(o, c)) c = o;
+        take_if(better(o, c), o, c);
     }
     if ((j & (kWave - 1)) == 0) {
         const int W = KTpad / kWave;
@@ -286,7 +299,7 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
             best.score = 0.f; best.lt = 0; best.lg = 0.f; best.f = -1; best.thr = -1;
             for (int w = 0; w < W; ++w) {
                 const Cand c = load_cand(cand_w + (int64_t)u * W + w);
-                if (better(c, best)) best = c;
+                take_if(better(c, best), c, best);
             }
             const NodeTotal nt = ntot[u];
             SplitRule r;

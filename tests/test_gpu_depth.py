@@ -135,3 +135,29 @@ def test_hist_extreme_grad_scale(hip, oracle_mod):
             assert np.all(err <= 1e-5 * mass + 1e-30 * scale)
         finally:
             g.close()
+
+
+@pytest.mark.parametrize("nb,hi", [(128, 126), (128, 64), (200, 190), (6, 4)])
+def test_exact_ties_pick_largest_threshold(hip, oracle_mod, nb, hi):
+    """Rows only in bins 0 and `hi`: thresholds 0..hi-1 give the same split, so their scores
+    are bit-identical and the reference's tie-break (frontier_cpu.cpp:415-426) keeps the
+    largest threshold, hi-1 — across wavefront boundaries of the candidate space too."""
+    N, E = 4000, 3
+    rng = np.random.default_rng(nb + hi)
+    p = make_problem(7, N, 2, E, nb, 1, inactive_frac=0.0)
+    p["bins"][:, 0] = np.where(rng.random(N) < 0.4, 0, hi).astype(np.uint8)
+    feats = np.array([0, 1], dtype=np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, want_cands=True,
+                                 min_samples_leaf=5)
+    g = GpuDepth(hip, p, 2, msl=5)
+    try:
+        g.hist(feats)
+        params = split_params(hip, msl=5)
+        c = g.score(feats, params, nb - 1)
+        dec = g.decide(params)
+        s0 = c["score"][0, 0, :hi]
+        assert np.all(s0.view(np.uint32) == s0[0].view(np.uint32))
+        assert (dec["feature"][0], dec["threshold"][0]) == (ref.feature[0], ref.threshold[0]), \
+            (dec["feature"][0], dec["threshold"][0], ref.feature[0], ref.threshold[0])
+    finally:
+        g.close()

@@ -1,0 +1,175 @@
+"""Teacher-forced fit parity: every depth of every round is compared against the oracle.
+
+The oracle runs the restated reference fit (booster.py:375-599 with the restated
+frontier_cpu.cpp split finder) and records, per depth, the active nodes' era row lists, the
+feature subset and its decisions. The GPU replays the same rounds through the C ABI with the
+oracle's predictions forced in at every round start (so gradients are identical) and at each
+depth must reproduce:
+  * the row -> node assignment (bit-exact, from its own partition of the previous depth),
+  * the histogram counts (bit-exact) and grad sums (1e-5 of the cell's |g| mass),
+  * the decisions: identical (feature, threshold) unless the oracle's scores of the two
+    choices tie within 1e-6, identical child counts.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(hip, oracle_mod, X, y, era_codes, kw, rounds):
+    import torch
+
+    from packboost_amd import PackBoostConfig
+    from packboost_amd.data import preprocess_features
+    from packboost_amd.engine import split_params, subset_size
+    from tests.helpers import PB_INACTIVE
+
+    cfg = PackBoostConfig(**kw)
+    bins = preprocess_features(X, cfg.max_bins).bins
+    N, F = bins.shape
+    trace: list = []
+    ref_preds = []
+    # oracle rounds one at a time to capture the predictions entering each round
+    gen = torch.Generator().manual_seed(int(kw["random_state"]))
+    preds_in = np.zeros(N, np.float32)
+    ref_kw = {k: v for k, v in kw.items() if k != "random_state"}
+    all_rounds = []
+    cur_preds = np.zeros(N, np.float32)
+    for r in range(rounds):
+        ref_preds.append(cur_preds.copy())
+        t: list = []
+        # continue from cur_preds: oracle.fit starts at preds 0, so fit on the residual target
+        res = oracle_mod.fit(bins, (y - cur_preds).astype(np.float32), era_codes, num_rounds=1,
+                             rng=gen, trace=t, **ref_kw)
+        for item in t:
+            item["round"] = r
+        trace += t
+        all_rounds.append(res.rounds[0])
+        cur_preds = (cur_preds + res.preds).astype(np.float32)
+
+    E = int(era_codes.max()) + 1
+    order = np.argsort(era_codes, kind="stable")
+    assert np.array_equal(order, np.arange(N)), "test data must be era-major"
+    offs = np.zeros(E + 1, np.int64)
+    np.cumsum(np.bincount(era_codes, minlength=E), out=offs[1:])
+    offs = offs.astype(np.int32)
+    K = subset_size(cfg, F)
+    D = cfg.max_depth
+    lib = hip.load()
+    ld = (N + 15) // 16 * 16
+    dims = hip.PbDims(num_rows=N, ld=ld, num_features=F, num_eras=E, max_bins=cfg.max_bins,
+                      max_depth=D, max_feats=K, min_samples_leaf=cfg.min_samples_leaf)
+    ctx = ctypes.c_void_p()
+    hip.check(lib.pb_ctx_create(ctypes.byref(dims), offs.ctypes.data, ctypes.byref(ctx)), "ctx")
+    dev = torch.device("cuda")
+    bfm = np.zeros((F, ld), np.uint8)
+    bfm[:, :N] = bins.T
+    bins_d = torch.from_numpy(bfm).to(dev)
+    yd = torch.zeros(ld, device=dev)
+    preds = torch.zeros(ld, device=dev)
+    grad = torch.zeros(ld, device=dev)
+    nid = torch.zeros(ld, dtype=torch.int16, device=dev)
+    tnode = torch.zeros(ld, dtype=torch.int16, device=dev)
+    maxn = [int(lib.pb_max_nodes(ctx, d)) for d in range(D)]
+    plane = max(int(lib.pb_hist_plane_elems(ctx, m)) for m in maxn)
+    cnt = torch.zeros(plane, dtype=torch.int32, device=dev)
+    gp = torch.zeros(plane, dtype=torch.float32, device=dev)
+    values = torch.zeros(1 << (D + 1), device=dev)
+    dec = torch.zeros(((1 << D) - 1) * 64, dtype=torch.uint8, device=dev)
+    params = split_params(cfg)
+    s = hip.stream_ptr()
+    yd[:N] = torch.from_numpy(np.zeros(N, np.float32))
+    try:
+        by_round: dict = {}
+        for item in trace:
+            by_round.setdefault(item["round"], []).append(item)
+        for r in range(rounds):
+            # grad = preds - y with preds := oracle preds entering the round, y := y
+            preds[:N] = torch.from_numpy(ref_preds[r]).to(dev)
+            yd[:N] = torch.from_numpy(y).to(dev)
+            hip.check(lib.pb_round_begin(ctx, preds.data_ptr(), yd.data_ptr(), grad.data_ptr(),
+                                         nid.data_ptr(), tnode.data_ptr(), s), "round_begin")
+            g_host = grad[:N].cpu().numpy()
+            for item in by_round.get(r, []):
+                d = item["depth"]
+                np.testing.assert_array_equal(g_host, item["grad"], err_msg=f"round {r} grad")
+                U = len(item["node_ids"])
+                exp = np.full(N, PB_INACTIVE, np.int64)
+                for u, er in enumerate(item["nodes_era_rows"]):
+                    for rows in er:
+                        exp[rows] = u
+                got_nid = nid.cpu().numpy().view(np.uint16)[:N].astype(np.int64)
+                np.testing.assert_array_equal(got_nid, exp, err_msg=f"round {r} depth {d} nid")
+                feats = torch.from_numpy(item["feats"].astype(np.int32)).to(dev)
+                hip.check(lib.pb_hist_build(ctx, bins_d.data_ptr(), grad.data_ptr(), nid.data_ptr(),
+                                            feats.data_ptr(), K, d, maxn[d], cnt.data_ptr(),
+                                            gp.data_ptr(), s), "hist")
+                ref = oracle_mod.split_batch(bins, item["grad"], item["nodes_era_rows"], item["feats"],
+                                             cfg.max_bins, cfg.k_cuts, cfg.cut_selection,
+                                             cfg.lambda_l2, cfg.lambda_dro, cfg.direction_weight,
+                                             cfg.era_alpha, cfg.min_samples_leaf, want_planes=True,
+                                             want_cands=True)
+                shape = (E, maxn[d], K, cfg.max_bins)
+                n = int(np.prod(shape))
+                c_got = cnt[:n].cpu().numpy().reshape(shape)[:, :U]
+                np.testing.assert_array_equal(c_got, ref.planes[0], err_msg=f"round {r} depth {d} counts")
+                hip.check(lib.pb_des_score(ctx, cnt.data_ptr(), gp.data_ptr(), feats.data_ptr(), K, d,
+                                           maxn[d], ctypes.byref(params), None, s), "score")
+                hip.check(lib.pb_decide(ctx, d, maxn[d], ctypes.byref(params), dec.data_ptr(),
+                                        values.data_ptr(), s), "decide")
+                dd = np.frombuffer(dec.cpu().numpy().tobytes(), dtype=hip.DECISION_DTYPE)
+                dd = dd[(1 << d) - 1: (1 << d) - 1 + U]
+                cs = ref.cands[0]
+                for u in range(U):
+                    if ref.feature[u] < 0:
+                        assert dd["split"][u] == 0, f"round {r} depth {d} node {u}"
+                        continue
+                    assert dd["split"][u] == 1, f"round {r} depth {d} node {u}"
+                    pick = (int(dd["feature"][u]), int(dd["threshold"][u]))
+                    want = (int(ref.feature[u]), int(ref.threshold[u]))
+                    if pick != want:
+                        k = int(np.nonzero(item["feats"] == pick[0])[0][0])
+                        T = cfg.max_bins - 1
+                        call = torch.zeros(maxn[d] * K * T * 32, dtype=torch.uint8, device=dev)
+                        hip.check(lib.pb_des_score(ctx, cnt.data_ptr(), gp.data_ptr(), feats.data_ptr(),
+                                                   K, d, maxn[d], ctypes.byref(params), call.data_ptr(), s),
+                                  "score dump")
+                        ca = np.frombuffer(call.cpu().numpy().tobytes(), dtype=hip.CANDIDATE_DTYPE)
+                        ca = ca.reshape(maxn[d], K, T)
+                        for t_ in range(max(0, pick[1] - 3), min(T, pick[1] + 4)):
+                            print("lane", u, k, t_, "j", k * T + t_, ca[u, k, t_], "oracle", cs[u, k, t_],
+                                  ref.cands[1][u, k, t_], ref.cands[3][u, k, t_], flush=True)
+                        alt = float(cs[u, k, pick[1]])
+                        best = float(ref.score[u])
+                        raise AssertionError(
+                            f"round {r} depth {d} node {u}: gpu {pick} (oracle score {alt!r}, "
+                            f"left {int(ref.cands[1][u, k, pick[1]])}) vs oracle {want} "
+                            f"(score {best!r}, left {int(ref.left_count[u])}); gpu left "
+                            f"{int(dd['left_count'][u])} score {float(dd['score'][u])!r}")
+                    assert dd["left_count"][u] == ref.left_count[u]
+                    assert dd["right_count"][u] == ref.right_count[u]
+                hip.check(lib.pb_partition(ctx, bins_d.data_ptr(), d, nid.data_ptr(),
+                                           tnode.data_ptr(), s), "partition")
+    finally:
+        torch.cuda.synchronize()
+        lib.pb_ctx_destroy(ctx)
+
+
+@pytest.mark.parametrize("kw", [
+    dict(pack_size=8, max_depth=5, learning_rate=0.05, lambda_l2=1.0, lambda_dro=0.5,
+         min_samples_leaf=20, max_bins=128, random_state=42),
+    dict(pack_size=4, max_depth=4, learning_rate=0.2, lambda_l2=1e-3, lambda_dro=0.1,
+         direction_weight=0.05, min_samples_leaf=5, max_bins=63, layer_feature_fraction=0.6,
+         era_alpha=1.5, random_state=13),
+], ids=["config1", "dir_alpha"])
+def test_teacher_forced_fit(hip, oracle_mod, kw):
+    from tests.test_gpu_fit import config1_data
+
+    X, y, era = config1_data()
+    print(f"[teacher forced] {kw}", flush=True)
+    _run(hip, oracle_mod, X, y, era.astype(np.int64), kw, rounds=6)
