@@ -24,6 +24,7 @@ struct pb_ctx {
     pb::SplitRule* rules;
     pb::NodeTotal* ntot;
     pb_candidate* cand_w;
+    pb_candidate* node_best;
     int32_t* ids[2];
     int32_t* thr_tab;
     int32_t last_w;
@@ -90,6 +91,7 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->rules);
     (void)hipFree(c->ntot);
     (void)hipFree(c->cand_w);
+    (void)hipFree(c->node_best);
     (void)hipFree(c->ids[0]);
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
@@ -147,7 +149,12 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     c->umax = 1;
     for (int dd = 0; dd < d.max_depth; ++dd) c->umax = std::max(c->umax, max_nodes_at(c, dd));
     const int tmax = std::max(1, d.max_bins - 1);
-    c->wmax = (int32_t)(((int64_t)d.max_feats * tmax + pb::kWave - 1) / pb::kWave);
+    c->wmax = 1;
+    for (int t = 1; t <= tmax; ++t)
+        for (int dd = 0; dd < d.max_depth; ++dd) {
+            const pb::ScoreShape sh = pb::score_shape(d.max_feats, t, d.num_eras, max_nodes_at(c, dd));
+            c->wmax = std::max(c->wmax, sh.ntiles * sh.wpt);
+        }
     c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 64 * 1024);
     c->force_copies = (int32_t)env_int("PB_HIST_COPIES", 0);
     c->force_ftile = (int32_t)env_int("PB_HIST_FTILE", 0);
@@ -158,6 +165,7 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
         (rc = dev_alloc(&c->rules, c->umax, "alloc split rules")) ||
         (rc = dev_alloc(&c->ntot, c->umax, "alloc node totals")) ||
         (rc = dev_alloc(&c->cand_w, (size_t)c->umax * c->wmax, "alloc candidates")) ||
+        (rc = dev_alloc(&c->node_best, c->umax, "alloc node winners")) ||
         (rc = dev_alloc(&c->ids[0], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
         (rc = dev_alloc(&c->ids[1], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
         (rc = dev_alloc(&c->thr_tab, (size_t)d.max_feats * tmax, "alloc threshold table"))) {
@@ -291,11 +299,10 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
                "kcuts launch");
         thr_tab = c->thr_tab;
     }
-    const int64_t KT = (int64_t)K * T;
-    const int64_t KTpad = (KT + pb::kWave - 1) / pb::kWave * pb::kWave;
-    const int64_t lanes = KTpad * max_nodes_at(c, depth);
-    const int64_t grid = (lanes + pb::kBlock - 1) / pb::kBlock;
+    const pb::ScoreShape sh = pb::score_shape(K, T, c->d.num_eras, max_nodes_at(c, depth));
+    const int64_t grid = (int64_t)sh.ntiles * max_nodes_at(c, depth);
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_des_score: grid too large");
+    if (sh.ntiles * sh.wpt > c->wmax) return fail(PB_ERR_INVALID, "pb_des_score: candidate buffer too small");
     pb::ScoreArgs a;
     a.cnt = hist_cnt;
     a.g = hist_grad;
@@ -316,8 +323,13 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     a.cand_w = c->cand_w;
     a.cand_all = cand_all;
     a.ntot = c->ntot;
-    c->last_w = (int32_t)(KTpad / pb::kWave);
-    PB_HIP(pb::launch_score(a, (int)grid, (hipStream_t)stream), "score launch");
+    a.fts = sh.fts;
+    a.ntiles = sh.ntiles;
+    a.ec = sh.ec;
+    a.wpt = sh.wpt;
+    a.rt = sh.rt;
+    c->last_w = sh.ntiles * sh.wpt;
+    PB_HIP(pb::launch_score(a, (int)grid, sh.lds_bytes, (hipStream_t)stream), "score launch");
     return PB_OK;
 }
 
@@ -329,7 +341,7 @@ int pb_decide(pb_ctx* c, int32_t depth, int32_t max_nodes, const pb_split_params
     (void)max_nodes;
     PB_HIP(pb::launch_decide(c->cand_w, c->last_w, c->ntot, c->st, depth, p->min_samples_leaf,
                              p->lambda_l2, c->ids[depth & 1], c->ids[(depth + 1) & 1], c->rules,
-                             dec, values, (hipStream_t)stream),
+                             dec, values, c->node_best, (hipStream_t)stream),
            "decide launch");
     return PB_OK;
 }

@@ -73,21 +73,35 @@ struct ScoreArgs {
     int32_t msl;
     const Frontier* st;
     int32_t depth;
-    pb_candidate* cand_w;    // [U][W] wavefront winners
+    pb_candidate* cand_w;    // [U][W] wavefront winners, W = ntiles * wpt
     pb_candidate* cand_all;  // optional [U][K][T]
     NodeTotal* ntot;         // [U]
+    int32_t fts;             // features per workgroup
+    int32_t ntiles;          // feature tiles per node
+    int32_t ec;              // eras staged in LDS per chunk
+    int32_t wpt;             // wavefront winners per tile (ceil(fts * T / 64))
+    int32_t rt;              // size of the 1/n table (equal era weights)
 };
+
+// Launch shape of the scorer for K features and T thresholds (shared by the context's
+// buffer sizing and the launch).
+struct ScoreShape {
+    int32_t fts, ntiles, ec, wpt, rt;
+    size_t lds_bytes;
+};
+ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes);
 
 // Launchers (defined in the .hip files; all return hipError_t of the launch).
 hipError_t launch_hist(const HistArgs& a, int grid, size_t lds_bytes, hipStream_t s);
-hipError_t launch_score(const ScoreArgs& a, int grid, hipStream_t s);
+hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_kcuts(const int32_t* cnt, int32_t E, int32_t U, int32_t K, int32_t nb,
                         int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                         int32_t* thr_tab, hipStream_t s);
 hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal* ntot,
                          Frontier* st, int32_t depth, int32_t msl, double lambda_l2,
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
-                         pb_decision* dec, float* values, hipStream_t s);
+                         pb_decision* dec, float* values, pb_candidate* node_best,
+                         hipStream_t s);
 hipError_t launch_partition(const uint8_t* bins, int64_t ld, int64_t rows_padded,
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s);

@@ -19,6 +19,8 @@
 // a 6-step xor-shuffle argmax yields the wavefront's winner. Ties on the exact score are
 // broken like the reference: larger left count, then larger feature id, then larger
 // threshold (frontier_cpu.cpp:415-426).
+#include <algorithm>
+
 #include "pb_internal.h"
 
 namespace pb {
@@ -89,96 +91,213 @@ __device__ __forceinline__ Cand load_cand(const pb_candidate* src) {
     return c;
 }
 
-__global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
-    const int KT = a.K * a.T;
-    const int KTpad = (KT + kWave - 1) & ~(kWave - 1);
-    const int64_t gid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-    const int u = (int)(gid / KTpad);
-    const int j = (int)(gid - (int64_t)u * KTpad);
-    const int Ua = a.st->u_active[a.depth];
-    if (u >= Ua) return;  // uniform per wavefront: KTpad is a multiple of 64
+// Scorer. One workgroup owns one (node, tile of `fts` features) = fts * T candidates and walks
+// the eras in chunks of `ec`, software-pipelined:
+//   every thread holds kPairs (candidate, era) pairs of the NEXT chunk in registers (the four
+//   plane values each needs), so the chunk's global loads are in flight while
+//   phase A (all threads) turns the current pairs into gain / weight / direction in LDS and
+//   phase B (one thread per candidate) runs the weighted Welford recurrence in era order over
+//   the previous chunk. LDS is double-buffered, so one barrier per chunk orders the stages.
+// With equal era weights (era_alpha == 0) the Welford factor w / wsum is 1 / n for the n-th
+// valid era, read from a table of IEEE divisions 1.0f / n (bit-identical to the division).
+constexpr int kPairs = 4;
 
-    const bool lane_ok = j < KT;
-    const int k = lane_ok ? j / a.T : 0;
-    const int t = lane_ok ? j - k * a.T : 0;
-    const int thr = a.thr_tab ? a.thr_tab[k * a.T + t] : t;
+struct PairIn {
+    int ctot, L;
+    float Gt, GL;
+};
+
+__global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
+    extern __shared__ unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int u = blockIdx.x / a.ntiles;
+    const int tile = blockIdx.x - u * a.ntiles;
+    const int Ua = a.st->u_active[a.depth];
+    if (u >= Ua) return;
+    const int k0 = tile * a.fts;
+    const int nf = min(a.fts, a.K - k0);
+    if (nf <= 0) return;
+    const int T = a.T;
     const int nb = a.nb;
-    const int64_t estride = (int64_t)a.U * a.K * nb;
-    const int32_t* pc = a.cnt + ((int64_t)u * a.K + k) * nb;
-    const float* pg = a.g + ((int64_t)u * a.K + k) * nb;
+    const int ncand = nf * T;
+    const int cstride = a.fts * T;  // LDS row stride (max candidates of a tile)
+    const int EC = a.ec;
+    const int RT = a.rt;
+    const int buf_words = EC * cstride;
+
+    float* recip = reinterpret_cast<float*>(smem);
+    float* base_f = recip + RT;
+    // buffer b: sG, sGL, sL, sWD (each EC x cstride), then sCt, sGt (each EC)
+    const int buf_stride = 4 * buf_words + 2 * EC;
+
+    for (int i = tid; i < RT; i += kBlock) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
+
     const float lam = a.lambda_l2;
     const float alpha = a.era_alpha;
     const bool use_dir = a.dir_w != 0.0f;
+    const bool unit_w = !(alpha > 0.0f);
+    const int64_t ustride = (int64_t)a.K * nb;
+    const int64_t estride = (int64_t)a.U * ustride;
+    const int64_t node_off = (int64_t)u * ustride;
+    const int nchunks = (a.E + EC - 1) / EC;
 
-    float wsum = 0.0f, mean = 0.0f, M2 = 0.0f, agn = 0.0f, agd = 0.0f;
-    float lg = 0.0f, tg = 0.0f;
-    int lt = 0, tc = 0;
-    for (int e = 0; e < a.E; ++e, pc += estride, pg += estride) {
-        const int ctot = pc[nb - 1];
-        if (ctot == 0) continue;
-        const float Gt = pg[nb - 1];
-        const int L = pc[thr];
-        const float GL = pg[thr];
-        const int R = ctot - L;
-        const float GR = Gt - GL;
-        lt += L;
-        lg = lg + GL;
-        tc += ctot;
-        tg = tg + Gt;
-        const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
-        const float w = (L > 0 && R > 0) ? wera : 0.0f;
-        if (w <= 0.0f) continue;
-        const float dL = (float)L + lam;
-        const float dR = (float)R + lam;
-        const float pden = (float)ctot + lam;
-        const float parent = (pden > 0.0f) ? (0.5f * (Gt * Gt)) / pden : 0.0f;
-        const float gain = 0.5f * ((GL * GL) / dL + (GR * GR) / dR) - parent;
-        const float delta = gain - mean;
-        const float wn = wsum + w;
-        if (wn > 0.0f) {
-            const float fac = w / wn;
-            mean = mean + fac * delta;
-            M2 = M2 + (w * delta) * (gain - mean);
-            wsum = wn;
+    PairIn pin[kPairs];
+    auto prefetch = [&](int chunk) {
+        const int e0 = chunk * EC;
+        const int ne = min(EC, a.E - e0);
+#pragma unroll
+        for (int i = 0; i < kPairs; ++i) {
+            const int pidx = tid + i * kBlock;
+            pin[i].ctot = 0;
+            pin[i].L = 0;
+            pin[i].Gt = 0.0f;
+            pin[i].GL = 0.0f;
+            if (pidx < ne * ncand) {
+                const int el = pidx / ncand;
+                const int c = pidx - el * ncand;
+                const int kk = c / T;
+                const int t = c - kk * T;
+                const int k = k0 + kk;
+                const int thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
+                const int64_t off = (int64_t)(e0 + el) * estride + node_off + (int64_t)k * nb;
+                pin[i].ctot = a.cnt[off + nb - 1];
+                pin[i].Gt = a.g[off + nb - 1];
+                pin[i].L = a.cnt[off + thr];
+                pin[i].GL = a.g[off + thr];
+            }
         }
-        if (use_dir) {
-            const float lv = -GL / dL;
-            const float rv = -GR / dR;
-            const float dir = (lv > rv) ? 1.0f : -1.0f;
-            agn = agn + w * dir;
-            agd = agd + w;
+    };
+
+    const bool owner = tid < ncand;
+    float wsum = 0.0f, mean = 0.0f, M2 = 0.0f, agn = 0.0f, agd = 0.0f, lg = 0.0f, tg = 0.0f;
+    int lt = 0, tc = 0;
+
+    prefetch(0);
+    for (int ch = 0; ch < nchunks; ++ch) {
+        const int e0 = ch * EC;
+        const int ne = min(EC, a.E - e0);
+        float* sG = base_f + (ch & 1) * buf_stride;
+        float* sGL = sG + buf_words;
+        int32_t* sL = reinterpret_cast<int32_t*>(sGL + buf_words);
+        float* sWD = reinterpret_cast<float*>(sL + buf_words);
+        int32_t* sCt = reinterpret_cast<int32_t*>(sWD + buf_words);
+        float* sGt = reinterpret_cast<float*>(sCt + EC);
+        // phase A on the prefetched pairs of this chunk
+#pragma unroll
+        for (int i = 0; i < kPairs; ++i) {
+            const int pidx = tid + i * kBlock;
+            if (pidx < ne * ncand) {
+                const int el = pidx / ncand;
+                const int c = pidx - el * ncand;
+                const int ctot = pin[i].ctot;
+                float gain = 0.0f, wd = 0.0f, GL = 0.0f;
+                int L = -1;  // -1: the node has no rows in this era (skipped entirely)
+                if (ctot != 0) {
+                    const float Gt = pin[i].Gt;
+                    L = pin[i].L;
+                    GL = pin[i].GL;
+                    const int R = ctot - L;
+                    const float GR = Gt - GL;
+                    const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
+                    const float w = (L > 0 && R > 0) ? wera : 0.0f;
+                    if (w > 0.0f) {
+                        const float dL = (float)L + lam;
+                        const float dR = (float)R + lam;
+                        const float pden = (float)ctot + lam;
+                        const float parent = (pden > 0.0f) ? (0.5f * (Gt * Gt)) / pden : 0.0f;
+                        gain = 0.5f * ((GL * GL) / dL + (GR * GR) / dR) - parent;
+                        bool pos = true;
+                        if (use_dir) {
+                            const float lv = -GL / dL;
+                            const float rv = -GR / dR;
+                            pos = lv > rv;
+                        }
+                        wd = pos ? w : -w;
+                    }
+                }
+                sG[el * cstride + c] = gain;
+                sGL[el * cstride + c] = GL;
+                sL[el * cstride + c] = L;
+                sWD[el * cstride + c] = wd;
+                if (c == 0) {
+                    sCt[el] = ctot;
+                    sGt[el] = pin[i].Gt;
+                }
+            }
+        }
+        if (ch + 1 < nchunks) prefetch(ch + 1);  // loads in flight across phase B
+        __syncthreads();
+        if (owner) {
+            for (int el = 0; el < ne; ++el) {
+                const int L = sL[el * cstride + tid];
+                const float GLv = sGL[el * cstride + tid];
+                const float wd = sWD[el * cstride + tid];
+                const float gain = sG[el * cstride + tid];
+                const int ct = sCt[el];
+                const float gt = sGt[el];
+                const bool has = L >= 0;
+                lt += has ? L : 0;
+                lg = has ? lg + GLv : lg;
+                tc += ct;
+                tg = (ct != 0) ? tg + gt : tg;
+                const float w = fabsf(wd);
+                const bool act = w > 0.0f;  // implies has; wsum + w > 0 then holds
+                const float wn = wsum + w;
+                const int wi = (int)wn;
+                const float fac = (unit_w && wi < RT) ? recip[act ? wi : 0] : w / (act ? wn : 1.0f);
+                const float delta = gain - mean;
+                const float mean_n = mean + fac * delta;
+                const float M2_n = M2 + (w * delta) * (gain - mean_n);
+                mean = act ? mean_n : mean;
+                M2 = act ? M2_n : M2;
+                wsum = act ? wn : wsum;
+                if (use_dir) {
+                    agn = act ? agn + w * ((wd > 0.0f) ? 1.0f : -1.0f) : agn;
+                    agd = act ? agd + w : agd;
+                }
+            }
         }
     }
 
     Cand c;
     c.lt = lt;
     c.lg = lg;
-    c.f = lane_ok ? a.feats[k] : -1;
-    c.thr = thr;
-    const int rt = tc - lt;
-    const float ws = (wsum < 1e-12f) ? 1e-12f : wsum;
-    const float var = M2 / ws;
-    const float sd = sqrtf((0.0f < var) ? var : 0.0f);
-    float score = mean - a.lambda_dro * sd;
-    if (use_dir && agd > 0.0f) score = score + a.dir_w * (agn / agd);
-    c.score = score;
-    // a node without rows never splits (the reference skips it, frontier_cpu.cpp:191-193)
-    c.valid = (lane_ok && tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
-
-    if (a.cand_all && lane_ok) store_cand(a.cand_all + ((int64_t)u * a.K + k) * a.T + t, c);
-    if (j == 0) {
-        a.ntot[u].count = tc;
-        a.ntot[u].grad = tg;
+    c.valid = 0;
+    c.score = 0.0f;
+    c.f = -1;
+    c.thr = -1;
+    if (owner) {
+        const int kk = tid / T;
+        const int t = tid - kk * T;
+        const int k = k0 + kk;
+        c.f = a.feats[k];
+        c.thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
+        const int rt = tc - lt;
+        const float ws = (wsum < 1e-12f) ? 1e-12f : wsum;
+        const float var = M2 / ws;
+        const float sd = sqrtf((0.0f < var) ? var : 0.0f);
+        float score = mean - a.lambda_dro * sd;
+        if (use_dir && agd > 0.0f) score = score + a.dir_w * (agn / agd);
+        c.score = score;
+        // a node without rows never splits (the reference skips it, frontier_cpu.cpp:191-193)
+        c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
+        if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
+        if (tile == 0 && tid == 0) {
+            a.ntot[u].count = tc;
+            a.ntot[u].grad = tg;
+        }
     }
-
+    const int wave = tid / kWave;
+    if (wave < a.wpt) {
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) {
-        const Cand o = shfl_xor_cand(c, m);
-        take_if(better(o, c), o, c);
-    }
-    if ((j & (kWave - 1)) == 0) {
-        const int W = KTpad / kWave;
-        store_cand(a.cand_w + (int64_t)u * W + (j / kWave), c);
+        for (int m = 1; m < kWave; m <<= 1) {
+            const Cand o = shfl_xor_cand(c, m);
+            take_if(better(o, c), o, c);
+        }
+        if ((tid & (kWave - 1)) == 0) {
+            const int W = a.ntiles * a.wpt;
+            store_cand(a.cand_w + (int64_t)u * W + tile * a.wpt + wave, c);
+        }
     }
 }
 
@@ -278,46 +397,108 @@ __global__ void kcuts_kernel(const int32_t* cnt, int32_t E, int32_t U, int32_t K
     }
 }
 
-// Decision step: one workgroup. Applies booster.py:527-563 to the unique frontier.
+// Block-wide exclusive scan of one int per thread (256 threads); returns the total.
+__device__ int block_exclusive_scan(int v, int* out_excl, int* s_wave) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int incl = v;
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        const int o = __shfl_up(incl, m);
+        if (lane >= m) incl += o;
+    }
+    if (lane == kWave - 1) s_wave[wave] = incl;
+    __syncthreads();
+    int before = 0, total = 0;
+    for (int w = 0; w < kBlock / kWave; ++w) {
+        before += (w < wave) ? s_wave[w] : 0;
+        total += s_wave[w];
+    }
+    __syncthreads();
+    *out_excl = before + incl - v;
+    return total;
+}
+
+// Decision step (booster.py:527-563 on the unique frontier), one workgroup:
+//  1. one wavefront per node reduces the node's W wavefront winners (same order as the
+//     scorer: valid, score, left count, feature, threshold);
+//  2. per node, in parallel: split or leaf, child counts, float32 child / leaf values computed
+//     in double like the reference's Python (-G / (H + lambda));
+//  3. exclusive scans over the frontier order give the children's TreeBuilder ids
+//     (tree_size + 2 * splits before) and their slots in the next frontier (children with
+//     >= 2 * min_samples_leaf rows, left before right).
 __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand_w, int32_t W,
                                                     const NodeTotal* ntot, Frontier* st,
                                                     int32_t depth, int32_t msl, double lambda_l2,
                                                     const int32_t* cur_ids, int32_t* next_ids,
                                                     SplitRule* rules, pb_decision* dec,
-                                                    float* values) {
+                                                    float* values, pb_candidate* node_best) {
+    __shared__ int s_wave[kBlock / kWave];
+    __shared__ int s_carry[2];
     const int Ua = st->u_active[depth];
-    pb_decision* dd = dec + ((1 << depth) - 1);
     const int tree_size0 = st->tree_size;
-    // Sequential scan in frontier order for child ids and next-frontier slots; the number
-    // of active nodes is small (<= 2^(D-1)) and this keeps the order trivially exact.
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    pb_decision* dd = dec + ((1 << depth) - 1);
+
+    for (int u = wave; u < Ua; u += kBlock / kWave) {
+        Cand best;
+        best.valid = 0; best.score = 0.0f; best.lt = 0; best.lg = 0.0f; best.f = -1; best.thr = -1;
+        for (int w = lane; w < W; w += kWave) {
+            const Cand c = load_cand(cand_w + (int64_t)u * W + w);
+            take_if(better(c, best), c, best);
+        }
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const Cand o = shfl_xor_cand(best, m);
+            take_if(better(o, best), o, best);
+        }
+        if (lane == 0) store_cand(node_best + u, best);
+    }
     if (threadIdx.x == 0) {
-        int next_id = tree_size0;
-        int slot = 0;
-        for (int u = 0; u < Ua; ++u) {
-            Cand best;
-            best.valid = 0;
-            best.score = 0.f; best.lt = 0; best.lg = 0.f; best.f = -1; best.thr = -1;
-            for (int w = 0; w < W; ++w) {
-                const Cand c = load_cand(cand_w + (int64_t)u * W + w);
-                take_if(better(c, best), c, best);
-            }
-            const NodeTotal nt = ntot[u];
+        s_carry[0] = 0;
+        s_carry[1] = 0;
+    }
+    __syncthreads();
+
+    for (int base = 0; base < Ua; base += kBlock) {
+        const int u = base + threadIdx.x;
+        const bool in = u < Ua;
+        Cand best;
+        best.valid = 0; best.lt = 0; best.lg = 0.0f; best.f = -1; best.thr = -1; best.score = 0.0f;
+        NodeTotal nt;
+        nt.count = 0;
+        nt.grad = 0.0f;
+        if (in) {
+            best = load_cand(node_best + u);
+            nt = ntot[u];
+        }
+        const int split = (in && best.valid) ? 1 : 0;
+        const int lc = split ? best.lt : 0;
+        const int rc = split ? nt.count - lc : 0;
+        const int la = (split && lc >= 2 * msl) ? 1 : 0;
+        const int ra = (split && rc >= 2 * msl) ? 1 : 0;
+        int split_before, act_before;
+        const int split_total = block_exclusive_scan(split, &split_before, s_wave);
+        const int act_total = block_exclusive_scan(la + ra, &act_before, s_wave);
+        split_before += s_carry[0];
+        act_before += s_carry[1];
+        if (in) {
             SplitRule r;
             pb_decision d;
             d.node_id = cur_ids[u];
             d.node_grad = nt.grad;
             d.node_count = nt.count;
             d.reserved = 0;
-            if (best.valid) {
-                const int lc = best.lt;
-                const int rc = nt.count - lc;
+            if (split) {
+                const int left_id = tree_size0 + 2 * split_before;
                 r.feature = best.f;
                 r.threshold = best.thr;
-                r.left_id = next_id;
-                r.next_slot[0] = (lc >= 2 * msl) ? (uint16_t)(slot++) : (uint16_t)PB_INACTIVE;
-                if (r.next_slot[0] != PB_INACTIVE) next_ids[r.next_slot[0]] = next_id;
-                r.next_slot[1] = (rc >= 2 * msl) ? (uint16_t)(slot++) : (uint16_t)PB_INACTIVE;
-                if (r.next_slot[1] != PB_INACTIVE) next_ids[r.next_slot[1]] = next_id + 1;
+                r.left_id = left_id;
+                r.next_slot[0] = la ? (uint16_t)act_before : (uint16_t)PB_INACTIVE;
+                r.next_slot[1] = ra ? (uint16_t)(act_before + la) : (uint16_t)PB_INACTIVE;
+                if (la) next_ids[act_before] = left_id;
+                if (ra) next_ids[act_before + la] = left_id + 1;
                 d.split = 1;
                 d.feature = best.f;
                 d.threshold = best.thr;
@@ -328,12 +509,11 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
                 d.right_hess = (float)nt.count - d.left_hess;
                 d.left_count = lc;
                 d.right_count = rc;
-                d.left_id = next_id;
-                d.right_id = next_id + 1;
-                values[next_id] = (float)(-(double)d.left_grad / ((double)d.left_hess + lambda_l2));
-                values[next_id + 1] =
+                d.left_id = left_id;
+                d.right_id = left_id + 1;
+                values[left_id] = (float)(-(double)d.left_grad / ((double)d.left_hess + lambda_l2));
+                values[left_id + 1] =
                     (float)(-(double)d.right_grad / ((double)d.right_hess + lambda_l2));
-                next_id += 2;
             } else {
                 r.feature = -1;
                 r.threshold = -1;
@@ -342,25 +522,57 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
                 d.split = 0;
                 d.feature = -1;
                 d.threshold = 0;
-                d.score = 0.f;
-                d.left_grad = d.left_hess = d.right_grad = d.right_hess = 0.f;
+                d.score = 0.0f;
+                d.left_grad = d.left_hess = d.right_grad = d.right_hess = 0.0f;
                 d.left_count = d.right_count = 0;
                 d.left_id = d.right_id = -1;
-                values[d.node_id] =
-                    (float)(-(double)nt.grad / ((double)(float)nt.count + lambda_l2));
+                values[d.node_id] = (nt.count == 0)
+                    ? 0.0f
+                    : (float)(-(double)nt.grad / ((double)(float)nt.count + lambda_l2));
             }
             rules[u] = r;
             dd[u] = d;
         }
-        st->tree_size = next_id;
-        if (depth + 1 <= PB_MAX_DEPTH) st->u_active[depth + 1] = slot;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            s_carry[0] += split_total;
+            s_carry[1] += act_total;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        st->tree_size = tree_size0 + 2 * s_carry[0];
+        if (depth + 1 <= PB_MAX_DEPTH) st->u_active[depth + 1] = s_carry[1];
     }
 }
 
 }  // namespace
 
-hipError_t launch_score(const ScoreArgs& a, int grid, hipStream_t s) {
-    hipLaunchKernelGGL(des_score_kernel, dim3(grid), dim3(kBlock), 0, s, a);
+ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes) {
+    ScoreShape sh;
+    // features per workgroup: enough candidates for a full phase-B wavefront at deep levels,
+    // but at least ~512 workgroups in the grid at shallow ones
+    const int max_fts = (T <= kWave) ? std::max(1, kWave / T) : 1;
+    int fts = 1;
+    while (fts * 2 <= max_fts && (int64_t)nodes * ((K + fts * 2 - 1) / (fts * 2)) >= 512) fts *= 2;
+    sh.fts = std::max(1, std::min<int32_t>(fts, K));
+    const int ncand = sh.fts * T;
+    sh.ntiles = (K + sh.fts - 1) / sh.fts;
+    sh.wpt = (ncand + kWave - 1) / kWave;
+    sh.rt = std::max(2, std::min<int32_t>(E + 1, 4096));
+    sh.ec = std::max(1, (kPairs * kBlock) / ncand);
+    sh.lds_bytes = (size_t)sh.rt * 4 + 2 * ((size_t)sh.ec * ncand * 16 + (size_t)sh.ec * 8);
+    return sh;
+}
+
+hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+    if (lds_bytes > 64 * 1024) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&des_score_kernel),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lds_bytes);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(des_score_kernel, dim3(grid), dim3(kBlock), lds_bytes, s, a);
     return hipGetLastError();
 }
 
@@ -377,9 +589,10 @@ hipError_t launch_kcuts(const int32_t* cnt, int32_t E, int32_t U, int32_t K, int
 hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal* ntot,
                          Frontier* st, int32_t depth, int32_t msl, double lambda_l2,
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
-                         pb_decision* dec, float* values, hipStream_t s) {
+                         pb_decision* dec, float* values, pb_candidate* node_best,
+                         hipStream_t s) {
     hipLaunchKernelGGL(decide_kernel, dim3(1), dim3(kBlock), 0, s, cand_w, W, ntot, st, depth,
-                       msl, lambda_l2, cur_ids, next_ids, rules, dec, values);
+                       msl, lambda_l2, cur_ids, next_ids, rules, dec, values, node_best);
     return hipGetLastError();
 }
 
