@@ -31,6 +31,7 @@ struct pb_ctx {
     int64_t lds_budget;
     int32_t force_copies;
     int32_t force_ftile;
+    int32_t force_pairs;
 };
 
 namespace {
@@ -155,7 +156,8 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
             const pb::ScoreShape sh = pb::score_shape(d.max_feats, t, d.num_eras, max_nodes_at(c, dd));
             c->wmax = std::max(c->wmax, sh.ntiles * sh.wpt);
         }
-    c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 64 * 1024);
+    c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 26 * 1024);
+    c->force_pairs = (int32_t)env_int("PB_HIST_PAIRS", 0);
     c->force_copies = (int32_t)env_int("PB_HIST_COPIES", 0);
     c->force_ftile = (int32_t)env_int("PB_HIST_FTILE", 0);
 
@@ -232,27 +234,34 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
         return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: eras above 65535 rows are not supported yet");
 
     const int nb = c->d.max_bins;
-    const int64_t cells = (int64_t)max_nodes * nb;
-    const int64_t budget = std::max<int64_t>(c->lds_budget, 8 * 1024);
-    int clog2 = 4;  // 16 copies: conflict-free 64-bit atomics
+    // Launch shape, from sweeps on MI355X at the 2.4M x 2376 x 5-bin panel: feature pairs share
+    // one atomic on joint bins when nb * nb <= 256; the LDS per workgroup stays near 26 KiB
+    // (occupancy beats copies), the largest feature tile that fits comes first, then as many
+    // histogram copies as fit in half of that.
+    int P = (nb <= 16 && K >= 2) ? 2 : 1;
+    if (c->force_pairs == 1 || (c->force_pairs == 2 && nb <= 16)) P = c->force_pairs;
+    const int64_t cells_group = (int64_t)max_nodes * (P == 2 ? nb * nb : nb);
+    const int64_t cap = std::max<int64_t>(c->lds_budget, 4 * 1024);
+    const int64_t groups_k = (K + P - 1) / P;
+    const int max_groups = (P == 2) ? 8 : 16;  // FT <= 16 (more registers cost occupancy)
+    int64_t groups = max_groups;
+    if (c->force_ftile > 0) groups = std::max<int64_t>(1, c->force_ftile / P);
+    while (groups > 1 && groups * cells_group * 8 > cap) groups /= 2;
+    int64_t need = 1;
+    while (need < groups_k) need *= 2;  // no more groups than the features present need
+    groups = std::min<int64_t>(groups, need);
+    int clog2 = 0;
     if (c->force_copies > 0) {
-        clog2 = 0;
-        while ((1 << (clog2 + 1)) <= c->force_copies && clog2 < 4) ++clog2;
+        while ((1 << (clog2 + 1)) <= c->force_copies && clog2 < 5) ++clog2;
     } else {
-        const int64_t want_feats = std::min<int64_t>(K, 8);
-        while (clog2 > 0 && cells * (int64_t(1) << clog2) * 8 * want_feats > budget) --clog2;
+        while (clog2 < 5 && groups * cells_group * (int64_t(2) << clog2) * 8 <= cap / 2) ++clog2;
     }
-    const int64_t per_feat = cells * (int64_t(1) << clog2) * 8;
-    int64_t ft = budget / per_feat;
-    if (c->force_ftile > 0) ft = c->force_ftile;
-    ft = std::min<int64_t>(ft, std::min<int64_t>(K, 16));
-    if (ft < 1)
+    const int64_t per_group = cells_group * (int64_t(1) << clog2) * 8;
+    const int ftile = (int)groups * P;
+    const size_t lds_bytes = (size_t)(groups * per_group);
+    if (lds_bytes > 160 * 1024)
         return fail(PB_ERR_UNSUPPORTED,
-                    "pb_hist_build: one feature's node x bin histogram exceeds the LDS budget");
-    int ftile = 1;
-    while (ftile * 2 <= ft) ftile *= 2;
-    const size_t lds_bytes = (size_t)(ftile * per_feat);
-    if (lds_bytes > 160 * 1024) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: LDS above 160 KiB");
+                    "pb_hist_build: one feature's node x bin histogram exceeds the 160 KiB LDS");
 
     pb::HistArgs a;
     a.bins = bins;
@@ -275,7 +284,7 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
     const int eras8 = (a.E + 7) / 8 * 8;
     const int64_t grid = (int64_t)eras8 * a.ntiles;
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: grid too large");
-    PB_HIP(pb::launch_hist(a, (int)grid, lds_bytes, (hipStream_t)stream), "hist launch");
+    PB_HIP(pb::launch_hist(a, P, (int)grid, lds_bytes, (hipStream_t)stream), "hist launch");
     return PB_OK;
 }
 

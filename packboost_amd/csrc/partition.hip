@@ -90,10 +90,17 @@ __global__ __launch_bounds__(kBlock) void round_begin_kernel(const float* __rest
         nid[r] = (r < N && root_active) ? (uint16_t)0 : (uint16_t)PB_INACTIVE;
         tnode[r] = 0;
     }
+    // block max, then one atomic per block (non-negative floats order as their bit patterns)
+    __shared__ float s_max[kBlock / kWave];
 #pragma unroll
     for (int m = 1; m < kWave; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
-    if ((threadIdx.x & (kWave - 1)) == 0 && amax > 0.0f)
-        atomicMax(&st->gmax_bits, __float_as_uint(amax));  // non-negative floats order as uints
+    if ((threadIdx.x & (kWave - 1)) == 0) s_max[threadIdx.x / kWave] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = s_max[0];
+        for (int w = 1; w < kBlock / kWave; ++w) b = fmaxf(b, s_max[w]);
+        if (b > 0.0f) atomicMax(&st->gmax_bits, __float_as_uint(b));
+    }
 }
 
 // pack_sum[r] = sum_{t<B} value[leaf(r)] in float32, tree order (booster.py:586-598, the
@@ -137,7 +144,7 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
     hipLaunchKernelGGL(reset_kernel, dim3(1), dim3(64), 0, s, st, root_active, cur_ids);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int grid = grid_for(rows_padded, kBlock, 8192);
+    const int grid = grid_for(rows_padded, kBlock, 1024);
     hipLaunchKernelGGL(round_begin_kernel, dim3(grid), dim3(kBlock), 0, s, preds, y, grad, nid,
                        tnode, N, rows_padded, root_active, st);
     return hipGetLastError();

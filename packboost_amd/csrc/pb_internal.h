@@ -92,7 +92,7 @@ struct ScoreShape {
 ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes);
 
 // Launchers (defined in the .hip files; all return hipError_t of the launch).
-hipError_t launch_hist(const HistArgs& a, int grid, size_t lds_bytes, hipStream_t s);
+hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_kcuts(const int32_t* cnt, int32_t E, int32_t U, int32_t K, int32_t nb,
                         int32_t k, int32_t mass, const Frontier* st, int32_t depth,

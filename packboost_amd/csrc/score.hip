@@ -301,6 +301,248 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     }
 }
 
+// Producer/consumer scorer for T <= 63 thresholds per feature. A workgroup owns up to 63
+// candidates (63 / T features of one node):
+//   wave 0 (consumer): one lane per candidate runs the Welford recurrence over the eras;
+//   waves 1-3 (producers): compute each (candidate, era) record — gain, left grad, left
+//   count, signed weight — for the NEXT chunk of eras into a double-buffered LDS ring,
+//   with the chunk after that already in flight in registers.
+// One barrier per chunk hands a buffer from the producers to the consumer, so the
+// consumer's sequential chain (the part that cannot be parallelised without changing the
+// reference's float order) runs at full wavefront width while its inputs are made alongside.
+constexpr int kPcEras = 24;            // eras per chunk
+constexpr int kPcProducers = kBlock - kWave;
+constexpr int kPcPairs = (kPcEras * kWave + kPcProducers - 1) / kPcProducers;
+
+__global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
+    extern __shared__ unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int u = blockIdx.x / a.ntiles;
+    const int tile = blockIdx.x - u * a.ntiles;
+    const int Ua = a.st->u_active[a.depth];
+    if (u >= Ua) return;
+    const int k0 = tile * a.fts;
+    const int nf = min(a.fts, a.K - k0);
+    if (nf <= 0) return;
+    const int T = a.T;
+    const int nb = a.nb;
+    const int ncand = nf * T;  // <= 63; lane 63 carries the node totals
+    const int RT = a.rt;
+
+    float* recip = reinterpret_cast<float*>(smem);
+    float4* ring = reinterpret_cast<float4*>(recip + ((RT + 3) & ~3));  // [2][kPcEras][64]
+
+    for (int i = tid; i < RT; i += kBlock) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
+
+    const float lam = a.lambda_l2;
+    const float alpha = a.era_alpha;
+    const bool use_dir = a.dir_w != 0.0f;
+    const bool unit_w = !(alpha > 0.0f);
+    const int64_t ustride = (int64_t)a.K * nb;
+    const int64_t estride = (int64_t)a.U * ustride;
+    const int64_t node_off = (int64_t)u * ustride;
+    const int nchunks = (a.E + kPcEras - 1) / kPcEras;
+    const bool consumer = tid < kWave;
+    const int ptid = tid - kWave;
+
+    // Producer slot i of this thread always maps to the same (era-in-chunk, candidate); the
+    // plane offsets are precomputed once, so a chunk costs only loads and the gain math.
+    int slot_el[kPcPairs], slot_c[kPcPairs], slot_thr[kPcPairs];
+    int64_t slot_off[kPcPairs];
+#pragma unroll
+    for (int i = 0; i < kPcPairs; ++i) {
+        const int pidx = ptid + i * kPcProducers;
+        const int el = pidx / ncand;
+        const int c = pidx - el * ncand;
+        const int kk = c / T;
+        const int t = c - kk * T;
+        const int k = k0 + kk;
+        slot_el[i] = (pidx >= 0 && pidx < kPcEras * ncand) ? el : kPcEras;  // kPcEras: unused
+        slot_c[i] = c;
+        slot_thr[i] = a.thr_tab ? a.thr_tab[k * T + t] : t;
+        slot_off[i] = (int64_t)el * estride + node_off + (int64_t)k * nb;
+    }
+
+    PairIn pin[kPcPairs];
+    auto prefetch = [&](int chunk) {
+        const int e0 = chunk * kPcEras;
+        const int ne = min(kPcEras, a.E - e0);
+        const int64_t eoff = (int64_t)e0 * estride;
+#pragma unroll
+        for (int i = 0; i < kPcPairs; ++i) {
+            pin[i].ctot = 0;
+            pin[i].L = 0;
+            pin[i].Gt = 0.0f;
+            pin[i].GL = 0.0f;
+            if (chunk < nchunks && slot_el[i] < ne) {
+                const int64_t off = eoff + slot_off[i];
+                pin[i].ctot = a.cnt[off + nb - 1];
+                pin[i].Gt = a.g[off + nb - 1];
+                pin[i].L = a.cnt[off + slot_thr[i]];
+                pin[i].GL = a.g[off + slot_thr[i]];
+            }
+        }
+    };
+    auto produce = [&](int chunk) {
+        const int e0 = chunk * kPcEras;
+        const int ne = min(kPcEras, a.E - e0);
+        float4* buf = ring + (chunk & 1) * kPcEras * kWave;
+#pragma unroll
+        for (int i = 0; i < kPcPairs; ++i) {
+            if (slot_el[i] < ne) {
+                const int el = slot_el[i];
+                const int c = slot_c[i];
+                const int ctot = pin[i].ctot;
+                float gain = 0.0f, wd = 0.0f, GL = 0.0f;
+                int L = -1;  // -1: the node has no rows in this era (skipped entirely)
+                if (ctot != 0) {
+                    const float Gt = pin[i].Gt;
+                    L = pin[i].L;
+                    GL = pin[i].GL;
+                    const int R = ctot - L;
+                    const float GR = Gt - GL;
+                    const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
+                    const float w = (L > 0 && R > 0) ? wera : 0.0f;
+                    if (w > 0.0f) {
+                        const float dL = (float)L + lam;
+                        const float dR = (float)R + lam;
+                        const float pden = (float)ctot + lam;
+                        const float parent = (pden > 0.0f) ? (0.5f * (Gt * Gt)) / pden : 0.0f;
+                        gain = 0.5f * ((GL * GL) / dL + (GR * GR) / dR) - parent;
+                        bool pos = true;
+                        if (use_dir) {
+                            const float lv = -GL / dL;
+                            const float rv = -GR / dR;
+                            pos = lv > rv;
+                        }
+                        wd = pos ? w : -w;
+                    }
+                }
+                buf[el * kWave + c] = make_float4(gain, GL, __int_as_float(L), wd);
+                if (c == 0) {
+                    // lane 63 pseudo-candidate: its left count / left grad sums become the
+                    // node's row count and float32 era-order grad total
+                    buf[el * kWave + (kWave - 1)] =
+                        make_float4(0.0f, pin[i].Gt, __int_as_float(ctot > 0 ? ctot : -1), 0.0f);
+                }
+            }
+        }
+    };
+
+    float wsum = 0.0f, mean = 0.0f, M2 = 0.0f, agn = 0.0f, agd = 0.0f, lg = 0.0f;
+    int lt = 0;
+    int tc = 0;
+    float tg = 0.0f;
+    const bool owner = tid < ncand;
+    // Consumer: eras in batches of 8 — all record reads first, then the weight-sum chain with
+    // its (independent) factor lookups, then the mean/M2 chain. The factor is 1/n from the
+    // table when every era weight is 1 (bit-identical to w / wsum), else the IEEE division.
+    const bool table = unit_w && a.E < RT;
+    auto consume = [&](int chunk) {
+        const int e0 = chunk * kPcEras;
+        const int ne = min(kPcEras, a.E - e0);
+        const float4* buf = ring + (chunk & 1) * kPcEras * kWave;
+        for (int b0 = 0; b0 < ne; b0 += 8) {
+            float4 rec[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                rec[j] = (b0 + j < ne) ? buf[(b0 + j) * kWave + tid]
+                                       : make_float4(0.0f, 0.0f, __int_as_float(-1), 0.0f);
+            float fac[8], wv[8];
+            bool actv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float w = fabsf(rec[j].w);
+                const bool act = w > 0.0f;  // implies a row-bearing era; wsum + w > 0 then holds
+                const float wn = wsum + w;
+                if (table) {
+                    fac[j] = recip[act ? (int)wn : 0];
+                } else {
+                    fac[j] = w / (act ? wn : 1.0f);
+                }
+                wv[j] = w;
+                actv[j] = act;
+                wsum = act ? wn : wsum;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int L = __float_as_int(rec[j].z);
+                const bool has = L >= 0;
+                lt += has ? L : 0;
+                lg = has ? lg + rec[j].y : lg;
+                const float gain = rec[j].x;
+                const float w = wv[j];
+                const bool act = actv[j];
+                const float delta = gain - mean;
+                const float mean_n = mean + fac[j] * delta;
+                const float M2_n = M2 + (w * delta) * (gain - mean_n);
+                mean = act ? mean_n : mean;
+                M2 = act ? M2_n : M2;
+                if (use_dir) {
+                    agn = act ? agn + w * ((rec[j].w > 0.0f) ? 1.0f : -1.0f) : agn;
+                    agd = act ? agd + w : agd;
+                }
+            }
+        }
+    };
+    if (!consumer) {
+        prefetch(0);
+        produce(0);
+        prefetch(1);
+    }
+    __syncthreads();
+    for (int ch = 0; ch < nchunks; ++ch) {
+        if (consumer) {
+            if (owner || tid == kWave - 1) consume(ch);
+        } else if (ch + 1 < nchunks) {
+            produce(ch + 1);
+            prefetch(ch + 2);
+        }
+        __syncthreads();
+    }
+    if (consumer) {
+        tc = __shfl(lt, kWave - 1);
+        tg = __shfl(lg, kWave - 1);
+    }
+
+    if (consumer) {
+        Cand c;
+        c.lt = lt;
+        c.lg = lg;
+        c.valid = 0;
+        c.score = 0.0f;
+        c.f = -1;
+        c.thr = -1;
+        if (owner) {
+            const int kk = tid / T;
+            const int t = tid - kk * T;
+            const int k = k0 + kk;
+            c.f = a.feats[k];
+            c.thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
+            const int rt = tc - lt;
+            const float ws = (wsum < 1e-12f) ? 1e-12f : wsum;
+            const float var = M2 / ws;
+            const float sd = sqrtf((0.0f < var) ? var : 0.0f);
+            float score = mean - a.lambda_dro * sd;
+            if (use_dir && agd > 0.0f) score = score + a.dir_w * (agn / agd);
+            c.score = score;
+            // a node without rows never splits (the reference skips it, frontier_cpu.cpp:191-193)
+            c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
+            if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
+            if (tile == 0 && tid == 0) {
+                a.ntot[u].count = tc;
+                a.ntot[u].grad = tg;
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const Cand o = shfl_xor_cand(c, m);
+            take_if(better(o, c), o, c);
+        }
+        if (tid == 0) store_cand(a.cand_w + (int64_t)u * a.ntiles + tile, c);
+    }
+}
+
 // K-cut threshold table (frontier_cpu.cpp:35-109, 322-335): per sampled feature, the
 // candidate thresholds are either evenly spaced or placed on the CDF of the feature's bin
 // counts summed over every active node and era. One lane per feature; k <= nb-1 <= 254.
@@ -550,29 +792,41 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
 
 ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes) {
     ScoreShape sh;
-    // features per workgroup: enough candidates for a full phase-B wavefront at deep levels,
-    // but at least ~512 workgroups in the grid at shallow ones
-    const int max_fts = (T <= kWave) ? std::max(1, kWave / T) : 1;
-    int fts = 1;
-    while (fts * 2 <= max_fts && (int64_t)nodes * ((K + fts * 2 - 1) / (fts * 2)) >= 512) fts *= 2;
-    sh.fts = std::max(1, std::min<int32_t>(fts, K));
-    const int ncand = sh.fts * T;
-    sh.ntiles = (K + sh.fts - 1) / sh.fts;
-    sh.wpt = (ncand + kWave - 1) / kWave;
     sh.rt = std::max(2, std::min<int32_t>(E + 1, 4096));
+    if (T < kWave) {
+        // producer/consumer kernel: a 64-lane consumer wavefront per workgroup, 63 candidate
+        // lanes + one lane for the node totals
+        sh.fts = std::max(1, std::min<int32_t>(K, (kWave - 1) / T));
+        sh.ntiles = (K + sh.fts - 1) / sh.fts;
+        sh.wpt = 1;
+        sh.ec = kPcEras;
+        sh.lds_bytes = (size_t)((sh.rt + 3) & ~3) * 4 + 2 * (size_t)kPcEras * kWave * 16;
+        (void)nodes;
+        return sh;
+    }
+    // many thresholds per feature (nb > 65): one feature per workgroup, all threads alternate
+    // between the two phases
+    sh.fts = 1;
+    const int ncand = T;
+    sh.ntiles = K;
+    sh.wpt = (ncand + kWave - 1) / kWave;
     sh.ec = std::max(1, (kPairs * kBlock) / ncand);
     sh.lds_bytes = (size_t)sh.rt * 4 + 2 * ((size_t)sh.ec * ncand * 16 + (size_t)sh.ec * 8);
     return sh;
 }
 
 hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+    const void* fn = (a.T < kWave) ? reinterpret_cast<const void*>(&des_score_pc_kernel)
+                                    : reinterpret_cast<const void*>(&des_score_kernel);
     if (lds_bytes > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&des_score_kernel),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds_bytes);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(des_score_kernel, dim3(grid), dim3(kBlock), lds_bytes, s, a);
+    if (a.T < kWave)
+        hipLaunchKernelGGL(des_score_pc_kernel, dim3(grid), dim3(kBlock), lds_bytes, s, a);
+    else
+        hipLaunchKernelGGL(des_score_kernel, dim3(grid), dim3(kBlock), lds_bytes, s, a);
     return hipGetLastError();
 }
 
