@@ -383,47 +383,49 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
             }
         }
     };
+    // Branch-free per pair (the same float operations as the reference, evaluated for every
+    // pair and selected), so the divide sequences of all pairs interleave.
     auto produce = [&](int chunk) {
         const int e0 = chunk * kPcEras;
         const int ne = min(kPcEras, a.E - e0);
         float4* buf = ring + (chunk & 1) * kPcEras * kWave;
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
-            if (slot_el[i] < ne) {
-                const int el = slot_el[i];
-                const int c = slot_c[i];
-                const int ctot = pin[i].ctot;
-                float gain = 0.0f, wd = 0.0f, GL = 0.0f;
-                int L = -1;  // -1: the node has no rows in this era (skipped entirely)
-                if (ctot != 0) {
-                    const float Gt = pin[i].Gt;
-                    L = pin[i].L;
-                    GL = pin[i].GL;
-                    const int R = ctot - L;
-                    const float GR = Gt - GL;
-                    const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
-                    const float w = (L > 0 && R > 0) ? wera : 0.0f;
-                    if (w > 0.0f) {
-                        const float dL = (float)L + lam;
-                        const float dR = (float)R + lam;
-                        const float pden = (float)ctot + lam;
-                        const float parent = (pden > 0.0f) ? (0.5f * (Gt * Gt)) / pden : 0.0f;
-                        gain = 0.5f * ((GL * GL) / dL + (GR * GR) / dR) - parent;
-                        bool pos = true;
-                        if (use_dir) {
-                            const float lv = -GL / dL;
-                            const float rv = -GR / dR;
-                            pos = lv > rv;
-                        }
-                        wd = pos ? w : -w;
-                    }
-                }
+            const int ctot = pin[i].ctot;
+            const bool has = ctot != 0;
+            const float Gt = pin[i].Gt;
+            const int Lc = pin[i].L;
+            const float GLc = pin[i].GL;
+            const int R = ctot - Lc;
+            const float GR = Gt - GLc;
+            const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
+            const float w = (has && Lc > 0 && R > 0) ? wera : 0.0f;
+            const float dL = (float)Lc + lam;
+            const float dR = (float)R + lam;
+            const float pden = (float)ctot + lam;
+            const float pq = (0.5f * (Gt * Gt)) / pden;
+            const float parent = (pden > 0.0f) ? pq : 0.0f;
+            const float gfull = 0.5f * ((GLc * GLc) / dL + (GR * GR) / dR) - parent;
+            bool pos = true;
+            if (use_dir) {
+                const float lv = -GLc / dL;
+                const float rv = -GR / dR;
+                pos = lv > rv;
+            }
+            const bool act = w > 0.0f;
+            const float gain = act ? gfull : 0.0f;
+            const float wd = act ? (pos ? w : -w) : 0.0f;
+            const int L = has ? Lc : -1;  // -1: the node has no rows in this era (skipped)
+            const float GL = has ? GLc : 0.0f;
+            const int el = slot_el[i];
+            const int c = slot_c[i];
+            if (el < ne) {
                 buf[el * kWave + c] = make_float4(gain, GL, __int_as_float(L), wd);
                 if (c == 0) {
                     // lane 63 pseudo-candidate: its left count / left grad sums become the
                     // node's row count and float32 era-order grad total
                     buf[el * kWave + (kWave - 1)] =
-                        make_float4(0.0f, pin[i].Gt, __int_as_float(ctot > 0 ? ctot : -1), 0.0f);
+                        make_float4(0.0f, Gt, __int_as_float(has ? ctot : -1), 0.0f);
                 }
             }
         }
