@@ -121,6 +121,7 @@ def main() -> int:
     import torch
 
     from packboost_amd import PackBoostConfig
+    from packboost_amd.backends import _hip
     from packboost_amd.engine import DeviceFit, tree_arrays_from_log
 
     c = dict(CONFIGS[args.config])
@@ -137,40 +138,43 @@ def main() -> int:
     rng = torch.Generator().manual_seed(42)
     print(f"[bench] config {args.config}: N={N} F={c['features']} E={c['eras']} K={fit.K} "
           f"warmup={args.warmup} steps={args.steps}", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
-        log = fit.run_round(rng)
+    for log, _, _ in fit.rounds(rng, args.warmup):
         tree_arrays_from_log(log, cfg, N)
     torch.cuda.synchronize()
-    events: list = []
+    # per-phase GPU time from HIP events the library records on the fit's stream
+    _hip.check(fit.lib.pb_profile_enable(fit.ctx, 1), "pb_profile_enable")
     logs = []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        log = fit.run_round(rng, events)
+    for log, _, _ in fit.rounds(rng, args.steps):
         tree_arrays_from_log(log, cfg, N)
         logs.append(log)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
+    D = fit.D
+    prof_ms = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.float64)
+    prof_n = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.int64)
+    _hip.check(fit.lib.pb_profile_read(fit.ctx, prof_ms.ctypes.data, prof_n.ctypes.data),
+               "pb_profile_read")
+    prof_ms = prof_ms.reshape(4, -1)[:, :D]
+    prof_n = prof_n.reshape(4, -1)[:, :D]
 
     # histogram roofline: algorithmic bytes per launch = rows of active nodes x K bin bytes
     # + rows x 6 (grad f32 + node id u16) + written planes U x E x K x nb x 8
     K, E, nb = fit.K, fit.E, fit.nb
-    phase_ms: dict[str, float] = {}
+    phase_ms = {name: float(prof_ms[i].sum()) for i, name in
+                enumerate(("hist", "score", "decide", "partition"))}
     hist_bytes = 0.0
-    hist_ms = 0.0
-    n_hist = 0
-    for (phase, d, a, b), log in zip(events, [l for l in logs for _ in range(4 * fit.D)]):
-        ms = a.elapsed_time(b)
-        phase_ms[phase] = phase_ms.get(phase, 0.0) + ms
-        if phase == "hist":
+    for log in logs:
+        for d in range(D):
             u = int(log.u_active[d])
             if u == 0:
                 continue
             base = (1 << d) - 1
             rows = int(log.decisions[base: base + u]["node_count"].astype(np.int64).sum())
             hist_bytes += rows * K + rows * 6 + u * E * K * nb * 8
-            hist_ms += ms
-            n_hist += 1
+    hist_ms = float(prof_ms[0].sum())
+    n_hist = int(prof_n[0].sum())
     achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     rounds_per_s = args.steps / elapsed
     out = {
@@ -205,6 +209,8 @@ def main() -> int:
             "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
         },
         "phase_ms_per_round": {k: round(v / args.steps, 4) for k, v in phase_ms.items()},
+        "hist_ms_per_depth": [round(float(prof_ms[0, d]) / max(1, int(prof_n[0, d])), 4)
+                              for d in range(D)],
         "cpu_baseline": None,
     }
     fit.close()

@@ -174,6 +174,48 @@ int pb_partition(pb_ctx* ctx, const uint8_t* bins_dev, int32_t depth, uint16_t* 
 int pb_round_end(pb_ctx* ctx, const uint16_t* tnode_dev, const float* values_dev,
                  int32_t pack_size, float learning_rate, float* preds_dev, void* stream);
 
+/* Per-round summary written on the device at the end of pb_grow_round, so one small copy
+ * gives the host everything it needs to rebuild the round's trees. */
+typedef struct {
+    int32_t u_active[PB_MAX_DEPTH + 1];  /* active unique nodes per depth */
+    int32_t tree_size;                   /* nodes in each tree of the round */
+    int32_t reserved[6];
+} pb_round_header;  /* 96 bytes */
+
+/* Device buffers of one fit, bound once for pb_grow_round. All row arrays hold rows_padded
+ * entries; hist planes hold pb_hist_plane_elems(ctx, pb_max_nodes(ctx, D-1)) entries. */
+typedef struct {
+    const uint8_t* bins_dev;     /* [F][ld] column-major */
+    const float* y_dev;
+    float* preds_dev;
+    float* grad_dev;
+    uint16_t* nid_dev;
+    uint16_t* tnode_dev;
+    int32_t* hist_cnt_dev;
+    float* hist_grad_dev;
+    float* values_dev;           /* [2^(D+1)] */
+    int32_t pack_size;
+    float learning_rate;
+    pb_split_params params;
+} pb_fit_buffers;
+
+/* One whole boosting round (booster.py:494-599) as a single asynchronous enqueue:
+ * pb_round_begin, then for every depth pb_hist_build -> pb_des_score -> pb_decide ->
+ * pb_partition, then pb_round_end. feats_dev: int32 [D][K] feature subsets (the host draws
+ * them, booster.py:519, 787-792); decisions_dev: pb_decision [2^D - 1]; header_dev: the
+ * round's pb_round_header. Depths whose frontier is empty run no work. */
+int pb_grow_round(pb_ctx* ctx, const pb_fit_buffers* buffers, const int32_t* feats_dev, int32_t K,
+                  pb_decision* decisions_dev, pb_round_header* header_dev, void* stream);
+
+/* GPU time of every phase of pb_grow_round, from HIP events recorded on the launch stream
+ * around each depth's hist / score / decide / partition launches (the device-side analogue of
+ * the per-depth hist_ms / scan_ms / score_ms / partition_ms instrumentation,
+ * booster.py:220-270). pb_profile_read waits for the recorded rounds, fills
+ * ms[phase * PB_MAX_DEPTH + depth] (phase 0 hist, 1 score, 2 decide, 3 partition) and the
+ * matching launch counts, and clears them. */
+int pb_profile_enable(pb_ctx* ctx, int32_t enable);
+int pb_profile_read(pb_ctx* ctx, double* ms, int64_t* launches);
+
 /* Teacher-forces the frontier of `depth`: `num_active` active slots whose TreeBuilder ids are
  * node_ids_host (NULL: 0..num_active-1) and a tree size of `tree_size`. Lets a caller run one
  * depth on its own row -> slot assignment (nid); the reference takes that assignment as the

@@ -25,7 +25,8 @@ EXPORTED_SYMBOLS = (
     "pb_last_error", "pb_version", "pb_device_available",
     "pb_ctx_create", "pb_ctx_destroy", "pb_hist_plane_elems", "pb_max_nodes",
     "pb_era_offsets_dev", "pb_round_begin", "pb_hist_build", "pb_des_score", "pb_decide",
-    "pb_partition", "pb_round_end", "pb_frontier_set", "pb_frontier_counts", "pb_predict_pack",
+    "pb_partition", "pb_round_end", "pb_grow_round", "pb_profile_enable",
+    "pb_profile_read", "pb_frontier_set", "pb_frontier_counts", "pb_predict_pack",
     "pb_predict_forest", "pb_predict_bins",
 )
 
@@ -51,6 +52,19 @@ class PbSplitParams(ctypes.Structure):
     ]
 
 
+class PbFitBuffers(ctypes.Structure):
+    _fields_ = [
+        ("bins_dev", ctypes.c_void_p), ("y_dev", ctypes.c_void_p), ("preds_dev", ctypes.c_void_p),
+        ("grad_dev", ctypes.c_void_p), ("nid_dev", ctypes.c_void_p), ("tnode_dev", ctypes.c_void_p),
+        ("hist_cnt_dev", ctypes.c_void_p), ("hist_grad_dev", ctypes.c_void_p),
+        ("values_dev", ctypes.c_void_p), ("pack_size", ctypes.c_int32),
+        ("learning_rate", ctypes.c_float), ("params", PbSplitParams),
+    ]
+
+
+HEADER_DTYPE = np.dtype([("u_active", "<i4", (PB_MAX_DEPTH + 1,)), ("tree_size", "<i4"),
+                         ("reserved", "<i4", (6,))])
+
 DECISION_DTYPE = np.dtype([
     ("node_id", "<i4"), ("split", "<i4"), ("feature", "<i4"), ("threshold", "<i4"),
     ("score", "<f4"), ("left_grad", "<f4"), ("left_hess", "<f4"), ("right_grad", "<f4"),
@@ -62,6 +76,7 @@ CANDIDATE_DTYPE = np.dtype([
     ("threshold", "<i4"), ("valid", "<i4"), ("reserved", "<i4", (2,)),
 ])
 assert DECISION_DTYPE.itemsize == 64 and CANDIDATE_DTYPE.itemsize == 32
+assert HEADER_DTYPE.itemsize == 96
 
 _VP = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -84,6 +99,9 @@ _SIGNATURES = {
     "pb_decide": (ctypes.c_int, [_VP, _I32, _I32, ctypes.POINTER(PbSplitParams), _VP, _VP, _VP]),
     "pb_partition": (ctypes.c_int, [_VP, _VP, _I32, _VP, _VP, _VP]),
     "pb_round_end": (ctypes.c_int, [_VP, _VP, _VP, _I32, _F32, _VP, _VP]),
+    "pb_grow_round": (ctypes.c_int, [_VP, ctypes.POINTER(PbFitBuffers), _VP, _I32, _VP, _VP, _VP]),
+    "pb_profile_enable": (ctypes.c_int, [_VP, _I32]),
+    "pb_profile_read": (ctypes.c_int, [_VP, _VP, _VP]),
     "pb_frontier_set": (ctypes.c_int, [_VP, _I32, _I32, _VP, _I32, _VP]),
     "pb_frontier_counts": (ctypes.c_int, [_VP, _VP, _VP, _VP]),
     "pb_predict_pack": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP,

@@ -237,10 +237,13 @@ class PackBoost:
         era_ids_dev = torch.from_numpy(np.repeat(np.arange(E), np.diff(offsets))).to(device)
         eval_states = self._prepare_eval(eval_sets, device)
         eval_every = _eval_every()
+        # metrics and eval predictions run on a side stream so that the next round, already
+        # enqueued on the fit's stream, keeps the GPU busy while the host builds trees
+        side = torch.cuda.Stream(device)
         try:
-            for round_idx in range(num_rounds):
-                t0 = perf_counter()
-                log = fitter.run_round(self._rng)
+            t0 = perf_counter()
+            for round_idx, (log, preds_after, ready) in enumerate(
+                    fitter.rounds(self._rng, num_rounds)):
                 arrs = tree_arrays_from_log(log, cfg, N)
                 self._rounds.append(arrs)
                 self._trees_cache = None
@@ -253,19 +256,24 @@ class PackBoost:
                     self._depth_logs.append(dl)
                     if self._logger.isEnabledFor(logging.INFO):
                         self._logger.info(json.dumps(dl))
-                if eval_states and eval_every > 0 and (
-                        (round_idx + 1) % eval_every == 0 or round_idx + 1 == num_rounds):
-                    self._update_eval(eval_states)
-                round_time = perf_counter() - t0
+                with torch.cuda.stream(side):
+                    side.wait_event(ready)
+                    if eval_states and eval_every > 0 and (
+                            (round_idx + 1) % eval_every == 0 or round_idx + 1 == num_rounds):
+                        self._update_eval(eval_states)
+                    train_corr = _era_corr_device(era_ids_dev, fitter.y[:N], preds_after[:N], E)
+                    eval_corr = {f"{st['name']}_corr": _era_corr_device(
+                        st["era_ids"], st["y"], st["preds"], st["num_eras"]) for st in eval_states}
+                t1 = perf_counter()
+                round_time = t1 - t0
+                t0 = t1
                 metrics = {
                     "round": round_idx + 1,
-                    "train_corr": _era_corr_device(era_ids_dev, fitter.y[:N], fitter.preds[:N], E),
+                    "train_corr": train_corr,
                     "trees_per_second": (cfg.pack_size / round_time) if round_time > 0 else float("inf"),
                     "round_seconds": round_time,
                 }
-                for st in eval_states:
-                    metrics[f"{st['name']}_corr"] = _era_corr_device(
-                        st["era_ids"], st["y"], st["preds"], st["num_eras"])
+                metrics.update(eval_corr)
                 self._round_metrics.append(metrics)
                 if round_callback is not None:
                     round_callback(round_idx + 1, metrics)

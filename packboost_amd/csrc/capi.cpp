@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
+#include <utility>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -32,6 +34,11 @@ struct pb_ctx {
     int32_t force_copies;
     int32_t force_ftile;
     int32_t force_pairs;
+    // phase timing of pb_grow_round (pb_profile_enable): per depth, 5 events bracket the
+    // hist / score / decide / partition launches on the caller's stream
+    bool profile;
+    std::vector<hipEvent_t> ev_free;
+    std::vector<std::pair<int32_t, std::array<hipEvent_t, 5>>> ev_pending;
 };
 
 namespace {
@@ -96,6 +103,9 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->ids[0]);
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
+    for (auto& p : c->ev_pending)
+        for (hipEvent_t e : p.second) c->ev_free.push_back(e);
+    for (hipEvent_t e : c->ev_free) (void)hipEventDestroy(e);
     delete c;
 }
 
@@ -375,6 +385,89 @@ int pb_round_end(pb_ctx* c, const uint16_t* tnode, const float* values, int32_t 
                                 (hipStream_t)stream),
            "round_end launch");
     return PB_OK;
+}
+
+int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int32_t K,
+                  pb_decision* dec, pb_round_header* header, void* stream) {
+    if (!c || !b || !feats || !dec || !header) return fail(PB_ERR_INVALID, "pb_grow_round: null argument");
+    if (!b->bins_dev || !b->y_dev || !b->preds_dev || !b->grad_dev || !b->nid_dev || !b->tnode_dev ||
+        !b->hist_cnt_dev || !b->hist_grad_dev || !b->values_dev)
+        return fail(PB_ERR_INVALID, "pb_grow_round: null buffer");
+    int rc = pb_round_begin(c, b->preds_dev, b->y_dev, b->grad_dev, b->nid_dev, b->tnode_dev, stream);
+    if (rc) return rc;
+    for (int d = 0; d < c->d.max_depth; ++d) {
+        const int32_t m = max_nodes_at(c, d);
+        const int32_t* f = feats + (int64_t)d * K;
+        std::array<hipEvent_t, 5> ev{};
+        const bool prof = c->profile;
+        if (prof) {
+            for (auto& e : ev) {
+                if (!c->ev_free.empty()) {
+                    e = c->ev_free.back();
+                    c->ev_free.pop_back();
+                } else {
+                    PB_HIP(hipEventCreate(&e), "profile event create");
+                }
+            }
+            c->ev_pending.emplace_back(d, ev);
+        }
+        auto mark = [&](int i) -> int {
+            if (prof) PB_HIP(hipEventRecord(ev[i], (hipStream_t)stream), "profile event record");
+            return PB_OK;
+        };
+        if ((rc = mark(0))) return rc;
+        if ((rc = pb_hist_build(c, b->bins_dev, b->grad_dev, b->nid_dev, f, K, d, m, b->hist_cnt_dev,
+                                b->hist_grad_dev, stream)))
+            return rc;
+        if ((rc = mark(1))) return rc;
+        if ((rc = pb_des_score(c, b->hist_cnt_dev, b->hist_grad_dev, f, K, d, m, &b->params, nullptr,
+                               stream)))
+            return rc;
+        if ((rc = mark(2))) return rc;
+        if ((rc = pb_decide(c, d, m, &b->params, dec, b->values_dev, stream))) return rc;
+        if ((rc = mark(3))) return rc;
+        if ((rc = pb_partition(c, b->bins_dev, d, b->nid_dev, b->tnode_dev, stream))) return rc;
+        if ((rc = mark(4))) return rc;
+    }
+    PB_HIP(pb::launch_round_header(c->st, header, (hipStream_t)stream), "round header launch");
+    return pb_round_end(c, b->tnode_dev, b->values_dev, b->pack_size, b->learning_rate, b->preds_dev,
+                        stream);
+}
+
+int pb_profile_enable(pb_ctx* c, int32_t enable) {
+    if (!c) return fail(PB_ERR_INVALID, "pb_profile_enable: null context");
+    c->profile = enable != 0;
+    return PB_OK;
+}
+
+int pb_profile_read(pb_ctx* c, double* ms, int64_t* launches) {
+    if (!c || !ms || !launches) return fail(PB_ERR_INVALID, "pb_profile_read: null argument");
+    for (int i = 0; i < 4 * PB_MAX_DEPTH; ++i) {
+        ms[i] = 0.0;
+        launches[i] = 0;
+    }
+    int rc = PB_OK;
+    for (auto& p : c->ev_pending) {
+        const int d = p.first;
+        auto& ev = p.second;
+        if (rc == PB_OK) {
+            hipError_t e = hipEventSynchronize(ev[4]);
+            if (e != hipSuccess) rc = hip_fail(e, "profile event sync");
+        }
+        for (int ph = 0; ph < 4 && rc == PB_OK; ++ph) {
+            float t = 0.f;
+            hipError_t e = hipEventElapsedTime(&t, ev[ph], ev[ph + 1]);
+            if (e != hipSuccess) {
+                rc = hip_fail(e, "profile elapsed time");
+                break;
+            }
+            ms[ph * PB_MAX_DEPTH + d] += t;
+            launches[ph * PB_MAX_DEPTH + d] += 1;
+        }
+        for (hipEvent_t e : ev) c->ev_free.push_back(e);
+    }
+    c->ev_pending.clear();
+    return rc;
 }
 
 int pb_frontier_set(pb_ctx* c, int32_t depth, int32_t num_active, const int32_t* node_ids_host,

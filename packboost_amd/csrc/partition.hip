@@ -120,6 +120,13 @@ __global__ __launch_bounds__(kBlock) void round_end_kernel(const uint16_t* __res
     }
 }
 
+__global__ void round_header_kernel(const Frontier* st, pb_round_header* h) {
+    const int i = threadIdx.x;
+    if (i <= PB_MAX_DEPTH) h->u_active[i] = st->u_active[i];
+    if (i == 0) h->tree_size = st->tree_size;
+    if (i < 6) h->reserved[i] = 0;
+}
+
 int grid_for(int64_t work, int per_block, int cap) {
     int64_t g = (work + per_block - 1) / per_block;
     if (g < 1) g = 1;
@@ -147,6 +154,11 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
     const int grid = grid_for(rows_padded, kBlock, 1024);
     hipLaunchKernelGGL(round_begin_kernel, dim3(grid), dim3(kBlock), 0, s, preds, y, grad, nid,
                        tnode, N, rows_padded, root_active, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s) {
+    hipLaunchKernelGGL(round_header_kernel, dim3(1), dim3(64), 0, s, st, h);
     return hipGetLastError();
 }
 

@@ -108,6 +108,7 @@ hipError_t launch_partition(const uint8_t* bins, int64_t ld, int64_t rows_padded
 hipError_t launch_round_begin(const float* preds, const float* y, float* grad, uint16_t* nid,
                               uint16_t* tnode, int64_t N, int64_t rows_padded, int32_t root_active,
                               Frontier* st, int32_t* cur_ids, hipStream_t s);
+hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s);
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
                             float lr, float* preds, int64_t N, hipStream_t s);
 hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,

@@ -9,11 +9,16 @@ sequence of asynchronous kernel launches on the caller's stream:
         hist_build -> des_score -> decide -> partition
     round_end                           preds += lr * pack_sum
 
-The only host round trip per round is the final copy of the decision log (a few KB), from
-which the host rebuilds the round's trees. Feature subsets are drawn on the host from the
-fit's CPU generator before the round; the generator is rewound afterwards to the state the
-reference would have after its actual number of draws (it draws only while a depth still
-has active nodes, booster.py:516-519).
+A whole round is one C-ABI call (pb_grow_round). The only host round trip per round is the
+copy of the decision log (a few KB) from which the host rebuilds the round's trees. Feature
+subsets are drawn on the host from the fit's CPU generator before the round; the generator
+is rewound afterwards to the state the reference would have after its actual number of draws
+(it draws only while a depth still has active nodes, booster.py:516-519).
+
+`DeviceFit.rounds` pipelines the host and the GPU: round r+1 is enqueued before round r's log
+is read, on the assumption that round r drew all D subsets. Its predictions are snapshotted
+first; in the rare case that round r stopped early, the snapshot is restored and round r+1
+is enqueued again with the generator rewound, so results never depend on the speculation.
 """
 
 from __future__ import annotations
@@ -125,6 +130,35 @@ class DeviceFit:
         self.feats_host = torch.zeros((self.D, self.K), dtype=torch.int32).pin_memory()
         self.root_grad_dev = torch.zeros(1, dtype=torch.float32, device=dev)
 
+        # pb_grow_round state: two slots (round parity) of feature subsets and of the round's
+        # log = [decisions (2^D - 1) x 64 B | header 96 B], device and pinned host copies
+        self._n_dec = n_dec
+        log_bytes = n_dec * _hip.DECISION_DTYPE.itemsize + _hip.HEADER_DTYPE.itemsize
+        self._log_dev = [torch.zeros(log_bytes, dtype=torch.uint8, device=dev) for _ in range(2)]
+        self._log_host = [torch.zeros(log_bytes, dtype=torch.uint8).pin_memory() for _ in range(2)]
+        self._feats_slot_dev = [torch.zeros((self.D, self.K), dtype=torch.int32, device=dev)
+                                for _ in range(2)]
+        self._feats_slot_host = [torch.zeros((self.D, self.K), dtype=torch.int32).pin_memory()
+                                 for _ in range(2)]
+        self._log_ready = [None, None]
+        self.preds_snap = torch.zeros_like(self.preds)
+        b = _hip.PbFitBuffers()
+        b.bins_dev = self.bins.data_ptr()
+        b.y_dev = self.y.data_ptr()
+        b.preds_dev = self.preds.data_ptr()
+        b.grad_dev = self.grad.data_ptr()
+        b.nid_dev = self.nid.data_ptr()
+        b.tnode_dev = self.tnode.data_ptr()
+        b.hist_cnt_dev = self.hist_cnt.data_ptr()
+        b.hist_grad_dev = self.hist_g.data_ptr()
+        b.values_dev = self.values.data_ptr()
+        b.pack_size = self.B
+        b.learning_rate = self.lr
+        b.params = self.params
+        self._bufs = b
+        # a root below 2*min_samples_leaf never splits: the per-phase path sets its value
+        self._root_splittable = self.N >= 2 * int(cfg.min_samples_leaf)
+
     # ------------------------------------------------------------------ lifecycle
     def close(self) -> None:
         if getattr(self, "ctx", None) is not None and self.ctx.value:
@@ -195,6 +229,86 @@ class DeviceFit:
         chk(lib.pb_round_end(ctx, self.tnode.data_ptr(), self.values.data_ptr(), self.B,
                              ctypes.c_float(self.lr), self.preds.data_ptr(), s), "pb_round_end")
 
+    def enqueue_grow(self, subsets: np.ndarray, slot: int) -> None:
+        """Enqueues one full round as a single pb_grow_round call plus the copy of its log
+        into host slot `slot` (no host synchronisation)."""
+        fh = self._feats_slot_host[slot]
+        fh.numpy()[...] = subsets
+        log_dev = self._log_dev[slot]
+        dec_ptr = log_dev.data_ptr()
+        hdr_ptr = dec_ptr + self._n_dec * _hip.DECISION_DTYPE.itemsize
+        with torch.cuda.stream(self.stream):
+            self._feats_slot_dev[slot].copy_(fh, non_blocking=True)
+            _hip.check(self.lib.pb_grow_round(self.ctx, ctypes.byref(self._bufs),
+                                              self._feats_slot_dev[slot].data_ptr(), self.K,
+                                              dec_ptr, hdr_ptr, _hip.stream_ptr(self.stream)),
+                       "pb_grow_round")
+            self._log_host[slot].copy_(log_dev, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+        self._log_ready[slot] = ev
+
+    def read_slot(self, slot: int) -> RoundLog:
+        """Waits for the log copy of `slot` (not for later work on the stream) and parses it."""
+        self._log_ready[slot].synchronize()
+        raw = self._log_host[slot].numpy()
+        nd = self._n_dec * _hip.DECISION_DTYPE.itemsize
+        dec = np.frombuffer(raw[:nd].tobytes(), dtype=_hip.DECISION_DTYPE)
+        hdr = np.frombuffer(raw[nd:].tobytes(), dtype=_hip.HEADER_DTYPE)[0]
+        u = np.asarray(hdr["u_active"], dtype=np.int32)
+        drawn = int(np.count_nonzero(u[: self.D] > 0))
+        return RoundLog(u_active=u[: self.D + 1].copy(), tree_size=int(hdr["tree_size"]),
+                        decisions=dec, root_grad=float(dec[0]["node_grad"]), depths_drawn=drawn)
+
+    def rounds(self, rng: torch.Generator, num_rounds: int):
+        """Runs `num_rounds` rounds with the host one round ahead of the GPU.
+
+        Yields (RoundLog, preds_after, ready) per round in order. `preds_after` holds the
+        predictions after that round until the consumer resumes the generator (the GPU may
+        already be running the next round on `preds`); `ready` is an event on the fit's
+        stream after which `preds_after` is valid, so a side stream can read it without
+        waiting for the next round.
+        """
+        def now() -> torch.cuda.Event:
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+            return ev
+
+        if not self._root_splittable:
+            for _ in range(num_rounds):
+                log = self.run_round(rng)
+                yield log, self.preds, now()
+            return
+        if num_rounds <= 0:
+            return
+        subs, states = self.draw_subsets(rng)
+        self.enqueue_grow(subs, 0)
+        for r in range(num_rounds):
+            slot = r & 1
+            ahead = r + 1 < num_rounds
+            if ahead:
+                with torch.cuda.stream(self.stream):
+                    self.preds_snap.copy_(self.preds)
+                ready = now()
+                subs_n, states_n = self.draw_subsets(rng)
+                self.enqueue_grow(subs_n, slot ^ 1)
+            log = self.read_slot(slot)
+            if log.depths_drawn < self.D:
+                # round r drew fewer subsets than assumed: rewind and redo round r + 1
+                rng.set_state(states[log.depths_drawn])
+                if ahead:
+                    self.stream.synchronize()
+                    with torch.cuda.stream(self.stream):
+                        self.preds.copy_(self.preds_snap)
+                    subs_n, states_n = self.draw_subsets(rng)
+                    self.enqueue_grow(subs_n, slot ^ 1)
+            if ahead:
+                yield log, self.preds_snap, ready
+            else:
+                yield log, self.preds, now()
+            if ahead:
+                states = states_n
+
     def _root_value_if_inactive(self) -> None:
         # Root below capacity (N < 2*msl): the tree is a single leaf -G/(N+lambda)
         # (booster.py:503-513). The decision kernels never run for it.
@@ -224,9 +338,15 @@ class DeviceFit:
                         root_grad=root_grad, depths_drawn=drawn)
 
     def run_round(self, rng: torch.Generator, events: list | None = None) -> RoundLog:
+        """One round, synchronously. With `events` (or a root that cannot split) the round
+        runs as per-phase C-ABI calls; otherwise as one pb_grow_round call."""
         subs, states = self.draw_subsets(rng)
-        self.enqueue_round(subs, events)
-        log = self.read_round()
+        if events is None and self._root_splittable:
+            self.enqueue_grow(subs, 0)
+            log = self.read_slot(0)
+        else:
+            self.enqueue_round(subs, events)
+            log = self.read_round()
         if log.depths_drawn < self.D:
             rng.set_state(states[log.depths_drawn])
         return log

@@ -105,3 +105,26 @@ def test_unsorted_eras_and_no_eras(hip, oracle_mod):
         _compare_rounds(model._rounds, ref.rounds)
         pred = model.predict(X)
         np.testing.assert_allclose(pred, oracle_mod.predict(ref.rounds, 2, 0.1, bins), atol=1e-5)
+
+
+@pytest.mark.parametrize("msl", [150, 2000], ids=["early_stop", "root_leaf"])
+def test_early_stopping_rounds(hip, oracle_mod, msl):
+    """Trees that stop before max_depth make the reference draw fewer feature subsets
+    (booster.py:516-519): the pipelined round loop must rewind its generator and redo the
+    round it enqueued ahead. msl=2000 > N/2 leaves every tree a single root leaf."""
+    from packboost_amd import PackBoost, PackBoostConfig
+    from packboost_amd.data import preprocess_features
+
+    X, y, era = config1_data(seed=9, n=3000, f=16, eras=5)
+    cfg_kw = dict(pack_size=4, max_depth=6, learning_rate=0.1, min_samples_leaf=msl, max_bins=31,
+                  lambda_dro=0.2, layer_feature_fraction=0.5, random_state=23)
+    print(f"[early stop] msl={msl}", flush=True)
+    cfg = PackBoostConfig(**cfg_kw)
+    model = PackBoost(cfg).fit(X, y, era, num_rounds=6)
+    bins = preprocess_features(X, cfg.max_bins).bins
+    ref = oracle_mod.fit(bins, y, era.astype(np.int64), num_rounds=6, **cfg_kw)
+    _compare_rounds(model._rounds, ref.rounds)
+    np.testing.assert_allclose(model._train_preds.cpu().numpy(), ref.preds, atol=1e-5, rtol=0)
+    if msl == 150:
+        assert max(int(np.count_nonzero(~np.asarray(r["is_leaf"]))) for r in ref.rounds) > 0
+        assert all(int(np.count_nonzero(~np.asarray(r["is_leaf"]))) < 63 for r in ref.rounds)
