@@ -103,6 +103,21 @@ def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None
     }
 
 
+def copy_probe(mib: int) -> int:
+    """Reads and writes exactly `mib` MiB per launch: the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters to HBM bytes."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_mib": mib, "launches": 5}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,7 +127,11 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=0, help="override row count (quick runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (counter calibration)")
     args = ap.parse_args()
+    if args.copy_probe:
+        return copy_probe(args.copy_probe)
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(see DESIGN.md for how the path would shard).", file=sys.stderr)

@@ -34,6 +34,7 @@ struct pb_ctx {
     int32_t force_copies;
     int32_t force_ftile;
     int32_t force_pairs;
+    int32_t score_wgs;  // workgroups the producer/consumer scorer aims for
     // phase timing of pb_grow_round (pb_profile_enable): per depth, 5 events bracket the
     // hist / score / decide / partition launches on the caller's stream
     bool profile;
@@ -152,7 +153,6 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     }
 
     pb_ctx* c = new pb_ctx();
-    std::memset(c, 0, sizeof(*c));
     c->d = d;
     c->rows_padded = (d.num_rows + 15) / 16 * 16;
     c->max_era_rows = max_era;
@@ -160,10 +160,12 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     c->umax = 1;
     for (int dd = 0; dd < d.max_depth; ++dd) c->umax = std::max(c->umax, max_nodes_at(c, dd));
     const int tmax = std::max(1, d.max_bins - 1);
+    c->score_wgs = (int32_t)env_int("PB_SCORE_WGS", 768);
     c->wmax = 1;
     for (int t = 1; t <= tmax; ++t)
         for (int dd = 0; dd < d.max_depth; ++dd) {
-            const pb::ScoreShape sh = pb::score_shape(d.max_feats, t, d.num_eras, max_nodes_at(c, dd));
+            const pb::ScoreShape sh = pb::score_shape(d.max_feats, t, d.num_eras, max_nodes_at(c, dd),
+                                                        c->score_wgs);
             c->wmax = std::max(c->wmax, sh.ntiles * sh.wpt);
         }
     c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 26 * 1024);
@@ -318,7 +320,8 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
                "kcuts launch");
         thr_tab = c->thr_tab;
     }
-    const pb::ScoreShape sh = pb::score_shape(K, T, c->d.num_eras, max_nodes_at(c, depth));
+    const pb::ScoreShape sh = pb::score_shape(K, T, c->d.num_eras, max_nodes_at(c, depth),
+                                                    c->score_wgs);
     const int64_t grid = (int64_t)sh.ntiles * max_nodes_at(c, depth);
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_des_score: grid too large");
     if (sh.ntiles * sh.wpt > c->wmax) return fail(PB_ERR_INVALID, "pb_des_score: candidate buffer too small");

@@ -89,7 +89,7 @@ struct ScoreShape {
     int32_t fts, ntiles, ec, wpt, rt;
     size_t lds_bytes;
 };
-ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes);
+ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t target_wgs);
 
 // Launchers (defined in the .hip files; all return hipError_t of the launch).
 hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s);

@@ -21,6 +21,8 @@
 // threshold (frontier_cpu.cpp:415-426).
 #include <algorithm>
 
+#include <type_traits>
+
 #include "pb_internal.h"
 
 namespace pb {
@@ -347,6 +349,9 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
 
     // Producer slot i of this thread always maps to the same (era-in-chunk, candidate); the
     // plane offsets are precomputed once, so a chunk costs only loads and the gain math.
+    // Only the first `np` slots can hold a record (workgroup-uniform): fewer candidates per
+    // workgroup mean fewer pairs per producer lane.
+    const int np = (kPcEras * ncand + kPcProducers - 1) / kPcProducers;
     int slot_el[kPcPairs], slot_c[kPcPairs], slot_thr[kPcPairs];
     int64_t slot_off[kPcPairs];
 #pragma unroll
@@ -370,6 +375,7 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
         const int64_t eoff = (int64_t)e0 * estride;
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
+            if (i >= np) break;
             pin[i].ctot = 0;
             pin[i].L = 0;
             pin[i].Gt = 0.0f;
@@ -391,6 +397,7 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
         float4* buf = ring + (chunk & 1) * kPcEras * kWave;
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
+            if (i >= np) break;
             const int ctot = pin[i].ctot;
             const bool has = ctot != 0;
             const float Gt = pin[i].Gt;
@@ -415,17 +422,23 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
             const bool act = w > 0.0f;
             const float gain = act ? gfull : 0.0f;
             const float wd = act ? (pos ? w : -w) : 0.0f;
-            const int L = has ? Lc : -1;  // -1: the node has no rows in this era (skipped)
+            // An era without rows of the node contributes L = 0, GL = +0 and weight 0, which
+            // leaves every consumer sum bit-unchanged: the reference skips such eras
+            // (frontier_cpu.cpp:367-369), and x + (+0) == x for every x the sums can hold
+            // (they start at +0 and never become -0).
+            const int L = has ? Lc : 0;
             const float GL = has ? GLc : 0.0f;
             const int el = slot_el[i];
             const int c = slot_c[i];
-            if (el < ne) {
+            // eras past the end of the last chunk get neutral records (no rows, zero
+            // weight: pin is zero there), so the consumer reads whole batches unconditionally
+            if (el < kPcEras) {
                 buf[el * kWave + c] = make_float4(gain, GL, __int_as_float(L), wd);
                 if (c == 0) {
                     // lane 63 pseudo-candidate: its left count / left grad sums become the
                     // node's row count and float32 era-order grad total
                     buf[el * kWave + (kWave - 1)] =
-                        make_float4(0.0f, Gt, __int_as_float(has ? ctot : -1), 0.0f);
+                        make_float4(0.0f, has ? Gt : 0.0f, __int_as_float(ctot), 0.0f);
                 }
             }
         }
@@ -433,54 +446,59 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
 
     float wsum = 0.0f, mean = 0.0f, M2 = 0.0f, agn = 0.0f, agd = 0.0f, lg = 0.0f;
     int lt = 0;
+    int nact = 0;  // active eras so far (unit weights: wsum == nact exactly)
     int tc = 0;
     float tg = 0.0f;
     const bool owner = tid < ncand;
     // Consumer: eras in batches of 8 — all record reads first, then the weight-sum chain with
-    // its (independent) factor lookups, then the mean/M2 chain. The factor is 1/n from the
-    // table when every era weight is 1 (bit-identical to w / wsum), else the IEEE division.
+    // its (independent) factor lookups, then the mean/M2 chain. With unit era weights
+    // (TABLE) the factor w / wsum is 1/n, read from the table of IEEE 1/n (bit-identical),
+    // and w * delta == delta; otherwise it is the IEEE division. Inactive eras get factor 0
+    // and keep mean/M2 by selection. TABLE and DIR are compile-time, so the loop has no
+    // branches.
     const bool table = unit_w && a.E < RT;
-    auto consume = [&](int chunk) {
+    auto consume = [&](int chunk, auto table_flag, auto dir_flag) {
+        constexpr bool TABLE = decltype(table_flag)::value;
+        constexpr bool DIR = decltype(dir_flag)::value;
         const int e0 = chunk * kPcEras;
         const int ne = min(kPcEras, a.E - e0);
         const float4* buf = ring + (chunk & 1) * kPcEras * kWave;
+        static_assert(kPcEras % 8 == 0, "batches of 8 eras must tile a chunk");
         for (int b0 = 0; b0 < ne; b0 += 8) {
             float4 rec[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j)
-                rec[j] = (b0 + j < ne) ? buf[(b0 + j) * kWave + tid]
-                                       : make_float4(0.0f, 0.0f, __int_as_float(-1), 0.0f);
+            for (int j = 0; j < 8; ++j) rec[j] = buf[(b0 + j) * kWave + tid];
             float fac[8], wv[8];
             bool actv[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float w = fabsf(rec[j].w);
                 const bool act = w > 0.0f;  // implies a row-bearing era; wsum + w > 0 then holds
-                const float wn = wsum + w;
-                if (table) {
-                    fac[j] = recip[act ? (int)wn : 0];
+                if (TABLE) {
+                    nact += act ? 1 : 0;
+                    fac[j] = recip[act ? nact : 0];
                 } else {
+                    const float wn = wsum + w;
                     fac[j] = w / (act ? wn : 1.0f);
+                    wsum = act ? wn : wsum;
                 }
                 wv[j] = w;
                 actv[j] = act;
-                wsum = act ? wn : wsum;
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int L = __float_as_int(rec[j].z);
-                const bool has = L >= 0;
-                lt += has ? L : 0;
-                lg = has ? lg + rec[j].y : lg;
+                lt += __float_as_int(rec[j].z);
+                lg = lg + rec[j].y;
                 const float gain = rec[j].x;
-                const float w = wv[j];
                 const bool act = actv[j];
                 const float delta = gain - mean;
                 const float mean_n = mean + fac[j] * delta;
-                const float M2_n = M2 + (w * delta) * (gain - mean_n);
+                const float wdelta = TABLE ? delta : wv[j] * delta;
+                const float M2_n = M2 + wdelta * (gain - mean_n);
                 mean = act ? mean_n : mean;
                 M2 = act ? M2_n : M2;
-                if (use_dir) {
+                if (DIR) {
+                    const float w = wv[j];
                     agn = act ? agn + w * ((rec[j].w > 0.0f) ? 1.0f : -1.0f) : agn;
                     agd = act ? agd + w : agd;
                 }
@@ -495,7 +513,19 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
     __syncthreads();
     for (int ch = 0; ch < nchunks; ++ch) {
         if (consumer) {
-            if (owner || tid == kWave - 1) consume(ch);
+            if (owner || tid == kWave - 1) {
+                if (table) {
+                    if (use_dir)
+                        consume(ch, std::true_type{}, std::true_type{});
+                    else
+                        consume(ch, std::true_type{}, std::false_type{});
+                } else {
+                    if (use_dir)
+                        consume(ch, std::false_type{}, std::true_type{});
+                    else
+                        consume(ch, std::false_type{}, std::false_type{});
+                }
+            }
         } else if (ch + 1 < nchunks) {
             produce(ch + 1);
             prefetch(ch + 2);
@@ -503,6 +533,7 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
         __syncthreads();
     }
     if (consumer) {
+        if (table) wsum = (float)nact;  // exact: a sum of ones below 2^24
         tc = __shfl(lt, kWave - 1);
         tg = __shfl(lg, kWave - 1);
     }
@@ -792,18 +823,22 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
 
 }  // namespace
 
-ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes) {
+ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t target_wgs) {
     ScoreShape sh;
     sh.rt = std::max(2, std::min<int32_t>(E + 1, 4096));
     if (T < kWave) {
-        // producer/consumer kernel: a 64-lane consumer wavefront per workgroup, 63 candidate
-        // lanes + one lane for the node totals
-        sh.fts = std::max(1, std::min<int32_t>(K, (kWave - 1) / T));
+        // producer/consumer kernel: a 64-lane consumer wavefront per workgroup, up to 63
+        // candidate lanes + one lane for the node totals. A workgroup walks all eras in
+        // order (the era recurrence is sequential), so its duration barely depends on how
+        // many candidates it carries: spread the candidates over about `target_wgs`
+        // workgroups (three fit in a CU's LDS) rather than packing 63 per workgroup.
+        const int64_t want = std::max<int64_t>(1, target_wgs);
+        const int64_t per = ((int64_t)K * std::max(1, nodes) + want - 1) / want;  // features / WG
+        sh.fts = (int)std::max<int64_t>(1, std::min<int64_t>({(int64_t)K, (kWave - 1) / T, per}));
         sh.ntiles = (K + sh.fts - 1) / sh.fts;
         sh.wpt = 1;
         sh.ec = kPcEras;
         sh.lds_bytes = (size_t)((sh.rt + 3) & ~3) * 4 + 2 * (size_t)kPcEras * kWave * 16;
-        (void)nodes;
         return sh;
     }
     // many thresholds per feature (nb > 65): one feature per workgroup, all threads alternate
