@@ -28,6 +28,15 @@
 #include <omp.h>
 #endif
 
+/* Planted mistakes for the tests that show the oracle's checks have teeth
+ * (tests/test_oracle_closed_form.py builds one copy per value; 0 = the restatement):
+ *   1 parent gain dropped          2 era weight ignores era_alpha
+ *   3 M2 update uses the old mean  4 direction sign flipped
+ *   5 threshold index off by one */
+#ifndef ORACLE_MUTANT
+#define ORACLE_MUTANT 0
+#endif
+
 #define OR_OK 0
 #define OR_ERR_INVALID (-1)
 #define OR_ERR_RANGE (-2)
@@ -154,12 +163,21 @@ static void score_feature(const int64_t* pc, const float* pg, int E, int nb, con
         for (int e = 0; e < E; ++e) {
             const int64_t total_e = pc[(int64_t)e * nb + nb - 1];
             if (total_e == 0) continue;
-            const int64_t left_e = pc[(int64_t)e * nb + thr];
+#if ORACLE_MUTANT == 5
+            const int32_t thr_m = (thr + 1 < nb - 1) ? thr + 1 : thr;
+#else
+            const int32_t thr_m = thr;
+#endif
+            const int64_t left_e = pc[(int64_t)e * nb + thr_m];
             const int64_t right_e = total_e - left_e;
-            const float left_grad_e = pg[(int64_t)e * nb + thr];
+            const float left_grad_e = pg[(int64_t)e * nb + thr_m];
             const float total_grad_e = pg[(int64_t)e * nb + nb - 1];
             const float right_grad_e = total_grad_e - left_grad_e;
+#if ORACLE_MUTANT == 2
+            const float era_w = 1.0f;
+#else
             const float era_w = (era_alpha > 0.0f) ? ((float)total_e + era_alpha) : 1.0f;
+#endif
             const float weight = (left_e > 0 && right_e > 0) ? era_w : 0.0f;
             left_total += left_e;
             left_grad_sum += left_grad_e;
@@ -167,22 +185,36 @@ static void score_feature(const int64_t* pc, const float* pg, int E, int nb, con
             const float denom_L = (float)left_e + lambda_l2;
             const float denom_R = (float)right_e + lambda_l2;
             const float parent_denom = (float)total_e + lambda_l2;
+#if ORACLE_MUTANT == 1
+            const float parent_gain = 0.0f * parent_denom;
+#else
             const float parent_gain =
                 (parent_denom > 0.0f) ? 0.5f * (total_grad_e * total_grad_e) / parent_denom : 0.0f;
+#endif
             const float gain_e = 0.5f * ((left_grad_e * left_grad_e) / denom_L +
                                          (right_grad_e * right_grad_e) / denom_R) - parent_gain;
             const float delta = gain_e - mean;
             const float wsum_new = wsum + weight;
             if (wsum_new > 0.0f) {
                 const float factor = weight / wsum_new;
+#if ORACLE_MUTANT == 3
+                const float mean_old = mean;
+                mean += factor * delta;
+                M2 += weight * delta * (gain_e - mean_old);
+#else
                 mean += factor * delta;
                 M2 += weight * delta * (gain_e - mean);
+#endif
                 wsum = wsum_new;
             }
             if (use_dir) {
                 const float left_val = -left_grad_e / denom_L;
                 const float right_val = -right_grad_e / denom_R;
+#if ORACLE_MUTANT == 4
+                const float direction = (left_val > right_val) ? -1.0f : 1.0f;
+#else
                 const float direction = (left_val > right_val) ? 1.0f : -1.0f;
+#endif
                 agr_num += weight * direction;
                 agr_den += weight;
             }

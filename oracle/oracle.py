@@ -39,25 +39,54 @@ def lib() -> ctypes.CDLL:
     if _lib is None:
         if not LIB_PATH.exists():
             build()
-        L = ctypes.CDLL(str(LIB_PATH))
-        P = ctypes.c_void_p
-        L.oracle_split_batch.restype = ctypes.c_int
-        L.oracle_split_batch.argtypes = (
-            [P, ctypes.c_int64, ctypes.c_int64, P, ctypes.c_int32, ctypes.c_int32, P, P, P,
-             ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float,
-             ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_int32] + [P] * 17)
-        L.oracle_score_planes.restype = ctypes.c_int
-        L.oracle_score_planes.argtypes = (
-            [P, P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, P, P,
-             ctypes.c_int32, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
-             ctypes.c_int32] + [P] * 9)
-        L.oracle_even_cuts.restype = ctypes.c_int
-        L.oracle_even_cuts.argtypes = [ctypes.c_int, ctypes.c_int, P]
-        L.oracle_mass_cuts.restype = ctypes.c_int
-        L.oracle_mass_cuts.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
-        L.oracle_num_threads.restype = ctypes.c_int
-        _lib = L
+        _lib = load_library(LIB_PATH)
     return _lib
+
+
+def build_mutant(n: int, out_dir: Path) -> Path:
+    """Compiles the restatement with planted mistake `n` (frontier_ref.c, ORACLE_MUTANT)."""
+    out = Path(out_dir) / f"liboracle_mutant{n}.so"
+    subprocess.run(["gcc", "-O2", "-fPIC", "-fopenmp", "-std=c11", f"-DORACLE_MUTANT={n}",
+                    "-shared", "-o", str(out), str(HERE / "frontier_ref.c"), "-lm"], check=True)
+    return out
+
+
+class use_library:
+    """Context manager: route every oracle call through another build of frontier_ref.c."""
+
+    def __init__(self, path: Path) -> None:
+        self.path = path
+
+    def __enter__(self):
+        global _lib
+        self.saved = _lib
+        _lib = load_library(self.path)
+        return _lib
+
+    def __exit__(self, *exc) -> None:
+        global _lib
+        _lib = self.saved
+
+
+def load_library(path: Path) -> ctypes.CDLL:
+    L = ctypes.CDLL(str(path))
+    P = ctypes.c_void_p
+    L.oracle_split_batch.restype = ctypes.c_int
+    L.oracle_split_batch.argtypes = (
+        [P, ctypes.c_int64, ctypes.c_int64, P, ctypes.c_int32, ctypes.c_int32, P, P, P,
+         ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_float,
+         ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_int32] + [P] * 17)
+    L.oracle_score_planes.restype = ctypes.c_int
+    L.oracle_score_planes.argtypes = (
+        [P, P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, P, P,
+         ctypes.c_int32, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+         ctypes.c_int32] + [P] * 9)
+    L.oracle_even_cuts.restype = ctypes.c_int
+    L.oracle_even_cuts.argtypes = [ctypes.c_int, ctypes.c_int, P]
+    L.oracle_mass_cuts.restype = ctypes.c_int
+    L.oracle_mass_cuts.argtypes = [P, ctypes.c_int, ctypes.c_int, P]
+    L.oracle_num_threads.restype = ctypes.c_int
+    return L
 
 
 def _p(a: np.ndarray | None):

@@ -1,0 +1,89 @@
+"""The oracle's fit loop and the host-side binning against the reference's own fit.
+
+tests/golden/fit_*.npz hold the reference PackBoost.fit (device="cpu", native split finder
+compiled from the reference's sources) on five small problems: trees of every round, bins
+and bin edges, and predict() on the training rows (tests/golden/make_fit_golden.py).
+These pin what no single-depth check can: the round/depth loop (booster.py:494-599) with its
+RNG draws only while a depth has active nodes (516-519), shard dedup, TreeBuilder numbering,
+leaf values in Python double, no-split leaves re-summed by torch (532-542), pack
+aggregation, era encoding of interleaved labels, even/mass K-cuts, and the quantile binning
+(data.py:31-111).
+
+Bars: bins, bin edges, tree structure and leaf values bit-identical; predictions bit-identical.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+CASES = sorted(p.stem for p in GOLDEN.glob("fit_*.npz"))
+
+
+def load_case(name: str) -> dict:
+    with np.load(GOLDEN / f"{name}.npz", allow_pickle=False) as z:
+        d = {k: z[k] for k in z.files}
+    d["config"] = json.loads(str(d["config"]))
+    d["rounds"] = int(d["rounds"])
+    d["trees"] = [{key: d[f"r{r}_{key}"] for key in
+                   ("feature", "threshold", "left", "right", "value", "is_leaf")}
+                  for r in range(d["rounds"])]
+    return d
+
+
+def era_codes(era: np.ndarray) -> np.ndarray:
+    return np.unique(era, return_inverse=True)[1].astype(np.int64).reshape(-1)
+
+
+def test_golden_cases_present():
+    assert len(CASES) == 5, CASES
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_binning_matches_reference(name):
+    from packboost_amd.data import preprocess_features
+
+    d = load_case(name)
+    res = preprocess_features(d["X"], d["config"]["max_bins"])
+    np.testing.assert_array_equal(res.bins, d["bins"])
+    assert bool(d["has_edges"]) == (res.bin_edges is not None)
+    if res.bin_edges is not None:
+        lens = [len(e) for e in res.bin_edges]
+        np.testing.assert_array_equal(lens, d["edge_lens"])
+        np.testing.assert_array_equal(np.concatenate([np.asarray(e, np.float64) for e in res.bin_edges]),
+                                      d["edges"])
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_oracle_fit_matches_reference(oracle_mod, name):
+    d = load_case(name)
+    cfg = d["config"]
+    res = oracle_mod.fit(d["bins"], d["y"], era_codes(d["era"]), num_rounds=d["rounds"], **cfg)
+    assert len(res.rounds) == d["rounds"]
+    for r, (got, want) in enumerate(zip(res.rounds, d["trees"])):
+        for key in ("feature", "threshold", "left", "right", "is_leaf"):
+            np.testing.assert_array_equal(np.asarray(got[key]), want[key], err_msg=f"round {r} {key}")
+        np.testing.assert_array_equal(np.asarray(got["value"], np.float64), want["value"],
+                                      err_msg=f"round {r} value")
+    pred = oracle_mod.predict(res.rounds, cfg["pack_size"], cfg["learning_rate"], d["bins"])
+    np.testing.assert_array_equal(pred, d["preds"])
+
+
+def test_early_stop_case_stops_early():
+    """The early-stop fixture really exercises the RNG rewind (trees shallower than D)."""
+    d = load_case("fit_early_stop")
+    D = d["config"]["max_depth"]
+    deepest = []
+    for t in d["trees"]:
+        depth = np.zeros(len(t["feature"]), np.int64)
+        for i in range(len(t["feature"])):
+            if not t["is_leaf"][i]:
+                depth[t["left"][i]] = depth[t["right"][i]] = depth[i] + 1
+        deepest.append(int(depth.max()))
+    # a round whose leaves all sit above depth D drew fewer than D subsets; later rounds
+    # then depend on the rewound generator
+    assert any(x < D for x in deepest[:-1]), deepest
