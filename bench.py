@@ -103,6 +103,19 @@ def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None
     }
 
 
+def profiled_traffic(config: int, rows: int) -> float | None:
+    """HBM bytes per hist launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of
+    this workload (profiles/hist_score_config<N>.md, its `traffic_bytes_per_launch` line), or
+    None when the workload differs from the profiled one."""
+    path = ROOT / "profiles" / f"hist_score_config{config}.md"
+    if rows != CONFIGS[config]["rows"] or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def copy_probe(mib: int) -> int:
     """Reads and writes exactly `mib` MiB per launch: the reference point that scales the
     FETCH_SIZE / WRITE_SIZE counters to HBM bytes."""
@@ -222,7 +235,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(args.config, N),
             "kernel": "hist_era_kernel",
             "avg_launch_ms": round(hist_ms / max(n_hist, 1), 4),
             "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),

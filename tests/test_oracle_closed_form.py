@@ -212,3 +212,28 @@ def test_planted_mistakes_are_caught(oracle_mod, tmp_path, mutant):
                 continue
             passed.append(name)
     assert not passed, f"mutant {mutant} passed {passed}"
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_score_planes_agrees_with_split_batch(oracle_mod, seed):
+    """The plane-fed scorer (used to feed the GPU scorer the oracle's histograms) gives the
+    split finder's candidates bit-for-bit on the split finder's own planes."""
+    rng = np.random.default_rng(300 + seed)
+    N, F, E, nb, U = 600, 4, 5, int(rng.integers(3, 20)), 3
+    bins = rng.integers(0, nb, size=(N, F)).astype(np.uint8)
+    grad = rng.standard_normal(N).astype(np.float32)
+    node = rng.integers(0, U, size=N)
+    era = rng.integers(0, E, size=N)
+    ner = [[np.nonzero((node == u) & (era == e))[0] for e in range(E)] for u in range(U)]
+    feats = rng.permutation(F).astype(np.int32)
+    kw = dict(lambda_l2=0.2, lambda_dro=0.3, direction_weight=0.1 * (seed % 2),
+              era_alpha=1.0 * (seed % 3 == 1), min_samples_leaf=5)
+    ref = oracle_mod.split_batch(bins, grad, ner, feats, nb, want_planes=True, want_cands=True, **kw)
+    sp = oracle_mod.score_planes(ref.planes[0], ref.planes[1], feats, None, **kw)
+    v = ref.cands[3].astype(bool)
+    np.testing.assert_array_equal(sp["valid"].astype(bool), v)
+    np.testing.assert_array_equal(sp["score"][v].view(np.uint32), ref.cands[0][v].view(np.uint32))
+    np.testing.assert_array_equal(sp["left_total"][v], ref.cands[1][v])
+    for u in range(U):
+        if ref.feature[u] >= 0:
+            assert (sp["best_feature"][u], sp["best_threshold"][u]) == (ref.feature[u], ref.threshold[u])
