@@ -35,6 +35,9 @@ struct pb_ctx {
     int32_t force_ftile;
     int32_t force_pairs;
     int32_t score_wgs;  // workgroups the producer/consumer scorer aims for
+    int32_t num_cus;        // compute units of the device
+    int32_t hist_resident;  // histogram: loop work items over a resident grid
+    int32_t hist_rounds;
     // phase timing of pb_grow_round (pb_profile_enable): per depth, 5 events bracket the
     // hist / score / decide / partition launches on the caller's stream
     bool profile;
@@ -161,6 +164,12 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     for (int dd = 0; dd < d.max_depth; ++dd) c->umax = std::max(c->umax, max_nodes_at(c, dd));
     const int tmax = std::max(1, d.max_bins - 1);
     c->score_wgs = (int32_t)env_int("PB_SCORE_WGS", 768);
+    c->hist_resident = (int32_t)env_int("PB_HIST_RESIDENT", 0);
+    c->hist_rounds = (int32_t)env_int("PB_HIST_ROUNDS", 1);
+    c->num_cus = 0;
+    if (hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, c->device) !=
+        hipSuccess)
+        c->num_cus = 0;
     c->wmax = 1;
     for (int t = 1; t <= tmax; ++t)
         for (int dd = 0; dd < d.max_depth; ++dd) {
@@ -251,13 +260,16 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
     // (occupancy beats copies), the largest feature tile that fits comes first, then as many
     // histogram copies as fit in half of that.
     int P = (nb <= 16 && K >= 2) ? 2 : 1;
-    if (c->force_pairs == 1 || (c->force_pairs == 2 && nb <= 16)) P = c->force_pairs;
-    const int64_t cells_group = (int64_t)max_nodes * (P == 2 ? nb * nb : nb);
+    if (c->force_pairs == 1 || (c->force_pairs == 2 && nb <= 16) ||
+        (c->force_pairs == 3 && nb <= 6 && K >= 3))
+        P = c->force_pairs;
+    const int64_t cells_group = (int64_t)max_nodes * (P == 3 ? nb * nb * nb : P == 2 ? nb * nb : nb);
     const int64_t cap = std::max<int64_t>(c->lds_budget, 4 * 1024);
     const int64_t groups_k = (K + P - 1) / P;
-    const int max_groups = (P == 2) ? 8 : 16;  // FT <= 16 (more registers cost occupancy)
+    // FT <= 16 (more registers cost occupancy); triples: FT <= 12
+    const int max_groups = (P == 3) ? 4 : (P == 2) ? 8 : 16;
     int64_t groups = max_groups;
-    if (c->force_ftile > 0) groups = std::max<int64_t>(1, c->force_ftile / P);
+    if (c->force_ftile > 0) groups = std::max<int64_t>(1, std::min(c->force_ftile, P == 2 ? 32 : 16) / P);
     while (groups > 1 && groups * cells_group * 8 > cap) groups /= 2;
     int64_t need = 1;
     while (need < groups_k) need *= 2;  // no more groups than the features present need
@@ -276,6 +288,8 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
                     "pb_hist_build: one feature's node x bin histogram exceeds the 160 KiB LDS");
 
     pb::HistArgs a;
+    a.resident_cus = c->hist_resident ? c->num_cus : 0;
+    a.rounds = c->hist_rounds;
     a.bins = bins;
     a.ld = c->d.ld;
     a.grad = grad;

@@ -37,6 +37,8 @@ struct NodeTotal {
 };
 
 struct HistArgs {
+    int32_t resident_cus;  // > 0: loop work items over a resident grid on this many CUs
+    int32_t rounds;        // resident grids' worth of workgroups (1 = one per slot)
     const uint8_t* bins;
     int64_t ld;
     const float* grad;
