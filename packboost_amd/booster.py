@@ -306,6 +306,12 @@ class PackBoost:
         out = self._predict_device(bins_fm, N, device)
         return out.cpu().numpy()
 
+    def save(self, path) -> "Path":
+        """Writes the fitted model as a versioned .npz bundle (see predictor.save_bundle)."""
+        from .predictor import save_bundle
+
+        return save_bundle(self, path)
+
     def predict_packwise(self, X, block_size_trees: int = 8) -> np.ndarray:
         if block_size_trees <= 0:
             raise ValueError("block_size_trees must be positive")
