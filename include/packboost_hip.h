@@ -227,6 +227,16 @@ int pb_frontier_set(pb_ctx* ctx, int32_t depth, int32_t num_active, const int32_
  * tree size to host memory; synchronises `stream`. */
 int pb_frontier_counts(pb_ctx* ctx, int32_t* u_active_host, int32_t* tree_size_host, void* stream);
 
+/* ---- round metrics ------------------------------------------------------------------ */
+/* Mean over eras of the Pearson correlation of y and preds (PackBoost._era_correlation_np,
+ * booster.py:909-929, the train/eval corr of booster.py:474-491, 604-655), in double with a
+ * fixed reduction order. Rows are era-major: era e is [era_off[e], era_off[e+1]) (device
+ * int32 [E+1]). An era counts with >= 2 rows, both standard deviations > 1e-12 and a finite
+ * correlation. era_corr_dev: double [E] per-era correlations (NaN where not counted);
+ * out_dev: double [1], the mean (NaN if no era counts). */
+int pb_era_corr(const float* y_dev, const float* preds_dev, const int32_t* era_off_dev,
+                int32_t num_eras, double* era_corr_dev, double* out_dev, void* stream);
+
 /* ---- prediction --------------------------------------------------------------------- */
 /* Kernel 4 — batched pack prediction. Replaces predict_pack_cuda (frontier_cuda.cu:925-1068):
  * out[r] = tree_weight * sum_t value(leaf_t(r)) over the B trees of one packed forest

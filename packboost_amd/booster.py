@@ -234,7 +234,8 @@ class PackBoost:
         fitter = DeviceFit(bins_fm, N, y_dev, offsets, cfg)
         self._fitter = fitter
         k = subset_size(cfg, F)
-        era_ids_dev = torch.from_numpy(np.repeat(np.arange(E), np.diff(offsets))).to(device)
+        era_off_dev = torch.from_numpy(np.asarray(offsets, dtype=np.int32)).to(device)
+        corr_scratch = torch.empty(E + 1, dtype=torch.float64, device=device)
         eval_states = self._prepare_eval(eval_sets, device)
         eval_every = _eval_every()
         # metrics and eval predictions run on a side stream so that the next round, already
@@ -261,9 +262,9 @@ class PackBoost:
                     if eval_states and eval_every > 0 and (
                             (round_idx + 1) % eval_every == 0 or round_idx + 1 == num_rounds):
                         self._update_eval(eval_states)
-                    train_corr = _era_corr_device(era_ids_dev, fitter.y[:N], preds_after[:N], E)
+                    train_corr = _era_corr_device(fitter.y, preds_after, era_off_dev, corr_scratch)
                     eval_corr = {f"{st['name']}_corr": _era_corr_device(
-                        st["era_ids"], st["y"], st["preds"], st["num_eras"]) for st in eval_states}
+                        st["y"], st["preds"], st["era_off"], st["corr_scratch"]) for st in eval_states}
                 t1 = perf_counter()
                 round_time = t1 - t0
                 t0 = t1
@@ -353,11 +354,18 @@ class PackBoost:
                 b = apply_bins(X_eval, self._binner.bin_edges, self.config.max_bins)
             n = b.shape[0]
             codes, uniq = encode_eras(era_eval, n)
+            E = int(uniq.shape[0])
+            # rows era-major (metrics only: eval predictions never leave the fit)
+            perm, offs = era_major_order(codes, E)
+            yv = np.asarray(y_eval, dtype=np.float32).reshape(-1)
+            if perm is not None:
+                b, yv = b[perm], yv[perm]
             states.append({
                 "name": name, "bins_fm": _to_column_major(b, device), "n": n,
-                "y": torch.from_numpy(np.asarray(y_eval, dtype=np.float32)).to(device),
-                "era_ids": torch.from_numpy(codes.astype(np.int64)).to(device),
-                "num_eras": int(uniq.shape[0]),
+                "y": torch.from_numpy(np.ascontiguousarray(yv)).to(device),
+                "era_off": torch.from_numpy(np.asarray(offs, dtype=np.int32)).to(device),
+                "corr_scratch": torch.empty(E + 1, dtype=torch.float64, device=device),
+                "num_eras": E,
                 "preds": torch.zeros(n, dtype=torch.float32, device=device),
             })
         return states
@@ -414,30 +422,12 @@ def _eval_every() -> int:
         return 1
 
 
-def _era_corr_device(era_ids: torch.Tensor, y: torch.Tensor, p: torch.Tensor, num_eras: int) -> float:
-    """Mean over eras of the Pearson correlation of y and preds (booster.py:909-929).
-
-    Eras with < 2 rows or a (near-)constant side are skipped; NaN if none remain.
-    """
-    yd = y.double()
-    pd_ = p.double()
-    ones = torch.ones_like(yd)
-
-    def seg(v):
-        return torch.zeros(num_eras, dtype=torch.float64, device=v.device).index_add_(0, era_ids, v)
-
-    n = seg(ones)
-    sy, sp = seg(yd), seg(pd_)
-    syy, spp, syp = seg(yd * yd), seg(pd_ * pd_), seg(yd * pd_)
-    nn = n.clamp_min(1)
-    my, mp = sy / nn, sp / nn
-    vy = (syy / nn - my * my).clamp_min(0)
-    vp = (spp / nn - mp * mp).clamp_min(0)
-    cov = syp / nn - my * mp
-    sy_, sp_ = vy.sqrt(), vp.sqrt()
-    ok = (n >= 2) & (sy_ > 1e-12) & (sp_ > 1e-12)
-    if not bool(ok.any()):
-        return float("nan")
-    corr = cov[ok] / (sy_[ok] * sp_[ok])
-    corr = corr[torch.isfinite(corr)]
-    return float(corr.mean().item()) if corr.numel() else float("nan")
+def _era_corr_device(y: torch.Tensor, p: torch.Tensor, era_off: torch.Tensor,
+                     scratch: torch.Tensor) -> float:
+    """Mean over eras of the Pearson correlation of y and preds (booster.py:909-929) by the
+    pb_era_corr kernel on the current stream; rows are era-major, era_off int32 [E+1]."""
+    E = int(era_off.numel()) - 1
+    lib = _hip.load()
+    _hip.check(lib.pb_era_corr(y.data_ptr(), p.data_ptr(), era_off.data_ptr(), E, scratch.data_ptr(),
+                               scratch.data_ptr() + 8 * E, _hip.stream_ptr()), "pb_era_corr")
+    return float(scratch[E].item())

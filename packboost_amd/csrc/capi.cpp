@@ -545,6 +545,16 @@ int pb_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const
     return PB_OK;
 }
 
+int pb_era_corr(const float* y, const float* preds, const int32_t* era_off, int32_t num_eras,
+                double* era_corr, double* out, void* stream) {
+    if (!y || !preds || !era_off || !era_corr || !out)
+        return fail(PB_ERR_INVALID, "pb_era_corr: null argument");
+    if (num_eras < 1) return fail(PB_ERR_INVALID, "pb_era_corr: num_eras must be >= 1");
+    PB_HIP(pb::launch_era_corr(y, preds, era_off, num_eras, era_corr, out, (hipStream_t)stream),
+           "era corr launch");
+    return PB_OK;
+}
+
 int pb_predict_forest(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
                       const int32_t* feature, const int32_t* threshold, const int32_t* left_abs,
                       const int32_t* right_abs, const float* value, const uint8_t* is_leaf,

@@ -113,6 +113,8 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
 hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s);
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
                             float lr, float* preds, int64_t N, hipStream_t s);
+hipError_t launch_era_corr(const float* y, const float* p, const int32_t* era_off, int32_t E,
+                           double* era_corr, double* out, hipStream_t s);
 hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
                                const int32_t* feature, const int32_t* threshold,
                                const int32_t* left_abs, const int32_t* right_abs,
