@@ -227,6 +227,24 @@ int pb_frontier_set(pb_ctx* ctx, int32_t depth, int32_t num_active, const int32_
  * tree size to host memory; synchronises `stream`. */
 int pb_frontier_counts(pb_ctx* ctx, int32_t* u_active_host, int32_t* tree_size_host, void* stream);
 
+/* ---- quantile binning ---------------------------------------------------------------- */
+/* Interior quantile edges of quantile_bin (data.py:44-56): for every column f of
+ * sorted_dev (float32 [F][ld], each column's n values ascending, NaN last) and level q[k]
+ * (double [num_q], the reference's linspace(0, 1, max_bins + 1)[1:-1]), edges[k][f] =
+ * float32 of NumPy's method="linear" quantile, its arithmetic restated exactly; a column with
+ * a NaN gets NaN edges. edges_dev: float32, row k at edges_dev + k * edge_stride. */
+int pb_quantile_edges(const float* sorted_dev, int64_t n, int64_t ld, int32_t F,
+                      const double* q_dev, int32_t num_q, float* edges_dev, int32_t edge_stride,
+                      void* stream);
+
+/* apply_bins (data.py:93-111): bins[f][r] = min(searchsorted(edges[:, f], x, side="left"),
+ * max_bins - 1) with NumPy's NaN-last order, x = xt[f][perm ? perm[r] : r] (xt: float32
+ * [F][ld_x] column-major values; perm: optional int64 [n] row gather, e.g. the era-major
+ * order). bins_dev: uint8 [F][ld_out], the histogram kernel's layout. */
+int pb_apply_bins(const float* xt_dev, int64_t n, int64_t ld_x, int32_t F, const float* edges_dev,
+                  int32_t num_edges, int32_t edge_stride, int32_t max_bins, const int64_t* perm_dev,
+                  uint8_t* bins_dev, int64_t ld_out, void* stream);
+
 /* ---- round metrics ------------------------------------------------------------------ */
 /* Mean over eras of the Pearson correlation of y and preds (PackBoost._era_correlation_np,
  * booster.py:909-929, the train/eval corr of booster.py:474-491, 604-655), in double with a

@@ -27,7 +27,7 @@ EXPORTED_SYMBOLS = (
     "pb_era_offsets_dev", "pb_round_begin", "pb_hist_build", "pb_des_score", "pb_decide",
     "pb_partition", "pb_round_end", "pb_grow_round", "pb_profile_enable",
     "pb_profile_read", "pb_frontier_set", "pb_frontier_counts", "pb_predict_pack",
-    "pb_predict_forest", "pb_predict_bins", "pb_era_corr",
+    "pb_predict_forest", "pb_predict_bins", "pb_era_corr", "pb_quantile_edges", "pb_apply_bins",
 )
 
 
@@ -102,6 +102,8 @@ _SIGNATURES = {
     "pb_grow_round": (ctypes.c_int, [_VP, ctypes.POINTER(PbFitBuffers), _VP, _I32, _VP, _VP, _VP]),
     "pb_profile_enable": (ctypes.c_int, [_VP, _I32]),
     "pb_era_corr": (ctypes.c_int, [_VP, _VP, _VP, _I32, _VP, _VP, _VP]),
+    "pb_quantile_edges": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _VP, _I32, _VP]),
+    "pb_apply_bins": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _I32, _I32, _VP, _VP, _I64, _VP]),
     "pb_profile_read": (ctypes.c_int, [_VP, _VP, _VP]),
     "pb_frontier_set": (ctypes.c_int, [_VP, _I32, _I32, _VP, _I32, _VP]),
     "pb_frontier_counts": (ctypes.c_int, [_VP, _VP, _VP, _VP]),

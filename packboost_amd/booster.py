@@ -24,8 +24,9 @@ import torch
 from . import backends as native_backends
 from .backends import _hip
 from .config import PackBoostConfig
-from .data import (BinningResult, apply_bins, encode_eras, era_major_order,
-                   feature_names_or_default, preprocess_features)
+from .data import (BinningResult, apply_bins, apply_bins_device, detect_prebinned, encode_eras,
+                   era_major_order, feature_names_or_default, preprocess_features,
+                   quantile_bin_device)
 from .engine import (DeviceFit, column_major_bins, depth_log_from_round, padded_rows,
                      subset_size, tree_arrays_from_log)
 
@@ -128,6 +129,32 @@ def _to_column_major(bins, device: torch.device) -> torch.Tensor:
     return out
 
 
+def _is_float_input(X) -> bool:
+    if isinstance(X, torch.Tensor):
+        return X.dtype.is_floating_point
+    arr = X.to_numpy() if hasattr(X, "to_numpy") else X
+    return not np.issubdtype(np.asarray(arr).dtype, np.integer)
+
+
+def _bins_fm_for(X, bin_edges, max_bins: int, device: torch.device,
+                 perm: np.ndarray | None = None) -> tuple[torch.Tensor, int]:
+    """Column-major uint8 bins [F, ld] on the device for prediction / evaluation: float inputs
+    are binned on the device with the model's edges (apply_bins_device); integer inputs are
+    taken as bins (apply_bins' prebinned rule)."""
+    if bin_edges is not None and _is_float_input(X):
+        out = apply_bins_device(X, bin_edges, max_bins, device, perm=perm)
+        return out, int(X.shape[0])
+    if isinstance(X, torch.Tensor):
+        if X.dtype.is_floating_point:
+            raise ValueError("float inputs need the model's bin edges (the model was trained on bins)")
+        bins = X if perm is None else X[torch.as_tensor(perm, device=X.device)]
+    else:
+        bins = apply_bins(X, bin_edges, max_bins)
+        if perm is not None:
+            bins = bins[perm]
+    return _to_column_major(bins, device), int(bins.shape[0])
+
+
 def _require_backend(device: torch.device) -> None:
     if device.type != "cuda":
         raise RuntimeError(
@@ -207,18 +234,21 @@ class PackBoost:
         self._feature_names = feature_names_or_default(feature_names, F)
         self._num_features = F
 
-        if isinstance(X, torch.Tensor):
-            if X.dtype.is_floating_point:
-                raise ValueError("torch inputs must be integer bins (prebinned)")
-            self._binner = BinningResult(bins=np.empty((0, F), np.uint8), bin_edges=None, prebinned=True)
-            bins_src = X
-        else:
-            self._binner = preprocess_features(X_arr, cfg.max_bins, assume_prebinned=bool(cfg.prebinned))
-            bins_src = self._binner.bins
         perm, offsets = era_major_order(codes, E)
         device = self._device if self._device.index is not None else torch.device(
             "cuda", torch.cuda.current_device())
-        bins_fm = column_major_bins(bins_src, perm, device)
+        if isinstance(X, torch.Tensor) and not X.dtype.is_floating_point:
+            self._binner = BinningResult(bins=np.empty((0, F), np.uint8), bin_edges=None, prebinned=True)
+            bins_fm = column_major_bins(X, perm, device)
+        elif not isinstance(X, torch.Tensor) and (bool(cfg.prebinned) or detect_prebinned(X_arr, cfg.max_bins)):
+            self._binner = preprocess_features(X_arr, cfg.max_bins, assume_prebinned=bool(cfg.prebinned))
+            bins_fm = column_major_bins(self._binner.bins, perm, device)
+        else:
+            # quantile binning on the device, rows gathered era-major (data.py:44-56)
+            bins_fm, edges = quantile_bin_device(X if isinstance(X, torch.Tensor) else X_arr,
+                                                 cfg.max_bins, device, perm=perm)
+            self._binner = BinningResult(bins=np.empty((0, F), np.uint8), bin_edges=edges,
+                                         prebinned=False)
         if N and int(bins_fm[:, :N].max().item()) >= cfg.max_bins:
             raise ValueError("bins must lie in [0, max_bins)")
         y_dev = torch.from_numpy(y_np if perm is None else y_np[perm]).to(device)
@@ -292,18 +322,14 @@ class PackBoost:
         _require_backend(self._device)
         if self._trained_pack_size is not None and int(self.config.pack_size) != self._trained_pack_size:
             raise RuntimeError("pack_size differs from training; keep it constant.")
-        if isinstance(X, torch.Tensor):
-            bins = X
-            N = int(X.shape[0])
-        else:
-            bins = apply_bins(X, self._binner.bin_edges, self.config.max_bins)
-            N = bins.shape[0]
+        N = int(X.shape[0])
         if not self._rounds:
             return np.zeros(N, dtype=np.float32)
         if self._tree_weight is None:
             raise RuntimeError("Missing _tree_weight; call fit() first.")
-        device = _device_of(bins)
-        bins_fm = _to_column_major(bins, device)
+        device = self._device if self._device.index is not None else torch.device(
+            "cuda", torch.cuda.current_device())
+        bins_fm, N = _bins_fm_for(X, self._binner.bin_edges, self.config.max_bins, device)
         out = self._predict_device(bins_fm, N, device)
         return out.cpu().numpy()
 
@@ -348,20 +374,18 @@ class PackBoost:
             name, X_eval, y_eval, era_eval = item
             if y_eval is None:
                 raise ValueError(f"eval set '{name}' requires y values for correlation logging")
-            if self.config.prebinned or self._binner.bin_edges is None:
-                b = apply_bins(X_eval, None, self.config.max_bins)
-            else:
-                b = apply_bins(X_eval, self._binner.bin_edges, self.config.max_bins)
-            n = b.shape[0]
+            n = int(X_eval.shape[0])
             codes, uniq = encode_eras(era_eval, n)
             E = int(uniq.shape[0])
             # rows era-major (metrics only: eval predictions never leave the fit)
             perm, offs = era_major_order(codes, E)
             yv = np.asarray(y_eval, dtype=np.float32).reshape(-1)
             if perm is not None:
-                b, yv = b[perm], yv[perm]
+                yv = yv[perm]
+            edges = None if self.config.prebinned else self._binner.bin_edges
+            bins_fm, _ = _bins_fm_for(X_eval, edges, self.config.max_bins, device, perm=perm)
             states.append({
-                "name": name, "bins_fm": _to_column_major(b, device), "n": n,
+                "name": name, "bins_fm": bins_fm, "n": n,
                 "y": torch.from_numpy(np.ascontiguousarray(yv)).to(device),
                 "era_off": torch.from_numpy(np.asarray(offs, dtype=np.int32)).to(device),
                 "corr_scratch": torch.empty(E + 1, dtype=torch.float64, device=device),

@@ -545,6 +545,32 @@ int pb_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const
     return PB_OK;
 }
 
+int pb_quantile_edges(const float* sorted, int64_t n, int64_t ld, int32_t F, const double* q,
+                      int32_t num_q, float* edges, int32_t edge_stride, void* stream) {
+    if (!sorted || !q || !edges) return fail(PB_ERR_INVALID, "pb_quantile_edges: null argument");
+    if (n < 0 || ld < n || F < 0 || num_q < 1 || num_q > 254 || edge_stride < F)
+        return fail(PB_ERR_INVALID, "pb_quantile_edges: bad shape");
+    if (F == 0) return PB_OK;
+    PB_HIP(pb::launch_quantile_edges(sorted, n, ld, F, q, num_q, edges, edge_stride,
+                                     (hipStream_t)stream),
+           "quantile edges launch");
+    return PB_OK;
+}
+
+int pb_apply_bins(const float* xt, int64_t n, int64_t ld_x, int32_t F, const float* edges,
+                  int32_t num_edges, int32_t edge_stride, int32_t max_bins, const int64_t* perm,
+                  uint8_t* bins, int64_t ld_out, void* stream) {
+    if (!xt || !edges || !bins) return fail(PB_ERR_INVALID, "pb_apply_bins: null argument");
+    if (n < 0 || ld_x < n || ld_out < n || F < 0 || num_edges < 1 || num_edges > 254 ||
+        edge_stride < F || max_bins < 2 || max_bins > 255 || F > 65535)
+        return fail(PB_ERR_INVALID, "pb_apply_bins: bad shape");
+    if (n == 0 || F == 0) return PB_OK;
+    PB_HIP(pb::launch_apply_bins(xt, n, ld_x, F, edges, num_edges, edge_stride, max_bins, perm, bins,
+                                 ld_out, (hipStream_t)stream),
+           "apply bins launch");
+    return PB_OK;
+}
+
 int pb_era_corr(const float* y, const float* preds, const int32_t* era_off, int32_t num_eras,
                 double* era_corr, double* out, void* stream) {
     if (!y || !preds || !era_off || !era_corr || !out)

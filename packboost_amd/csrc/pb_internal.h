@@ -113,6 +113,12 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
 hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s);
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
                             float lr, float* preds, int64_t N, hipStream_t s);
+hipError_t launch_quantile_edges(const float* sorted, int64_t n, int64_t ld, int32_t F,
+                                 const double* q, int32_t nq, float* edges, int32_t edge_stride,
+                                 hipStream_t s);
+hipError_t launch_apply_bins(const float* xt, int64_t n, int64_t ld_x, int32_t F,
+                             const float* edges, int32_t ne, int32_t edge_stride, int32_t max_bins,
+                             const int64_t* perm, uint8_t* bins, int64_t ld_out, hipStream_t s);
 hipError_t launch_era_corr(const float* y, const float* p, const int32_t* era_off, int32_t E,
                            double* era_corr, double* out, hipStream_t s);
 hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,

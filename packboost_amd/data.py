@@ -8,6 +8,10 @@ Semantics follow the reference's packboost/data.py:
     clipped to [0, nb-1];
   * build_era_index (data.py:114-134): per era, ascending row ids.
 Bins are returned as uint8 (values identical to the reference's int8 for max_bins <= 128).
+
+quantile_bin_device / apply_bins_device do the same on the HIP device (pb_quantile_edges,
+pb_apply_bins) and write the histogram kernel's column-major layout directly; their edges and
+bins are bit-identical to the NumPy path.
 """
 
 from __future__ import annotations
@@ -142,3 +146,69 @@ def feature_names_or_default(feature_names: Sequence[str] | None, n_features: in
             raise ValueError("feature_names length must match X columns")
         return names
     return [f"f{i}" for i in range(n_features)]
+
+
+def _float_matrix_device(X, device):
+    import torch
+
+    if isinstance(X, torch.Tensor):
+        return X.detach().to(device=device, dtype=torch.float32).contiguous()
+    Xn = np.ascontiguousarray(ensure_numpy(X), dtype=np.float32)
+    return torch.from_numpy(Xn).to(device)
+
+
+def _device_bins(X, max_bins: int, device, perm, edges, chunk_features: int):
+    import torch
+
+    from .backends import _hip
+
+    lib = _hip.load()
+    x = _float_matrix_device(X, device)
+    if x.dim() != 2:
+        raise ValueError("X must be 2-D [rows, features]")
+    N, F = int(x.shape[0]), int(x.shape[1])
+    ld = (N + 15) // 16 * 16
+    nq = int(max_bins) - 1
+    out = torch.zeros((F, ld), dtype=torch.uint8, device=device)
+    perm_dev = None
+    if perm is not None:
+        perm_dev = torch.as_tensor(np.ascontiguousarray(perm, dtype=np.int64)).to(device)
+    if edges is None:
+        qs = np.linspace(0.0, 1.0, int(max_bins) + 1, dtype=np.float64)[1:-1]
+        q_dev = torch.from_numpy(np.ascontiguousarray(qs)).to(device)
+        edges_dev = torch.empty((nq, F), dtype=torch.float32, device=device)
+    else:
+        q_dev = None
+        edges_dev = torch.from_numpy(np.ascontiguousarray(edges, dtype=np.float32)).to(device)
+        if tuple(edges_dev.shape) != (nq, F):
+            raise ValueError(f"bin_edges must be [{nq}, {F}]")
+    s = _hip.stream_ptr()
+    for f0 in range(0, F, chunk_features):
+        f1 = min(F, f0 + chunk_features)
+        xt = x[:, f0:f1].t().contiguous()  # [fc, N] column values
+        e_ptr = edges_dev.data_ptr() + 4 * f0
+        if q_dev is not None:
+            srt = torch.sort(xt, dim=1).values  # ascending, NaN last
+            _hip.check(lib.pb_quantile_edges(srt.data_ptr(), N, N, f1 - f0, q_dev.data_ptr(), nq,
+                                             e_ptr, F, s), "pb_quantile_edges")
+            del srt
+        _hip.check(lib.pb_apply_bins(xt.data_ptr(), N, N, f1 - f0, e_ptr, nq, F, int(max_bins),
+                                     None if perm_dev is None else perm_dev.data_ptr(),
+                                     out[f0].data_ptr(), ld, s), "pb_apply_bins")
+        del xt
+    return out, (edges_dev.cpu().numpy() if edges is None else np.asarray(edges, np.float32))
+
+
+def quantile_bin_device(X, max_bins: int, device, *, perm: np.ndarray | None = None,
+                        chunk_features: int = 256):
+    """quantile_bin on the device: (bins uint8 [F, roundup16(N)] on `device` with row r holding
+    input row perm[r], edges float32 [max_bins - 1, F] on the host)."""
+    _check_max_bins(max_bins)
+    return _device_bins(X, max_bins, device, perm, None, chunk_features)
+
+
+def apply_bins_device(X, bin_edges: np.ndarray, max_bins: int, device, *,
+                      perm: np.ndarray | None = None, chunk_features: int = 256):
+    """apply_bins on the device with given edges: uint8 [F, roundup16(N)] on `device`."""
+    _check_max_bins(max_bins)
+    return _device_bins(X, max_bins, device, perm, bin_edges, chunk_features)[0]

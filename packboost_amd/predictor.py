@@ -31,7 +31,6 @@ import torch
 
 from .backends import _hip
 from .config import PackBoostConfig
-from .data import apply_bins
 
 BUNDLE_FORMAT = "packboost-bundle"
 BUNDLE_VERSION = 1
@@ -143,17 +142,12 @@ class PackBoostPredictor:
         return self._forest
 
     def _bins_fm(self, X) -> tuple[torch.Tensor, int]:
-        from .booster import _to_column_major
+        from .booster import _bins_fm_for
 
-        if isinstance(X, torch.Tensor) and not X.dtype.is_floating_point:
-            bins = X
-        else:
-            bins = apply_bins(X, self.bin_edges, self.config.max_bins)
-        n = int(bins.shape[0])
-        if self.feature_names and int(bins.shape[1]) != len(self.feature_names):
-            raise ValueError(f"X has {int(bins.shape[1])} features; the model expects "
-                             f"{len(self.feature_names)}")
-        return _to_column_major(bins, self.device), n
+        nf = int(X.shape[1])
+        if self.feature_names and nf != len(self.feature_names):
+            raise ValueError(f"X has {nf} features; the model expects {len(self.feature_names)}")
+        return _bins_fm_for(X, self.bin_edges, self.config.max_bins, self.device)
 
     def predict(self, X) -> np.ndarray:
         """float32 predictions, bit-identical to PackBoost.predict on the same model."""

@@ -24,7 +24,7 @@ def _model_from_golden(name="fit_config1"):
     if bool(d["has_edges"]):
         lens = d["edge_lens"]
         assert np.all(lens == lens[0])
-        edges = d["edges"].reshape(len(lens), -1).T.astype(np.float32)  # [max_bins - 1, F]
+        edges = d["edges"].reshape(len(lens), -1).astype(np.float32)  # [max_bins - 1, F]
     m._binner = BinningResult(bins=d["bins"], bin_edges=edges, prebinned=edges is None)
     m._tree_weight = float(d["tree_weight"])
     m._trained_pack_size = cfg.pack_size
