@@ -263,8 +263,19 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
     if (c->force_pairs == 1 || (c->force_pairs == 2 && nb <= 16) ||
         (c->force_pairs == 3 && nb <= 6 && K >= 3))
         P = c->force_pairs;
-    const int64_t cells_group = (int64_t)max_nodes * (P == 3 ? nb * nb * nb : P == 2 ? nb * nb : nb);
-    const int64_t cap = std::max<int64_t>(c->lds_budget, 4 * 1024);
+    const int64_t cells_node = (P == 3 ? nb * nb * nb : P == 2 ? nb * nb : nb);
+    int64_t cap = std::max<int64_t>(c->lds_budget, 4 * 1024);
+    // node tiles when one feature's node x bin histogram does not fit: single features, up
+    // to 64 KiB of LDS, as many nodes per tile as fit
+    int node_tile = max_nodes;
+    if ((int64_t)max_nodes * cells_node * 8 > cap) {
+        P = 1;
+        cap = std::max<int64_t>(cap, 64 * 1024);
+        node_tile = (int)std::max<int64_t>(1, std::min<int64_t>(max_nodes, cap / ((int64_t)nb * 8)));
+    }
+    const int node_tiles = (max_nodes + node_tile - 1) / node_tile;
+    const int64_t cells_group =
+        (int64_t)node_tile * (P == 3 ? nb * nb * nb : P == 2 ? nb * nb : nb);
     const int64_t groups_k = (K + P - 1) / P;
     // FT <= 16 (more registers cost occupancy); triples: FT <= 12
     const int max_groups = (P == 3) ? 4 : (P == 2) ? 8 : 16;
@@ -301,6 +312,8 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
     a.ntiles = (K + ftile - 1) / ftile;
     a.ftile = ftile;
     a.U = max_nodes;
+    a.node_tile = node_tile;
+    a.node_tiles = node_tiles;
     a.nb = nb;
     a.clog2 = clog2;
     a.st = c->st;
@@ -308,7 +321,7 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
     a.out_cnt = hist_cnt;
     a.out_g = hist_grad;
     const int eras8 = (a.E + 7) / 8 * 8;
-    const int64_t grid = (int64_t)eras8 * a.ntiles;
+    const int64_t grid = (int64_t)eras8 * a.ntiles * node_tiles;
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: grid too large");
     PB_HIP(pb::launch_hist(a, P, (int)grid, lds_bytes, (hipStream_t)stream), "hist launch");
     return PB_OK;

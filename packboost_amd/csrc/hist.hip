@@ -53,7 +53,8 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
     const int nb = a.nb;
     const int cells_node = (P == 3) ? nb * nb * nb : (P == 2) ? nb * nb : nb;  // joint cells/node
     const int C = 1 << a.clog2;
-    const int words_group = a.U * cells_node * C;    // LDS words per group
+    const int UT = a.node_tile;                      // nodes held in LDS per work item
+    const int words_group = UT * cells_node * C;     // LDS words per group
     const float gmax = __uint_as_float(a.st->gmax_bits);
     int ex = 0;
     (void)frexpf(gmax, &ex);
@@ -66,15 +67,19 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
     // Work items (era, feature tile), XCD-aware: item i goes to XCD i % 8, and all tiles of an
     // era share one XCD. The grid is a multiple of 8, so a workgroup's items stay on its XCD;
     // looping lets a workgroup's plane stores drain while it already builds its next item.
-    const int n_items = ((a.E + 7) / 8) * 8 * a.ntiles;
+    const int per_era = a.ntiles * a.node_tiles;
+    const int n_items = ((a.E + 7) / 8) * 8 * per_era;
     for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
         const int xcd = item & 7;
         const int i = item >> 3;
-        const int era = (i / a.ntiles) * 8 + xcd;
-        const int tile = i - (i / a.ntiles) * a.ntiles;
+        const int era = (i / per_era) * 8 + xcd;
+        const int rem_i = i - (i / per_era) * per_era;
+        const int tile = rem_i / a.node_tiles;
+        const int u0 = (rem_i - tile * a.node_tiles) * UT;  // first node of this item
+        const int Un = min(UT, Ua - u0);                    // its nodes, UT or fewer
         const int k0 = tile * FT;
         const int nf = min(FT, a.K - k0);
-        if (era >= a.E || nf <= 0) continue;  // uniform over the workgroup
+        if (era >= a.E || nf <= 0 || Un <= 0) continue;  // uniform over the workgroup
 
         const int ng = (nf + P - 1) / P;
         const int words = ng * words_group;
@@ -133,8 +138,9 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
     #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int r = c + j;
-                const bool ok = (r >= r0) && (r < r1) && (n4[j] < (uint32_t)Ua);
-                const uint32_t nj = ok ? n4[j] : 0u;
+                const uint32_t nl = n4[j] - (uint32_t)u0;  // node within the item's tile
+                const bool ok = (r >= r0) && (r < r1) && (nl < (uint32_t)Un);
+                const uint32_t nj = ok ? nl : 0u;
                 base[j] = (__umul24(nj, cells_c) + copy) * 8u;  // nj < 2^16, cells_c < 2^24
                 const long long q = (long long)__float2int_rn(g4[j] * scale);
                 qv[j] = ok ? (((unsigned long long)q << kCountBits) + 1ull) : 0ull;
@@ -179,7 +185,7 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
         __syncthreads();
 
         // Flush. (1) Fold the C copies of every cell into copy 0 (all threads).
-        const int cells_total = ng * a.U * cells_node;
+        const int cells_total = ng * UT * cells_node;
         if (C > 1) {
             for (int x = threadIdx.x; x < cells_total; x += kBlock) {
                 unsigned long long* cp = lds + (int64_t)x * C;
@@ -197,7 +203,7 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
         const double inv_scale = ldexp(1.0, -sh);
         if (P == 1) {
             // single features own their cells: prefix them in place, one thread per (node, feature)
-            for (int p = threadIdx.x; p < nf * Ua; p += kBlock) {
+            for (int p = threadIdx.x; p < nf * Un; p += kBlock) {
                 const int u = p / nf;
                 const int kk = p - u * nf;
                 unsigned long long* hc = lds + ((int64_t)kk * words_group + (int64_t)u * cells_node * C);
@@ -210,7 +216,7 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
             __syncthreads();
         }
         const int run_len = nf * nb;
-        const int items = Ua * run_len;
+        const int items = Un * run_len;
         // marginal of element (u, kk, bb) alone (P == 1: the prefix, already in place)
         auto marginal = [&](int it, bool prefix) -> unsigned long long {
             const int u = it / run_len;
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
             const int rem = it - u * run_len;
             const uint32_t cnt = (uint32_t)(tot & ((1ull << kCountBits) - 1ull));
             const long long Q = ((long long)(tot - cnt)) >> kCountBits;
-            const int64_t o = ((int64_t)era * a.U + u) * a.K * nb + (int64_t)k0 * nb + rem;
+            const int64_t o = ((int64_t)era * a.U + u0 + u) * a.K * nb + (int64_t)k0 * nb + rem;
             a.out_cnt[o] = (int32_t)cnt;
             a.out_g[o] = (float)((double)Q * inv_scale);
         };

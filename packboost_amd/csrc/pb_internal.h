@@ -50,6 +50,8 @@ struct HistArgs {
     int32_t ntiles;
     int32_t ftile;
     int32_t U;      // node stride of the output planes (max nodes)
+    int32_t node_tile;   // nodes per work item (LDS tile), node_tiles * node_tile >= U
+    int32_t node_tiles;
     int32_t nb;
     int32_t clog2;  // log2 of LDS histogram copies
     const Frontier* st;

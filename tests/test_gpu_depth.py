@@ -27,6 +27,9 @@ CASES = [
     (4, 3000, 8, 3, 2, 2, 8, 1, 0.5, 0.0, 0.0, 0.0),
     (5, 20000, 40, 40, 5, 32, 24, 20, 1e-6, 0.5, 0.0, 0.0),
     (6, 5000, 10, 5, 255, 3, 10, 3, 1.0, 1.0, 0.0, 2.5),
+    # 100 nodes x 255 bins: one feature's histogram exceeds the LDS -> node tiles
+    (7, 30000, 12, 6, 255, 100, 6, 5, 1e-6, 0.5, 0.0, 0.0),
+    (8, 12000, 9, 4, 200, 70, 9, 3, 1.0, 0.2, 0.1, 1.0),
 ]
 
 
