@@ -279,6 +279,26 @@ int pb_predict_forest(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
                       const int32_t* offsets_dev, int32_t T, int32_t total_nodes,
                       float tree_weight, float* out_dev, void* stream);
 
+/* Compiled forest for repeated prediction (the reference re-packs per call,
+ * booster.py:730-783 + predict_pack_cuda, frontier_cuda.cu:925-1068). pb_forest_create reads
+ * the packed SoA forest (same arrays and layout as pb_predict_forest, offsets int32 [T+1],
+ * device pointers), checks every tree (children inside the tree, no node reached twice,
+ * 0 <= feature < 2^24 - 1, 0 <= threshold <= 255) and stores one 16-byte record per node
+ * in device memory the handle owns. pb_forest_predict gives the same result as
+ * pb_predict_forest: out[r] = sum over trees in order of float32(tree_weight * leaf value),
+ * one float32 rounding per product and per add (booster.py:709-712). A lane walks 8 trees
+ * at once. leaf_dev (optional): int32 [T][N] absolute leaf index per tree. PB_ERR_RANGE if a
+ * split feature is >= F. */
+typedef struct pb_forest pb_forest;
+int pb_forest_create(const int32_t* feature_dev, const int32_t* threshold_dev,
+                     const int32_t* left_abs_dev, const int32_t* right_abs_dev,
+                     const float* value_dev, const uint8_t* is_leaf_dev,
+                     const int32_t* offsets_dev, int32_t T, int32_t total_nodes, pb_forest** out);
+int pb_forest_predict(const pb_forest* forest, const uint8_t* bins_dev, int64_t N, int64_t ld,
+                      int32_t F, float tree_weight, float* out_dev, int32_t* leaf_dev,
+                      void* stream);
+int pb_forest_destroy(pb_forest* forest);
+
 /* Single tree. Replaces predict_bins_cuda (frontier_cuda.cu:193-233, 853-920):
  * out[r] = value(leaf(r)) with child indices relative to the tree. */
 int pb_predict_bins(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "pb_partition", "pb_round_end", "pb_grow_round", "pb_profile_enable",
     "pb_profile_read", "pb_frontier_set", "pb_frontier_counts", "pb_predict_pack",
     "pb_predict_forest", "pb_predict_bins", "pb_era_corr", "pb_quantile_edges", "pb_apply_bins",
+    "pb_forest_create", "pb_forest_predict", "pb_forest_destroy",
 )
 
 
@@ -102,6 +103,9 @@ _SIGNATURES = {
     "pb_grow_round": (ctypes.c_int, [_VP, ctypes.POINTER(PbFitBuffers), _VP, _I32, _VP, _VP, _VP]),
     "pb_profile_enable": (ctypes.c_int, [_VP, _I32]),
     "pb_era_corr": (ctypes.c_int, [_VP, _VP, _VP, _I32, _VP, _VP, _VP]),
+    "pb_forest_create": (ctypes.c_int, [_VP] * 7 + [_I32, _I32, _VP]),
+    "pb_forest_predict": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I32, _F32, _VP, _VP, _VP]),
+    "pb_forest_destroy": (ctypes.c_int, [_VP]),
     "pb_quantile_edges": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _VP, _I32, _VP]),
     "pb_apply_bins": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _I32, _I32, _VP, _VP, _I64, _VP]),
     "pb_profile_read": (ctypes.c_int, [_VP, _VP, _VP]),

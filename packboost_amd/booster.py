@@ -357,16 +357,14 @@ class PackBoost:
         return forest
 
     def _predict_device(self, bins_fm: torch.Tensor, N: int, device: torch.device) -> torch.Tensor:
-        f = self._forest_device(device)
-        out = torch.empty(N, dtype=torch.float32, device=device)
-        lib = _hip.load()
-        _hip.check(lib.pb_predict_forest(
-            bins_fm.data_ptr(), N, bins_fm.shape[1], bins_fm.shape[0], f["feature"].data_ptr(),
-            f["threshold"].data_ptr(), f["left_abs"].data_ptr(), f["right_abs"].data_ptr(),
-            f["value"].data_ptr(), f["is_leaf"].data_ptr(), f["offsets"].data_ptr(),
-            int(f["offsets"].numel() - 1), int(f["value"].numel()),
-            float(self._tree_weight), out.data_ptr(), _hip.stream_ptr()), "pb_predict_forest")
-        return out
+        from .predictor import CompiledForest
+
+        key = (str(device), len(self._rounds))
+        cached = getattr(self, "_compiled_forest", None)
+        if cached is None or cached[0] != key:
+            cached = (key, CompiledForest(self._forest_device(device)))
+            self._compiled_forest = cached
+        return cached[1].predict(bins_fm, N, float(self._tree_weight))
 
     def _prepare_eval(self, eval_sets, device) -> list[dict]:
         states = []

@@ -612,6 +612,121 @@ int pb_predict_forest(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
     return PB_OK;
 }
 
+struct pb_forest {
+    int4* rec = nullptr;       // one record per node
+    int32_t* roots = nullptr;  // tree roots (node index)
+    int32_t T = 0;
+    int32_t total_nodes = 0;
+    int32_t depth = 0;         // deepest leaf over all trees
+    int32_t max_feature = -1;
+};
+
+int pb_forest_create(const int32_t* feature, const int32_t* threshold, const int32_t* left_abs,
+                     const int32_t* right_abs, const float* value, const uint8_t* is_leaf,
+                     const int32_t* offsets, int32_t T, int32_t total_nodes, pb_forest** out) {
+    if (!out) return fail(PB_ERR_INVALID, "pb_forest_create: null output");
+    *out = nullptr;
+    if (T < 0 || total_nodes < 0) return fail(PB_ERR_INVALID, "pb_forest_create: bad shape");
+    if (T > 0 && (!feature || !threshold || !left_abs || !right_abs || !value || !is_leaf || !offsets))
+        return fail(PB_ERR_INVALID, "pb_forest_create: null argument");
+    std::vector<int32_t> f(total_nodes), th(total_nodes), l(total_nodes), r(total_nodes), off(T + 1);
+    std::vector<float> v(total_nodes);
+    std::vector<uint8_t> lf(total_nodes);
+    if (T > 0) {
+        PB_HIP(hipMemcpy(off.data(), offsets, sizeof(int32_t) * (T + 1), hipMemcpyDeviceToHost), "forest copy");
+        if (total_nodes > 0) {
+            PB_HIP(hipMemcpy(f.data(), feature, 4 * (size_t)total_nodes, hipMemcpyDeviceToHost), "forest copy");
+            PB_HIP(hipMemcpy(th.data(), threshold, 4 * (size_t)total_nodes, hipMemcpyDeviceToHost), "forest copy");
+            PB_HIP(hipMemcpy(l.data(), left_abs, 4 * (size_t)total_nodes, hipMemcpyDeviceToHost), "forest copy");
+            PB_HIP(hipMemcpy(r.data(), right_abs, 4 * (size_t)total_nodes, hipMemcpyDeviceToHost), "forest copy");
+            PB_HIP(hipMemcpy(v.data(), value, 4 * (size_t)total_nodes, hipMemcpyDeviceToHost), "forest copy");
+            PB_HIP(hipMemcpy(lf.data(), is_leaf, (size_t)total_nodes, hipMemcpyDeviceToHost), "forest copy");
+        }
+    }
+    auto* fo = new pb_forest();
+    fo->T = T;
+    fo->total_nodes = total_nodes;
+    std::vector<int4> rec(std::max(1, total_nodes));
+    std::vector<int32_t> roots(std::max(1, T));
+    std::vector<int32_t> depth(total_nodes, -1);
+    for (int t = 0; t < T; ++t) {
+        const int lo = off[t], hi = off[t + 1];
+        if (lo < 0 || hi > total_nodes || hi <= lo) {
+            delete fo;
+            return fail(PB_ERR_INVALID, "pb_forest_create: bad tree offsets");
+        }
+        roots[t] = lo;
+        // breadth-first from the root: every reachable node once, children inside the tree
+        std::vector<int32_t> q{lo};
+        depth[lo] = 0;
+        for (size_t k = 0; k < q.size(); ++k) {
+            const int n = q[k];
+            if (lf[n]) {
+                rec[n] = make_int4((int)pb::kLeafFeatureBits, n, n, __builtin_bit_cast(int, v[n]));
+                fo->depth = std::max(fo->depth, depth[n]);
+                continue;
+            }
+            const int fe = f[n], tr = th[n], a = l[n], b = r[n];
+            if (fe < 0 || fe >= (1 << 24) - 1 || tr < 0 || tr > 255 || a < lo || a >= hi || b < lo ||
+                b >= hi || depth[a] >= 0 || depth[b] >= 0 || a == b) {
+                delete fo;
+                return fail(PB_ERR_INVALID, "pb_forest_create: malformed tree (feature, threshold "
+                                            "or child out of range, or a cycle)");
+            }
+            fo->max_feature = std::max(fo->max_feature, fe);
+            rec[n] = make_int4((int)((uint32_t)fe | ((uint32_t)tr << 24)), a, b, 0);
+            depth[a] = depth[b] = depth[n] + 1;
+            q.push_back(a);
+            q.push_back(b);
+        }
+    }
+    if (hipMalloc(&fo->rec, sizeof(int4) * rec.size()) != hipSuccess ||
+        hipMalloc(&fo->roots, sizeof(int32_t) * roots.size()) != hipSuccess) {
+        (void)hipFree(fo->rec);
+        (void)hipFree(fo->roots);
+        delete fo;
+        return fail(PB_ERR_NOMEM, "pb_forest_create: device allocation failed");
+    }
+    hipError_t e1 = hipMemcpy(fo->rec, rec.data(), sizeof(int4) * rec.size(), hipMemcpyHostToDevice);
+    hipError_t e2 = hipMemcpy(fo->roots, roots.data(), sizeof(int32_t) * roots.size(), hipMemcpyHostToDevice);
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+        (void)hipFree(fo->rec);
+        (void)hipFree(fo->roots);
+        delete fo;
+        return hip_fail(e1 != hipSuccess ? e1 : e2, "forest upload");
+    }
+    *out = fo;
+    return PB_OK;
+}
+
+int pb_forest_predict(const pb_forest* fo, const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                      float tree_weight, float* out, int32_t* leaf, void* stream) {
+    if (!fo) return fail(PB_ERR_INVALID, "pb_forest_predict: null forest");
+    if (N < 0 || ld < N || F < 1) return fail(PB_ERR_INVALID, "pb_forest_predict: bad shape");
+    if (fo->max_feature >= F)
+        return fail(PB_ERR_RANGE, "pb_forest_predict: the forest splits on a feature >= F");
+    if (N == 0) return PB_OK;
+    if (!bins || !out) return fail(PB_ERR_INVALID, "pb_forest_predict: null argument");
+    if (fo->T == 0) {
+        PB_HIP(hipMemsetAsync(out, 0, sizeof(float) * (size_t)N, (hipStream_t)stream), "zero predictions");
+        return PB_OK;
+    }
+    static const int32_t group = (int32_t)env_int("PB_FOREST_GROUP", 8);
+    static const int32_t max_grid = (int32_t)env_int("PB_FOREST_GRID", 0);
+    PB_HIP(pb::launch_forest(bins, N, ld, fo->rec, fo->roots, fo->T, fo->depth, tree_weight, out, leaf,
+                             group, max_grid, (hipStream_t)stream),
+           "forest launch");
+    return PB_OK;
+}
+
+int pb_forest_destroy(pb_forest* fo) {
+    if (!fo) return PB_OK;
+    (void)hipFree(fo->rec);
+    (void)hipFree(fo->roots);
+    delete fo;
+    return PB_OK;
+}
+
 int pb_predict_bins(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const int32_t* feature,
                     const int32_t* threshold, const int32_t* left, const int32_t* right,
                     const float* value, const uint8_t* is_leaf, int32_t num_nodes, float* out,

@@ -12,6 +12,7 @@ constexpr int kWave = 64;          // CDNA wavefront width
 constexpr int kBlock = 256;        // threads per workgroup for the row kernels
 constexpr int kCountBits = 16;     // low bits of a histogram word hold the row count
 constexpr int kMaxEraRowsDirect = (1 << kCountBits) - 1;
+constexpr uint32_t kLeafFeatureBits = 0xFFFFFFu;  // compiled-forest leaf marker
 constexpr int kGradScaleLog2 = 30; // |grad| * scale < 2^30 -> fixed point fits int32 per row
 
 // Frontier state of the round in flight; lives in device memory and is only written
@@ -123,6 +124,10 @@ hipError_t launch_apply_bins(const float* xt, int64_t n, int64_t ld_x, int32_t F
                              const int64_t* perm, uint8_t* bins, int64_t ld_out, hipStream_t s);
 hipError_t launch_era_corr(const float* y, const float* p, const int32_t* era_off, int32_t E,
                            double* era_corr, double* out, hipStream_t s);
+hipError_t launch_forest(const uint8_t* bins, int64_t N, int64_t ld, const int4* rec,
+                         const int32_t* roots, int32_t T, int32_t depth, float tree_weight,
+                         float* out, int32_t* leaf, int32_t group, int32_t max_grid,
+                         hipStream_t s);
 hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
                                const int32_t* feature, const int32_t* threshold,
                                const int32_t* left_abs, const int32_t* right_abs,

@@ -11,6 +11,8 @@
 //
 // One lane per row: a wavefront reads 64 consecutive rows of the same column while its rows
 // sit in the same node, and the forest arrays are small enough to stay in L2.
+#include <algorithm>
+
 #include "pb_internal.h"
 
 namespace pb {
@@ -77,6 +79,50 @@ __global__ __launch_bounds__(kBlock) void predict_bins_kernel(
     }
 }
 
+// Compiled forest: one 16-byte record per node {feature | threshold << 24, left, right,
+// value bits}; a leaf has feature field 0xFFFFFF. A lane walks kTreeGroup trees at once, all
+// one level per step, so their record and bin loads overlap; the leaf values are then added
+// in tree order, one float32 rounding per product and per add (PackBoost.predict's order).
+// The grid can be capped so that the rows in flight keep their bins in the caches.
+constexpr uint32_t kLeafFeature = kLeafFeatureBits;
+
+template <int kTreeGroup>
+__global__ __launch_bounds__(kBlock) void forest_kernel(
+    const uint8_t* __restrict__ bins, int64_t N, int64_t ld, const int4* __restrict__ rec,
+    const int32_t* __restrict__ roots, int32_t T, int32_t depth, float tree_weight,
+    float* __restrict__ out, int32_t* __restrict__ leaf) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x; r < N; r += stride) {
+        float s = 0.0f;
+        for (int t0 = 0; t0 < T; t0 += kTreeGroup) {
+            int node[kTreeGroup];
+#pragma unroll
+            for (int j = 0; j < kTreeGroup; ++j) node[j] = roots[min(t0 + j, T - 1)];
+            for (int lvl = 0; lvl < depth; ++lvl) {
+#pragma unroll
+                for (int j = 0; j < kTreeGroup; ++j) {
+                    const int4 q = rec[node[j]];
+                    const uint32_t f = (uint32_t)q.x & 0xFFFFFFu;
+                    if (f != kLeafFeature) {
+                        const uint32_t thr = (uint32_t)q.x >> 24;
+                        const uint32_t b = bins[(int64_t)f * ld + r];
+                        node[j] = (b <= thr) ? q.y : q.z;
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < kTreeGroup; ++j) {
+                if (t0 + j < T) {
+                    const float v = __int_as_float(rec[node[j]].w);
+                    s = s + tree_weight * v;
+                    if (leaf) leaf[(int64_t)(t0 + j) * N + r] = node[j];
+                }
+            }
+        }
+        out[r] = s;
+    }
+}
+
 int grid_rows(int64_t N) {
     int64_t g = (N + kBlock - 1) / kBlock;
     if (g < 1) g = 1;
@@ -97,6 +143,32 @@ hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32
     hipLaunchKernelGGL(predict_pack_kernel, dim3(grid_rows(N)), dim3(kBlock), 0, s, bins, N, ld,
                        F, feature, threshold, left_abs, right_abs, value, is_leaf, offsets, B,
                        tree_weight, sequential, out, leaf);
+    return hipGetLastError();
+}
+
+hipError_t launch_forest(const uint8_t* bins, int64_t N, int64_t ld, const int4* rec,
+                         const int32_t* roots, int32_t T, int32_t depth, float tree_weight,
+                         float* out, int32_t* leaf, int32_t group, int32_t max_grid,
+                         hipStream_t s) {
+    int grid = grid_rows(N);
+    if (max_grid > 0) grid = std::min(grid, max_grid);
+    switch (group) {
+        case 4:
+            hipLaunchKernelGGL(forest_kernel<4>, dim3(grid), dim3(kBlock), 0, s, bins, N, ld, rec,
+                               roots, T, depth, tree_weight, out, leaf);
+            break;
+        case 16:
+            hipLaunchKernelGGL(forest_kernel<16>, dim3(grid), dim3(kBlock), 0, s, bins, N, ld, rec,
+                               roots, T, depth, tree_weight, out, leaf);
+            break;
+        case 32:
+            hipLaunchKernelGGL(forest_kernel<32>, dim3(grid), dim3(kBlock), 0, s, bins, N, ld, rec,
+                               roots, T, depth, tree_weight, out, leaf);
+            break;
+        default:
+            hipLaunchKernelGGL(forest_kernel<8>, dim3(grid), dim3(kBlock), 0, s, bins, N, ld, rec,
+                               roots, T, depth, tree_weight, out, leaf);
+    }
     return hipGetLastError();
 }
 

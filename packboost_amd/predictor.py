@@ -16,8 +16,9 @@ advertises `PackBoostPredictor`). The bundle here is one `.npz` (no pickles; loa
                                TreeBuilder numbering, children relative to the tree
 
 `PackBoostPredictor.predict` expands the rounds into the packed forest of booster.py:730-783
-(B copies per round, absolute child indices) and runs pb_predict_forest, which sums the trees
-in PackBoost.predict's order (booster.py:709-712): its output is bit-identical to the trainer's.
+(B copies per round, absolute child indices), compiles it once (pb_forest_create) and runs
+pb_forest_predict, which sums the trees in PackBoost.predict's order (booster.py:709-712): its
+output is bit-identical to the trainer's.
 """
 
 from __future__ import annotations
@@ -100,6 +101,46 @@ def load_bundle(path: str | Path) -> dict:
     return d
 
 
+class CompiledForest:
+    """A packed forest (booster.pack_forest arrays) compiled into device node records
+    (pb_forest_create); predict() equals pb_predict_forest bit for bit."""
+
+    def __init__(self, forest: dict[str, torch.Tensor]) -> None:
+        import ctypes
+
+        self._lib = _hip.load()
+        self.T = int(forest["offsets"].numel() - 1)
+        h = ctypes.c_void_p()
+        _hip.check(self._lib.pb_forest_create(
+            forest["feature"].data_ptr(), forest["threshold"].data_ptr(),
+            forest["left_abs"].data_ptr(), forest["right_abs"].data_ptr(),
+            forest["value"].data_ptr(), forest["is_leaf"].data_ptr(), forest["offsets"].data_ptr(),
+            self.T, int(forest["value"].numel()), ctypes.byref(h)), "pb_forest_create")
+        self._h = h
+        self.offsets = forest["offsets"]
+
+    def predict(self, bins_fm: torch.Tensor, n: int, tree_weight: float,
+                leaves: torch.Tensor | None = None) -> torch.Tensor:
+        out = torch.empty(n, dtype=torch.float32, device=bins_fm.device)
+        _hip.check(self._lib.pb_forest_predict(
+            self._h, bins_fm.data_ptr(), n, bins_fm.shape[1], bins_fm.shape[0], float(tree_weight),
+            out.data_ptr(), None if leaves is None else leaves.data_ptr(), _hip.stream_ptr()),
+            "pb_forest_predict")
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            torch.cuda.synchronize()
+            self._lib.pb_forest_destroy(self._h)
+            self._h = None
+
+    def __del__(self) -> None:  # pragma: no cover - best effort
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class PackBoostPredictor:
     """Inference-only view of a fitted model: a bundle path, a loaded bundle, or a model."""
 
@@ -141,6 +182,11 @@ class PackBoostPredictor:
             self._forest = pack_forest(self.rounds, self.pack_size, self.device)
         return self._forest
 
+    def _compiled(self) -> CompiledForest:
+        if getattr(self, "_cforest", None) is None:
+            self._cforest = CompiledForest(self._packed())
+        return self._cforest
+
     def _bins_fm(self, X) -> tuple[torch.Tensor, int]:
         from .booster import _bins_fm_for
 
@@ -154,16 +200,7 @@ class PackBoostPredictor:
         bins_fm, n = self._bins_fm(X)
         if not self.rounds or n == 0:
             return np.zeros(n, dtype=np.float32)
-        f = self._packed()
-        out = torch.empty(n, dtype=torch.float32, device=self.device)
-        lib = _hip.load()
-        _hip.check(lib.pb_predict_forest(
-            bins_fm.data_ptr(), n, bins_fm.shape[1], bins_fm.shape[0], f["feature"].data_ptr(),
-            f["threshold"].data_ptr(), f["left_abs"].data_ptr(), f["right_abs"].data_ptr(),
-            f["value"].data_ptr(), f["is_leaf"].data_ptr(), f["offsets"].data_ptr(),
-            int(f["offsets"].numel() - 1), int(f["value"].numel()), float(self.tree_weight),
-            out.data_ptr(), _hip.stream_ptr()), "pb_predict_forest")
-        return out.cpu().numpy()
+        return self._compiled().predict(bins_fm, n, self.tree_weight).cpu().numpy()
 
     def predict_leaves(self, X) -> np.ndarray:
         """int32 [num_trees, N]: each tree's leaf, as a node index within that tree."""
@@ -171,15 +208,8 @@ class PackBoostPredictor:
         T = self.num_trees
         if T == 0 or n == 0:
             return np.zeros((T, n), dtype=np.int32)
-        f = self._packed()
+        cf = self._compiled()
         leaf = torch.empty((T, n), dtype=torch.int32, device=self.device)
-        out = torch.empty(n, dtype=torch.float32, device=self.device)
-        lib = _hip.load()
-        _hip.check(lib.pb_predict_pack(
-            bins_fm.data_ptr(), n, bins_fm.shape[1], bins_fm.shape[0], f["feature"].data_ptr(),
-            f["threshold"].data_ptr(), f["left_abs"].data_ptr(), f["right_abs"].data_ptr(),
-            f["value"].data_ptr(), f["is_leaf"].data_ptr(), f["offsets"].data_ptr(), T,
-            int(f["value"].numel()), float(self.tree_weight), out.data_ptr(), leaf.data_ptr(),
-            _hip.stream_ptr()), "pb_predict_pack")
-        offs = f["offsets"][:-1].to(torch.int32)[:, None]
+        cf.predict(bins_fm, n, self.tree_weight, leaves=leaf)
+        offs = cf.offsets[:-1].to(torch.int32)[:, None]
         return (leaf - offs).cpu().numpy()
