@@ -28,6 +28,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+PROFILE_EVERY = 4  # timed rounds whose histogram launches carry HIP timing events
 METRIC = "boosting rounds/sec (B=8,D=6, 2.4M×2376) on 1 GPU; hist-build HBM GB/s"
 
 CONFIGS = {
@@ -277,31 +278,42 @@ def main() -> int:
     for log, _, _ in fit.rounds(rng, args.warmup):
         tree_arrays_from_log(log, cfg, N)
     torch.cuda.synchronize()
-    # per-phase GPU time from HIP events the library records on the fit's stream
-    _hip.check(fit.lib.pb_profile_enable(fit.ctx, 1), "pb_profile_enable")
+    D = fit.D
+
+    def read_profile():
+        ms = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.float64)
+        n = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.int64)
+        _hip.check(fit.lib.pb_profile_read(fit.ctx, ms.ctypes.data, n.ctypes.data), "pb_profile_read")
+        return ms.reshape(4, -1)[:, :D], n.reshape(4, -1)[:, :D]
+
+    # Timed region: the histogram launches of every PROFILE_EVERY-th round are bracketed by HIP
+    # events on the fit's stream (each event is a queue barrier, so only those rounds pay it).
     logs = []
     t0 = time.perf_counter()
-    for log, _, _ in fit.rounds(rng, args.steps):
+    for log, _, _ in fit.rounds(rng, args.steps, profile_every=PROFILE_EVERY, profile_mode=2):
         tree_arrays_from_log(log, cfg, N)
         logs.append(log)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
-    D = fit.D
-    prof_ms = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.float64)
-    prof_n = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.int64)
-    _hip.check(fit.lib.pb_profile_read(fit.ctx, prof_ms.ctypes.data, prof_n.ctypes.data),
-               "pb_profile_read")
-    prof_ms = prof_ms.reshape(4, -1)[:, :D]
-    prof_n = prof_n.reshape(4, -1)[:, :D]
+    prof_ms, prof_n = read_profile()
+    # Untimed: every phase of a few more rounds, for the per-phase breakdown.
+    n_phase = min(args.steps, 20)
+    for log, _, _ in fit.rounds(rng, n_phase, profile_every=1, profile_mode=1):
+        tree_arrays_from_log(log, cfg, N)
+    torch.cuda.synchronize()
+    phase_raw, _ = read_profile()
 
     # histogram roofline: algorithmic bytes per launch = rows of active nodes x K bin bytes
-    # + rows x 6 (grad f32 + node id u16) + written planes U x E x K x nb x 8
+    # + rows x 6 (grad f32 + node id u16) + written planes U x E x K x nb x 8, summed over
+    # the profiled rounds
     K, E, nb = fit.K, fit.E, fit.nb
-    phase_ms = {name: float(prof_ms[i].sum()) for i, name in
+    phase_ms = {name: float(phase_raw[i].sum()) for i, name in
                 enumerate(("hist", "score", "decide", "partition"))}
     hist_bytes = 0.0
-    for log in logs:
+    for r, log in enumerate(logs):
+        if r % PROFILE_EVERY:
+            continue
         for d in range(D):
             u = int(log.u_active[d])
             if u == 0:
@@ -349,7 +361,9 @@ def main() -> int:
             "avg_launch_ms": round(hist_ms / max(n_hist, 1), 4),
             "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
         },
-        "phase_ms_per_round": {k: round(v / args.steps, 4) for k, v in phase_ms.items()},
+        "profiled_rounds": {"hist_events": f"every {PROFILE_EVERY}th timed round",
+                            "phase_breakdown": f"{n_phase} untimed rounds"},
+        "phase_ms_per_round": {k: round(v / n_phase, 4) for k, v in phase_ms.items()},
         "hist_ms_per_depth": [round(float(prof_ms[0, d]) / max(1, int(prof_n[0, d])), 4)
                               for d in range(D)],
         "cpu_baseline": None,

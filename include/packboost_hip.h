@@ -207,12 +207,13 @@ typedef struct {
 int pb_grow_round(pb_ctx* ctx, const pb_fit_buffers* buffers, const int32_t* feats_dev, int32_t K,
                   pb_decision* decisions_dev, pb_round_header* header_dev, void* stream);
 
-/* GPU time of every phase of pb_grow_round, from HIP events recorded on the launch stream
+/* GPU time of the phases of pb_grow_round, from HIP events recorded on the launch stream
  * around each depth's hist / score / decide / partition launches (the device-side analogue of
  * the per-depth hist_ms / scan_ms / score_ms / partition_ms instrumentation,
- * booster.py:220-270). pb_profile_read waits for the recorded rounds, fills
- * ms[phase * PB_MAX_DEPTH + depth] (phase 0 hist, 1 score, 2 decide, 3 partition) and the
- * matching launch counts, and clears them. */
+ * booster.py:220-270). enable: 0 off, 1 every phase, 2 the histogram launches only (two
+ * events per depth instead of five: each recorded event is a queue barrier). pb_profile_read
+ * waits for the recorded rounds, fills ms[phase * PB_MAX_DEPTH + depth] (phase 0 hist,
+ * 1 score, 2 decide, 3 partition) and the matching launch counts, and clears them. */
 int pb_profile_enable(pb_ctx* ctx, int32_t enable);
 int pb_profile_read(pb_ctx* ctx, double* ms, int64_t* launches);
 

@@ -40,7 +40,7 @@ struct pb_ctx {
     int32_t hist_rounds;
     // phase timing of pb_grow_round (pb_profile_enable): per depth, 5 events bracket the
     // hist / score / decide / partition launches on the caller's stream
-    bool profile;
+    int32_t profile;  // 0 off, 1 every phase, 2 the histogram only
     std::vector<hipEvent_t> ev_free;
     std::vector<std::pair<int32_t, std::array<hipEvent_t, 5>>> ev_pending;
 };
@@ -108,7 +108,8 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
     for (auto& p : c->ev_pending)
-        for (hipEvent_t e : p.second) c->ev_free.push_back(e);
+        for (hipEvent_t e : p.second)
+            if (e) c->ev_free.push_back(e);
     for (hipEvent_t e : c->ev_free) (void)hipEventDestroy(e);
     delete c;
 }
@@ -429,9 +430,11 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
         const int32_t m = max_nodes_at(c, d);
         const int32_t* f = feats + (int64_t)d * K;
         std::array<hipEvent_t, 5> ev{};
-        const bool prof = c->profile;
+        const bool prof = c->profile != 0;
+        const int n_ev = c->profile == 2 ? 2 : 5;  // hist only: events 0 and 1
         if (prof) {
-            for (auto& e : ev) {
+            for (int i = 0; i < n_ev; ++i) {
+                hipEvent_t& e = ev[i];
                 if (!c->ev_free.empty()) {
                     e = c->ev_free.back();
                     c->ev_free.pop_back();
@@ -442,7 +445,7 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
             c->ev_pending.emplace_back(d, ev);
         }
         auto mark = [&](int i) -> int {
-            if (prof) PB_HIP(hipEventRecord(ev[i], (hipStream_t)stream), "profile event record");
+            if (prof && i < n_ev) PB_HIP(hipEventRecord(ev[i], (hipStream_t)stream), "profile event record");
             return PB_OK;
         };
         if ((rc = mark(0))) return rc;
@@ -466,7 +469,8 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
 
 int pb_profile_enable(pb_ctx* c, int32_t enable) {
     if (!c) return fail(PB_ERR_INVALID, "pb_profile_enable: null context");
-    c->profile = enable != 0;
+    if (enable < 0 || enable > 2) return fail(PB_ERR_INVALID, "pb_profile_enable: mode must be 0, 1 or 2");
+    c->profile = enable;
     return PB_OK;
 }
 
@@ -480,11 +484,12 @@ int pb_profile_read(pb_ctx* c, double* ms, int64_t* launches) {
     for (auto& p : c->ev_pending) {
         const int d = p.first;
         auto& ev = p.second;
+        const int n_ph = ev[4] ? 4 : 1;  // hist-only entries hold events 0 and 1
         if (rc == PB_OK) {
-            hipError_t e = hipEventSynchronize(ev[4]);
+            hipError_t e = hipEventSynchronize(ev[n_ph]);
             if (e != hipSuccess) rc = hip_fail(e, "profile event sync");
         }
-        for (int ph = 0; ph < 4 && rc == PB_OK; ++ph) {
+        for (int ph = 0; ph < n_ph && rc == PB_OK; ++ph) {
             float t = 0.f;
             hipError_t e = hipEventElapsedTime(&t, ev[ph], ev[ph + 1]);
             if (e != hipSuccess) {
@@ -494,7 +499,8 @@ int pb_profile_read(pb_ctx* c, double* ms, int64_t* launches) {
             ms[ph * PB_MAX_DEPTH + d] += t;
             launches[ph * PB_MAX_DEPTH + d] += 1;
         }
-        for (hipEvent_t e : ev) c->ev_free.push_back(e);
+        for (hipEvent_t e : ev)
+            if (e) c->ev_free.push_back(e);
     }
     c->ev_pending.clear();
     return rc;

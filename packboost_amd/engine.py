@@ -260,8 +260,13 @@ class DeviceFit:
         return RoundLog(u_active=u[: self.D + 1].copy(), tree_size=int(hdr["tree_size"]),
                         decisions=dec, root_grad=float(dec[0]["node_grad"]), depths_drawn=drawn)
 
-    def rounds(self, rng: torch.Generator, num_rounds: int):
+    def rounds(self, rng: torch.Generator, num_rounds: int, *, profile_every: int = 0,
+               profile_mode: int = 2):
         """Runs `num_rounds` rounds with the host one round ahead of the GPU.
+
+        profile_every > 0 turns the library's phase timing (pb_profile_enable, mode
+        `profile_mode`) on for every profile_every-th round only, so that the events' queue
+        barriers touch few rounds.
 
         Yields (RoundLog, preds_after, ready) per round in order. `preds_after` holds the
         predictions after that round until the consumer resumes the generator (the GPU may
@@ -281,7 +286,13 @@ class DeviceFit:
             return
         if num_rounds <= 0:
             return
+        def set_profile(r: int) -> None:
+            if profile_every > 0:
+                on = profile_mode if r % profile_every == 0 else 0
+                _hip.check(self.lib.pb_profile_enable(self.ctx, on), "pb_profile_enable")
+
         subs, states = self.draw_subsets(rng)
+        set_profile(0)
         self.enqueue_grow(subs, 0)
         for r in range(num_rounds):
             slot = r & 1
@@ -291,6 +302,7 @@ class DeviceFit:
                     self.preds_snap.copy_(self.preds)
                 ready = now()
                 subs_n, states_n = self.draw_subsets(rng)
+                set_profile(r + 1)
                 self.enqueue_grow(subs_n, slot ^ 1)
             log = self.read_slot(slot)
             if log.depths_drawn < self.D:
@@ -301,10 +313,13 @@ class DeviceFit:
                     with torch.cuda.stream(self.stream):
                         self.preds.copy_(self.preds_snap)
                     subs_n, states_n = self.draw_subsets(rng)
+                    set_profile(r + 1)
                     self.enqueue_grow(subs_n, slot ^ 1)
             if ahead:
                 yield log, self.preds_snap, ready
             else:
+                if profile_every > 0:
+                    _hip.check(self.lib.pb_profile_enable(self.ctx, 0), "pb_profile_enable")
                 yield log, self.preds, now()
             if ahead:
                 states = states_n

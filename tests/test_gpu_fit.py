@@ -128,3 +128,49 @@ def test_early_stopping_rounds(hip, oracle_mod, msl):
     if msl == 150:
         assert max(int(np.count_nonzero(~np.asarray(r["is_leaf"]))) for r in ref.rounds) > 0
         assert all(int(np.count_nonzero(~np.asarray(r["is_leaf"]))) < 63 for r in ref.rounds)
+
+
+def test_profile_modes(hip):
+    """pb_profile_enable: mode 2 times the histogram launches only, mode 1 every phase; the
+    events change no result (same trees as an unprofiled run)."""
+    import ctypes
+
+    import torch
+    from packboost_amd import PackBoostConfig
+    from packboost_amd.backends import _hip
+    from packboost_amd.data import preprocess_features
+    from packboost_amd.engine import DeviceFit, tree_arrays_from_log
+
+    X, y, era = config1_data(seed=4, n=4096, f=12, eras=4)
+    cfg = PackBoostConfig(pack_size=2, max_depth=4, learning_rate=0.1, min_samples_leaf=8,
+                          max_bins=31, random_state=3, prebinned=True)
+    bins = preprocess_features(X, cfg.max_bins).bins
+    dev = torch.device("cuda")
+    bins_fm = torch.from_numpy(np.ascontiguousarray(bins.T)).to(dev)
+    off = np.array([0, 1024, 2048, 3072, 4096], np.int32)
+    D, P = cfg.max_depth, _hip.PB_MAX_DEPTH
+
+    def run(every, mode):
+        fit = DeviceFit(bins_fm, 4096, torch.from_numpy(y).to(dev), off, cfg)
+        trees = [tree_arrays_from_log(log, cfg, 4096)
+                 for log, _, _ in fit.rounds(torch.Generator().manual_seed(1), 5,
+                                             profile_every=every, profile_mode=mode)]
+        torch.cuda.synchronize()
+        ms = np.zeros(4 * P, np.float64)
+        n = np.zeros(4 * P, np.int64)
+        _hip.check(fit.lib.pb_profile_read(fit.ctx, ms.ctypes.data, n.ctypes.data), "read")
+        assert fit.lib.pb_profile_enable(fit.ctx, 3) < 0  # modes are 0, 1, 2
+        fit.close()
+        return trees, ms.reshape(4, P)[:, :D], n.reshape(4, P)[:, :D]
+
+    base, _, n0 = run(0, 0)
+    assert n0.sum() == 0
+    hist_only, ms2, n2 = run(2, 2)
+    all_ph, ms1, n1 = run(1, 1)
+    assert n2[0, 0] == 3 and n2[1:].sum() == 0  # rounds 0, 2, 4
+    assert (ms2[0][n2[0] > 0] > 0).all()
+    assert n1[0, 0] == 5 and (n1[:, 0] == 5).all() and (ms1[:, 0] > 0).all()
+    for a, b, c in zip(base, hist_only, all_ph):
+        for key in ("feature", "threshold", "left", "right", "is_leaf", "value"):
+            np.testing.assert_array_equal(np.asarray(a[key]), np.asarray(b[key]))
+            np.testing.assert_array_equal(np.asarray(a[key]), np.asarray(c[key]))
