@@ -305,9 +305,10 @@ def main() -> int:
     phase_raw, _ = read_profile()
 
     # histogram roofline: algorithmic bytes per launch = rows of active nodes x K bin bytes
-    # + rows x 6 (grad f32 + node id u16) + written planes U x E x K x nb x 8, summed over
-    # the profiled rounds
+    # (1 per row, 1/2 in the nibble layout) + rows x 6 (grad f32 + node id u16) + written
+    # planes U x E x K x nb x 8, summed over the profiled rounds
     K, E, nb = fit.K, fit.E, fit.nb
+    bin_bytes = 0.5 if fit.bins4 is not None else 1.0
     phase_ms = {name: float(phase_raw[i].sum()) for i, name in
                 enumerate(("hist", "score", "decide", "partition"))}
     hist_bytes = 0.0
@@ -320,7 +321,7 @@ def main() -> int:
                 continue
             base = (1 << d) - 1
             rows = int(log.decisions[base: base + u]["node_count"].astype(np.int64).sum())
-            hist_bytes += rows * K + rows * 6 + u * E * K * nb * 8
+            hist_bytes += rows * K * bin_bytes + rows * 6 + u * E * K * nb * 8
     hist_ms = float(prof_ms[0].sum())
     n_hist = int(prof_n[0].sum())
     achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
@@ -358,6 +359,7 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": profiled_traffic(args.config, N),
             "kernel": "hist_era_kernel",
+            "bin_layout": "nibble" if fit.bins4 is not None else "u8",
             "avg_launch_ms": round(hist_ms / max(n_hist, 1), 4),
             "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
         },

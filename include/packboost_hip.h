@@ -186,6 +186,9 @@ typedef struct {
  * entries; hist planes hold pb_hist_plane_elems(ctx, pb_max_nodes(ctx, D-1)) entries. */
 typedef struct {
     const uint8_t* bins_dev;     /* [F][ld] column-major */
+    const uint8_t* bins4_dev;    /* NULL, or the same bins in the nibble layout of
+                                  * pb_pack_bins4 ([F][ld / 2], max_bins <= 16): the
+                                  * histogram and partition read it instead of bins_dev */
     const float* y_dev;
     float* preds_dev;
     float* grad_dev;
@@ -237,6 +240,21 @@ int pb_frontier_counts(pb_ctx* ctx, int32_t* u_active_host, int32_t* tree_size_h
 int pb_quantile_edges(const float* sorted_dev, int64_t n, int64_t ld, int32_t F,
                       const double* q_dev, int32_t num_q, float* edges_dev, int32_t edge_stride,
                       void* stream);
+
+/* Layout of the bins_dev that pb_hist_build and pb_partition read: 0 = uint8 [F][ld] (the
+ * default), 1 = the nibble layout of pb_pack_bins4 ([F][ld / 2], max_bins <= 16). The
+ * reference's per-depth kernels take int8 feature-major bins only (frontier_cuda.cu:576-716,
+ * 719-851); pb_grow_round picks its layout from pb_fit_buffers instead. */
+int pb_set_bin_layout(pb_ctx* ctx, int32_t layout);
+
+/* Nibble layout of the frontier kernels' feature-major bins (the reference builds
+ * bins.t().contiguous() as int8 [F][N], booster.py:419-426): out_dev[f][ld / 2] receives, for
+ * every 8 rows, one 4-byte word whose byte j holds row j in its low and row j + 4 in its high
+ * nibble; rows n .. ld-1 are written as 0. For max_bins <= 16 (bins must be < 16);
+ * pb_fit_buffers.bins4_dev takes the result and halves the bin bytes the histogram reads.
+ * ld % 16 == 0, 0 <= n <= ld; bins_dev 16-byte aligned, out_dev 8-byte aligned. */
+int pb_pack_bins4(const uint8_t* bins_dev, int64_t n, int64_t ld, int32_t F, uint8_t* out_dev,
+                  void* stream);
 
 /* apply_bins (data.py:93-111): bins[f][r] = min(searchsorted(edges[:, f], x, side="left"),
  * max_bins - 1) with NumPy's NaN-last order, x = xt[f][perm ? perm[r] : r] (xt: float32

@@ -28,7 +28,8 @@ EXPORTED_SYMBOLS = (
     "pb_partition", "pb_round_end", "pb_grow_round", "pb_profile_enable",
     "pb_profile_read", "pb_frontier_set", "pb_frontier_counts", "pb_predict_pack",
     "pb_predict_forest", "pb_predict_bins", "pb_era_corr", "pb_quantile_edges", "pb_apply_bins",
-    "pb_forest_create", "pb_forest_predict", "pb_forest_destroy",
+    "pb_forest_create", "pb_forest_predict", "pb_forest_destroy", "pb_pack_bins4",
+    "pb_set_bin_layout",
 )
 
 
@@ -55,7 +56,8 @@ class PbSplitParams(ctypes.Structure):
 
 class PbFitBuffers(ctypes.Structure):
     _fields_ = [
-        ("bins_dev", ctypes.c_void_p), ("y_dev", ctypes.c_void_p), ("preds_dev", ctypes.c_void_p),
+        ("bins_dev", ctypes.c_void_p), ("bins4_dev", ctypes.c_void_p),
+        ("y_dev", ctypes.c_void_p), ("preds_dev", ctypes.c_void_p),
         ("grad_dev", ctypes.c_void_p), ("nid_dev", ctypes.c_void_p), ("tnode_dev", ctypes.c_void_p),
         ("hist_cnt_dev", ctypes.c_void_p), ("hist_grad_dev", ctypes.c_void_p),
         ("values_dev", ctypes.c_void_p), ("pack_size", ctypes.c_int32),
@@ -108,6 +110,8 @@ _SIGNATURES = {
     "pb_forest_destroy": (ctypes.c_int, [_VP]),
     "pb_quantile_edges": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _VP, _I32, _VP]),
     "pb_apply_bins": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _I32, _I32, _VP, _VP, _I64, _VP]),
+    "pb_pack_bins4": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _VP]),
+    "pb_set_bin_layout": (ctypes.c_int, [_VP, _I32]),
     "pb_profile_read": (ctypes.c_int, [_VP, _VP, _VP]),
     "pb_frontier_set": (ctypes.c_int, [_VP, _I32, _I32, _VP, _I32, _VP]),
     "pb_frontier_counts": (ctypes.c_int, [_VP, _VP, _VP, _VP]),

@@ -10,6 +10,8 @@
 //  * bins: searchsorted(edges, x, side="left") clipped to [0, max_bins - 1], with NumPy's
 //    NaN-last order (NaN > every number), written column-major for the histogram kernel,
 //    optionally gathering rows through a permutation (era-major order).
+#include <algorithm>
+
 #include "pb_internal.h"
 
 namespace pb {
@@ -81,7 +83,47 @@ __global__ __launch_bounds__(kBlock) void apply_bins_kernel(
     }
 }
 
+// Nibble layout for nb <= 16: every 8 rows of a uint8 column (bytes b0..b7) become one dword
+// whose byte j is b_j | b_{j+4} << 4. One thread converts 16 rows (one 16-byte load, one
+// 8-byte store); bins above 15 lose their high bits (callers guarantee bins < nb <= 16).
+// Rows n .. ld-1 (padding) are written as bin 0: the histogram reads them unmasked.
+__global__ __launch_bounds__(kBlock) void pack_bins4_kernel(const uint8_t* __restrict__ bins,
+                                                         int64_t ld, int64_t n,
+                                                         int64_t units_per_col, int64_t units,
+                                                         uint8_t* __restrict__ out) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < units; t += stride) {
+        const int64_t f = t / units_per_col;
+        const int64_t u = t - f * units_per_col;
+        uint4 v = *reinterpret_cast<const uint4*>(bins + f * ld + u * 16);
+        const int64_t r0 = u * 16;  // first row of this unit
+        if (r0 + 16 > n) {
+            uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+    #pragma unroll
+            for (int q = 0; q < 4; ++q)
+    #pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    if (r0 + 4 * q + b >= n) wv[q] &= ~(0xffu << (8 * b));
+            v = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+        }
+        uint2 o;
+        o.x = (v.x & 0x0f0f0f0fu) | ((v.y & 0x0f0f0f0fu) << 4);
+        o.y = (v.z & 0x0f0f0f0fu) | ((v.w & 0x0f0f0f0fu) << 4);
+        *reinterpret_cast<uint2*>(out + f * (ld / 2) + u * 8) = o;
+    }
+}
+
 }  // namespace
+
+hipError_t launch_pack_bins4(const uint8_t* bins, int64_t n, int64_t ld, int32_t F, uint8_t* out,
+                             hipStream_t s) {
+    const int64_t per_col = ld / 16;
+    const int64_t units = per_col * F;
+    const int grid = (int)std::min<int64_t>((units + kBlock - 1) / kBlock, 65536);
+    hipLaunchKernelGGL(pack_bins4_kernel, dim3(std::max(grid, 1)), dim3(kBlock), 0, s, bins, ld, n,
+                       per_col, units, out);
+    return hipGetLastError();
+}
 
 hipError_t launch_quantile_edges(const float* sorted, int64_t n, int64_t ld, int32_t F,
                                  const double* q, int32_t nq, float* edges, int32_t edge_stride,

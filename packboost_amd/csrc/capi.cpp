@@ -41,6 +41,7 @@ struct pb_ctx {
     // phase timing of pb_grow_round (pb_profile_enable): per depth, 5 events bracket the
     // hist / score / decide / partition launches on the caller's stream
     int32_t profile;  // 0 off, 1 every phase, 2 the histogram only
+    int32_t bin_layout;  // bins_dev of pb_hist_build / pb_partition: 0 uint8, 1 nibble
     std::vector<hipEvent_t> ev_free;
     std::vector<std::pair<int32_t, std::array<hipEvent_t, 5>>> ev_pending;
 };
@@ -180,6 +181,7 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
         }
     c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 26 * 1024);
     c->force_pairs = (int32_t)env_int("PB_HIST_PAIRS", 0);
+    c->bin_layout = 0;
     c->force_copies = (int32_t)env_int("PB_HIST_COPIES", 0);
     c->force_ftile = (int32_t)env_int("PB_HIST_FTILE", 0);
 
@@ -240,9 +242,13 @@ int pb_round_begin(pb_ctx* c, const float* preds, const float* y, float* grad, u
     return PB_OK;
 }
 
-int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint16_t* nid,
-                  const int32_t* feats, int32_t K, int32_t depth, int32_t max_nodes,
-                  int32_t* hist_cnt, float* hist_grad, void* stream) {
+namespace {
+
+// pb_hist_build over either bin layout: uint8 columns of stride ld (nibble 0) or the
+// two-rows-per-byte columns of stride ld / 2 that pb_pack_bins4 writes (nibble 1).
+int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble, const float* grad,
+               const uint16_t* nid, const int32_t* feats, int32_t K, int32_t depth,
+               int32_t max_nodes, int32_t* hist_cnt, float* hist_grad, void* stream) {
     if (!c || !bins || !grad || !nid || !feats || !hist_cnt || !hist_grad)
         return fail(PB_ERR_INVALID, "pb_hist_build: null argument");
     if (K < 1 || K > c->d.max_feats) return fail(PB_ERR_INVALID, "pb_hist_build: K out of range");
@@ -256,11 +262,14 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
         return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: eras above 65535 rows are not supported yet");
 
     const int nb = c->d.max_bins;
-    // Launch shape, from sweeps on MI355X at the 2.4M x 2376 x 5-bin panel: feature pairs share
-    // one atomic on joint bins when nb * nb <= 256; the LDS per workgroup stays near 26 KiB
+    // Launch shape, from sweeps on MI355X at the 2.4M x 2376 x 5-bin panel: feature pairs (or
+    // triples) share one atomic on joint bins when nb * nb <= 256; the LDS per workgroup stays near 26 KiB
     // (occupancy beats copies), the largest feature tile that fits comes first, then as many
     // histogram copies as fit in half of that.
     int P = (nb <= 16 && K >= 2) ? 2 : 1;
+    // feature triples while their joint histogram stays small (at most 512 cells per copy:
+    // depths 0-2 at 5 bins), where a third fewer atomics beat the larger flush
+    if (nb <= 6 && K >= 3 && (int64_t)max_nodes * nb * nb * nb <= 512) P = 3;
     if (c->force_pairs == 1 || (c->force_pairs == 2 && nb <= 16) ||
         (c->force_pairs == 3 && nb <= 6 && K >= 3))
         P = c->force_pairs;
@@ -293,6 +302,7 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
         while (clog2 < 5 && groups * cells_group * (int64_t(2) << clog2) * 8 <= cap / 2) ++clog2;
     }
     const int64_t per_group = cells_group * (int64_t(1) << clog2) * 8;
+    while (groups > 1 && groups * per_group > 160 * 1024) groups /= 2;  // forced copies
     const int ftile = (int)groups * P;
     const size_t lds_bytes = (size_t)(groups * per_group);
     if (lds_bytes > 160 * 1024)
@@ -303,7 +313,8 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
     a.resident_cus = c->hist_resident ? c->num_cus : 0;
     a.rounds = c->hist_rounds;
     a.bins = bins;
-    a.ld = c->d.ld;
+    a.ld = ld_bytes;
+    a.nibble = nibble;
     a.grad = grad;
     a.nid = nid;
     a.era_off = c->era_off_dev;
@@ -325,6 +336,38 @@ int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint1
     const int64_t grid = (int64_t)eras8 * a.ntiles * node_tiles;
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: grid too large");
     PB_HIP(pb::launch_hist(a, P, (int)grid, lds_bytes, (hipStream_t)stream), "hist launch");
+    return PB_OK;
+}
+
+int partition(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble, int32_t depth,
+              uint16_t* nid, uint16_t* tnode, void* stream) {
+    if (!c || !bins || !nid || !tnode) return fail(PB_ERR_INVALID, "pb_partition: null argument");
+    if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_partition: depth out of range");
+    if ((reinterpret_cast<uintptr_t>(nid) & 3) || (reinterpret_cast<uintptr_t>(tnode) & 3))
+        return fail(PB_ERR_INVALID, "pb_partition: nid/tnode must be 4-byte aligned");
+    PB_HIP(pb::launch_partition(bins, ld_bytes, nibble, c->rows_padded, c->rules, c->st, depth, nid,
+                                tnode, (hipStream_t)stream),
+           "partition launch");
+    return PB_OK;
+}
+
+}  // namespace
+
+int pb_hist_build(pb_ctx* c, const uint8_t* bins, const float* grad, const uint16_t* nid,
+                  const int32_t* feats, int32_t K, int32_t depth, int32_t max_nodes,
+                  int32_t* hist_cnt, float* hist_grad, void* stream) {
+    if (!c) return fail(PB_ERR_INVALID, "pb_hist_build: null argument");
+    const int32_t nib = c->bin_layout;
+    return hist_build(c, bins, nib ? c->d.ld / 2 : c->d.ld, nib, grad, nid, feats, K, depth,
+                      max_nodes, hist_cnt, hist_grad, stream);
+}
+
+int pb_set_bin_layout(pb_ctx* c, int32_t layout) {
+    if (!c) return fail(PB_ERR_INVALID, "pb_set_bin_layout: null context");
+    if (layout != 0 && layout != 1) return fail(PB_ERR_INVALID, "pb_set_bin_layout: layout must be 0 or 1");
+    if (layout == 1 && c->d.max_bins > 16)
+        return fail(PB_ERR_INVALID, "pb_set_bin_layout: the nibble layout needs max_bins <= 16");
+    c->bin_layout = layout;
     return PB_OK;
 }
 
@@ -398,14 +441,9 @@ int pb_decide(pb_ctx* c, int32_t depth, int32_t max_nodes, const pb_split_params
 
 int pb_partition(pb_ctx* c, const uint8_t* bins, int32_t depth, uint16_t* nid, uint16_t* tnode,
                  void* stream) {
-    if (!c || !bins || !nid || !tnode) return fail(PB_ERR_INVALID, "pb_partition: null argument");
-    if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_partition: depth out of range");
-    if ((reinterpret_cast<uintptr_t>(nid) & 3) || (reinterpret_cast<uintptr_t>(tnode) & 3))
-        return fail(PB_ERR_INVALID, "pb_partition: nid/tnode must be 4-byte aligned");
-    PB_HIP(pb::launch_partition(bins, c->d.ld, c->rows_padded, c->rules, c->st, depth, nid, tnode,
-                                (hipStream_t)stream),
-           "partition launch");
-    return PB_OK;
+    if (!c) return fail(PB_ERR_INVALID, "pb_partition: null argument");
+    const int32_t nib = c->bin_layout;
+    return partition(c, bins, nib ? c->d.ld / 2 : c->d.ld, nib, depth, nid, tnode, stream);
 }
 
 int pb_round_end(pb_ctx* c, const uint16_t* tnode, const float* values, int32_t pack_size,
@@ -424,6 +462,14 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
     if (!b->bins_dev || !b->y_dev || !b->preds_dev || !b->grad_dev || !b->nid_dev || !b->tnode_dev ||
         !b->hist_cnt_dev || !b->hist_grad_dev || !b->values_dev)
         return fail(PB_ERR_INVALID, "pb_grow_round: null buffer");
+    // the nibble copy, when bound, serves the histogram and partition reads
+    const int32_t nib = b->bins4_dev ? 1 : 0;
+    const uint8_t* bins = nib ? b->bins4_dev : b->bins_dev;
+    const int64_t ld_bytes = nib ? c->d.ld / 2 : c->d.ld;
+    if (nib && c->d.max_bins > 16)
+        return fail(PB_ERR_INVALID, "pb_grow_round: the nibble bin layout needs max_bins <= 16");
+    if (nib && (reinterpret_cast<uintptr_t>(b->bins4_dev) & 15))
+        return fail(PB_ERR_INVALID, "pb_grow_round: bins4 must be 16-byte aligned");
     int rc = pb_round_begin(c, b->preds_dev, b->y_dev, b->grad_dev, b->nid_dev, b->tnode_dev, stream);
     if (rc) return rc;
     for (int d = 0; d < c->d.max_depth; ++d) {
@@ -449,8 +495,8 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
             return PB_OK;
         };
         if ((rc = mark(0))) return rc;
-        if ((rc = pb_hist_build(c, b->bins_dev, b->grad_dev, b->nid_dev, f, K, d, m, b->hist_cnt_dev,
-                                b->hist_grad_dev, stream)))
+        if ((rc = hist_build(c, bins, ld_bytes, nib, b->grad_dev, b->nid_dev, f, K, d, m,
+                             b->hist_cnt_dev, b->hist_grad_dev, stream)))
             return rc;
         if ((rc = mark(1))) return rc;
         if ((rc = pb_des_score(c, b->hist_cnt_dev, b->hist_grad_dev, f, K, d, m, &b->params, nullptr,
@@ -459,7 +505,7 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
         if ((rc = mark(2))) return rc;
         if ((rc = pb_decide(c, d, m, &b->params, dec, b->values_dev, stream))) return rc;
         if ((rc = mark(3))) return rc;
-        if ((rc = pb_partition(c, b->bins_dev, d, b->nid_dev, b->tnode_dev, stream))) return rc;
+        if ((rc = partition(c, bins, ld_bytes, nib, d, b->nid_dev, b->tnode_dev, stream))) return rc;
         if ((rc = mark(4))) return rc;
     }
     PB_HIP(pb::launch_round_header(c->st, header, (hipStream_t)stream), "round header launch");
@@ -587,6 +633,17 @@ int pb_apply_bins(const float* xt, int64_t n, int64_t ld_x, int32_t F, const flo
     PB_HIP(pb::launch_apply_bins(xt, n, ld_x, F, edges, num_edges, edge_stride, max_bins, perm, bins,
                                  ld_out, (hipStream_t)stream),
            "apply bins launch");
+    return PB_OK;
+}
+
+int pb_pack_bins4(const uint8_t* bins, int64_t n, int64_t ld, int32_t F, uint8_t* out, void* stream) {
+    if (!bins || !out) return fail(PB_ERR_INVALID, "pb_pack_bins4: null argument");
+    if (ld < 0 || ld % 16 != 0 || F < 0) return fail(PB_ERR_INVALID, "pb_pack_bins4: ld must be a multiple of 16");
+    if (n < 0 || n > ld) return fail(PB_ERR_INVALID, "pb_pack_bins4: n must lie in [0, ld]");
+    if ((reinterpret_cast<uintptr_t>(bins) & 15) || (reinterpret_cast<uintptr_t>(out) & 7))
+        return fail(PB_ERR_INVALID, "pb_pack_bins4: bins must be 16-byte and out 8-byte aligned");
+    if (ld == 0 || F == 0) return PB_OK;
+    PB_HIP(pb::launch_pack_bins4(bins, n, ld, F, out, (hipStream_t)stream), "pack bins launch");
     return PB_OK;
 }
 

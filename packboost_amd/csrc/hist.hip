@@ -19,13 +19,20 @@
 //    reference's row-order sum.
 //  * Joint bins (P = 2 for nb <= 16, P = 3 for nb <= 6): the P features of a group share one
 //    atomic on the joint cell (b1 * nb + b2, or (b1 * nb + b2) * nb + b3). The joint index is
-//    below 256, so for 4 rows it comes from 32-bit multiply-adds of the packed bin dwords.
+//    below 256, so for 4 rows it comes from byte-wise multiply-adds of the packed bin dwords.
 //    The flush recovers every marginal by integer sums over the other features' bins, so the
 //    histogram is exactly the one-feature-per-atomic result with 1/P of the LDS atomics.
-//  * The histogram is replicated `C` times in LDS, interleaved per word, and lane l adds
-//    into copy l % C: with C = 32 the 32 lanes an LDS cycle serves for 64-bit operands land in
-//    distinct 8-byte slots, so same-cell rows never serialise (measured on gfx950: 16 copies
-//    still conflict). The host trades C against features per workgroup under an LDS budget.
+//  * The histogram is replicated `C` times in LDS, interleaved per word, and lane l adds into
+//    copy l % C. gfx950 serves a wave's 64-bit LDS atomics in 32-lane halves; lanes of a half
+//    that share a copy collide when their cells alias one bank (measured: about 6.5 cycles per
+//    conflict-free wave-level ds_add_u64, 10.6 at C = 8 over 25 joint cells, 6.7 at C >= 16).
+//    Copies cost LDS (occupancy) and a fold per era, and with eras of a few thousand rows the
+//    kernel waits on memory more than on the LDS, so the host keeps the LDS per workgroup
+//    small and takes the copies that fit.
+//  * Nibble layout (NIB, nb <= 16): every 4 bytes of a column hold 8 rows, byte j = row j in
+//    the low nibble and row j + 4 in the high one, so one dword load brings 8 rows and
+//    (w & 0x0f0f0f0f), ((w >> 4) & 0x0f0f0f0f) are the byte-per-row dwords of rows 0-3 and
+//    4-7: the bin bytes read per depth halve and the per-quad code is the uint8 one.
 //  * Lanes whose 4 rows all lie outside the era (or in no active node) skip their atomics.
 //  * blockIdx -> (era, tile) is XCD-aware: the 8 XCDs receive blocks round-robin, so all
 //    feature tiles of one era run on the same XCD and share the era's row state in its L2.
@@ -36,16 +43,35 @@
 namespace pb {
 namespace {
 
-// 32-bit product that the compiler keeps as its own instruction (see the joint index).
-__device__ __forceinline__ uint32_t mul_sep(uint32_t x, uint32_t y) {
-    uint32_t p = x * y;
-    asm volatile("" : "+v"(p));
-    return p;
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// v moved across lanes by the DPP control CTRL (both 32-bit halves); lanes with no source in
+// range read 0 (bound_ctrl).
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, true);
+    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
-template <int FT, int P>
-__global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
+// Byte-wise x * m + y for four bytes at once, when every byte's result stays below 256: in
+// each 16-bit half (hi * 256 + lo) * m + (yh * 256 + yl) = (hi * m + yh) * 256 + (lo * m + yl)
+// with no carry out of the low byte, so one full-rate packed 16-bit multiply-add
+// (v_pk_mad_u16) replaces a quarter-rate 32-bit multiply.
+__device__ __forceinline__ uint32_t mad_bytes(uint32_t x, uint32_t m, uint32_t y) {
+    const u16x2 a = __builtin_bit_cast(u16x2, x);
+    const u16x2 b = __builtin_bit_cast(u16x2, y);
+    const u16x2 mm = {(unsigned short)m, (unsigned short)m};
+    return __builtin_bit_cast(uint32_t, (u16x2)(a * mm + b));
+}
+
+// Six waves per SIMD (at most 80 VGPRs): more loads in flight per CU (measured 6% faster over
+// the depths of a 2.4M-row, 5-bin round than the unconstrained 104-VGPR, 4-wave build).
+template <int FT, int P, bool NIB>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) void hist_era_kernel(
+    HistArgs a) {
     static_assert(FT % P == 0, "feature tile must hold whole groups");
+    constexpr int RL = NIB ? 8 : 4;  // rows per lane per pass (rows per bin dword)
     constexpr int G = FT / P;  // atomic groups (single features or feature pairs) per tile
     extern __shared__ unsigned long long lds[];
     const int Ua = a.st->u_active[a.depth];
@@ -88,7 +114,7 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
 
         const int r0 = a.era_off[era];
         const int r1 = a.era_off[era + 1];
-        const int a0 = r0 & ~3;
+        const int a0 = r0 & ~(RL - 1);
 
         const uint8_t* col[FT];
     #pragma unroll
@@ -105,18 +131,26 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
         // their groups add into LDS that the flush never reads. A lane with no rows in the era
         // loads its first position (in bounds) and its rows fail the range check. Offsets are
         // 32-bit (ld * F < 2^32 is not needed: columns are addressed from their own base).
-        constexpr int kStride = kBlock * 4;
-        int c = a0 + (int)threadIdx.x * 4;
+        constexpr int kStride = kBlock * RL;
+        constexpr uint32_t kByteShift = NIB ? 1u : 0u;  // row -> byte offset of its bin dword
+        int c = a0 + (int)threadIdx.x * RL;
         uint32_t w[FT];
-        uint2 nn;
-        float4 gg;
+        uint4 nn;   // node ids of the lane's rows (.x, .y used when RL == 4)
+        float4 gg[RL / 4];
         {
             const uint32_t cl = (uint32_t)(c < r1 ? c : a0);
     #pragma unroll
             for (int kk = 0; kk < FT; ++kk)
-                w[kk] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(col[kk] + cl));
-            nn = *reinterpret_cast<const uint2*>(a.nid + cl);
-            gg = *reinterpret_cast<const float4*>(a.grad + cl);
+                w[kk] = __builtin_nontemporal_load(
+                    reinterpret_cast<const uint32_t*>(col[kk] + (cl >> kByteShift)));
+            if (NIB) {
+                nn = *reinterpret_cast<const uint4*>(a.nid + cl);
+            } else {
+                const uint2 n2 = *reinterpret_cast<const uint2*>(a.nid + cl);
+                nn = make_uint4(n2.x, n2.y, 0u, 0u);
+            }
+    #pragma unroll
+            for (int h = 0; h < RL / 4; ++h) gg[h] = *reinterpret_cast<const float4*>(a.grad + cl + 4 * h);
         }
         for (; c < r1; c += kStride) {
             // Unconditional loads keep the wait counts exact (a branch around them makes the
@@ -127,17 +161,30 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
             uint32_t wn[FT];
     #pragma unroll
             for (int kk = 0; kk < FT; ++kk)
-                wn[kk] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(col[kk] + on));
-            const uint2 nnn = *reinterpret_cast<const uint2*>(a.nid + on);
-            const float4 ggn = *reinterpret_cast<const float4*>(a.grad + on);
-            const uint32_t n4[4] = {nn.x & 0xffffu, nn.x >> 16, nn.y & 0xffffu, nn.y >> 16};
-            const float g4[4] = {gg.x, gg.y, gg.z, gg.w};
+                wn[kk] = __builtin_nontemporal_load(
+                    reinterpret_cast<const uint32_t*>(col[kk] + (on >> kByteShift)));
+            uint4 nnn;
+            if (NIB) {
+                nnn = *reinterpret_cast<const uint4*>(a.nid + on);
+            } else {
+                const uint2 n2 = *reinterpret_cast<const uint2*>(a.nid + on);
+                nnn = make_uint4(n2.x, n2.y, 0u, 0u);
+            }
+            float4 ggn[RL / 4];
+    #pragma unroll
+            for (int h = 0; h < RL / 4; ++h) ggn[h] = *reinterpret_cast<const float4*>(a.grad + on + 4 * h);
+    #pragma unroll
+          for (int h = 0; h < RL / 4; ++h) {  // quads of rows c + 4h .. c + 4h + 3
+            const uint32_t nq0 = h ? nn.z : nn.x;
+            const uint32_t nq1 = h ? nn.w : nn.y;
+            const uint32_t n4[4] = {nq0 & 0xffffu, nq0 >> 16, nq1 & 0xffffu, nq1 >> 16};
+            const float g4[4] = {gg[h].x, gg[h].y, gg[h].z, gg[h].w};
             uint32_t base[4];  // byte offset of (node, cell 0, this lane's copy) in a group's block
             unsigned long long qv[4];
-            uint32_t keep = 0u;  // 0xff in byte j iff row c+j is counted; other bytes read as bin 0
+            uint32_t keep = 0u;  // 0xff in byte j iff row c+4h+j is counted; other bytes read as bin 0
     #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int r = c + j;
+                const int r = c + 4 * h + j;
                 const uint32_t nl = n4[j] - (uint32_t)u0;  // node within the item's tile
                 const bool ok = (r >= r0) && (r < r1) && (nl < (uint32_t)Un);
                 const uint32_t nj = ok ? nl : 0u;
@@ -146,29 +193,33 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
                 qv[j] = ok ? (((unsigned long long)q << kCountBits) + 1ull) : 0ull;
                 keep |= ok ? (0xffu << (8 * j)) : 0u;
             }
+            // this quad's byte-per-row bin dwords. uint8 columns: bytes of uncounted rows are
+            // masked to bin 0 (the caller's padding rows may hold anything). Nibble columns: every
+            // row holds a valid bin (rows past N are zero, pb_pack_bins4), and uncounted rows add
+            // zero, so no mask is needed.
+            const uint32_t kmask = NIB ? 0xffffffffu : keep;
+            auto wq = [&](int kk) -> uint32_t {
+                return NIB ? ((w[kk] >> (4 * h)) & 0x0f0f0f0fu) : (w[kk] & kmask);
+            };
             if (keep != 0u) {  // lanes without a counted row skip the atomics
     #pragma unroll
                 for (int gi = 0; gi < G; ++gi) {
                     const int kk = gi * P;
                     char* hk = lds_bytes + (uint32_t)(gi * words_group) * 8u;
                     uint32_t wk;
-                    // The products stay apart from the adds (mul_sep): fused into v_mad_u64_u32,
-                    // the 64-bit addend's unused high half may alias a register of the next
-                    // pass's loads and make the atomics wait for them.
                     if (P == 3) {
                         // (b1 * nb + b2) * nb + b3 <= nb^3 - 1 <= 215 for nb <= 6: every partial
                         // result stays below 256, so no byte carries into the next row's byte
-                        const uint32_t w2 = (kk + 1 < nf) ? w[kk + 1] : 0u;
-                        const uint32_t w3 = (kk + 2 < nf) ? w[kk + 2] : 0u;
-                        const uint32_t t = mul_sep(w[kk] & keep, (uint32_t)nb) + (w2 & keep);
-                        wk = mul_sep(t, (uint32_t)nb) + (w3 & keep);
+                        const uint32_t w2 = (kk + 1 < nf) ? wq(kk + 1) : 0u;
+                        const uint32_t w3 = (kk + 2 < nf) ? wq(kk + 2) : 0u;
+                        wk = mad_bytes(mad_bytes(wq(kk), (uint32_t)nb, w2), (uint32_t)nb, w3);
                     } else if (P == 2) {
                         // joint index per byte: b1 * nb + b2 <= 255 (no carry between bytes);
                         // a lone last feature pairs with bin 0
-                        const uint32_t w2 = (kk + 1 < nf) ? w[kk + 1] : 0u;
-                        wk = mul_sep(w[kk] & keep, (uint32_t)nb) + (w2 & keep);
+                        const uint32_t w2 = (kk + 1 < nf) ? wq(kk + 1) : 0u;
+                        wk = mad_bytes(wq(kk), (uint32_t)nb, w2);
                     } else {
-                        wk = w[kk] & keep;
+                        wk = wq(kk);
                     }
     #pragma unroll
                     for (int j = 0; j < 4; ++j) {
@@ -177,21 +228,34 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
                     }
                 }
             }
+          }  // quads
     #pragma unroll
             for (int kk = 0; kk < FT; ++kk) w[kk] = wn[kk];
             nn = nnn;
-            gg = ggn;
+    #pragma unroll
+            for (int h = 0; h < RL / 4; ++h) gg[h] = ggn[h];
         }
         __syncthreads();
 
-        // Flush. (1) Fold the C copies of every cell into copy 0 (all threads).
+        // Flush. (1) Fold the C copies of every cell into copy 0. A cell's copies are C adjacent
+        // words, so each wave reads 64 consecutive words (64 / C whole cells, no bank conflicts;
+        // a thread walking one cell's copies would make all lanes hit one bank), sums every C
+        // lanes with DPP row shifts (an inclusive scan inside each 16-lane row, then a row
+        // broadcast for C = 32; lanes shifted in from outside a row read 0), so lane C-1 of every
+        // C-lane group holds its cell's total, and writes it back to copy 0.
         const int cells_total = ng * UT * cells_node;
         if (C > 1) {
-            for (int x = threadIdx.x; x < cells_total; x += kBlock) {
-                unsigned long long* cp = lds + (int64_t)x * C;
-                unsigned long long tot = 0ull;
-                for (int cc = 0; cc < C; ++cc) tot += cp[cc];
-                cp[0] = tot;
+            const int total_words = cells_total * C;
+            const int lane = (int)(threadIdx.x & (kWave - 1));
+            for (int wb = (int)(threadIdx.x / kWave) * kWave; wb < total_words; wb += kBlock) {
+                const int wi = wb + lane;
+                unsigned long long v = wi < total_words ? lds[wi] : 0ull;
+                v += dpp_u64<0x111>(v);                 // row_shr:1
+                if (C > 2) v += dpp_u64<0x112>(v);      // row_shr:2
+                if (C > 4) v += dpp_u64<0x114>(v);      // row_shr:4
+                if (C > 8) v += dpp_u64<0x118>(v);      // row_shr:8
+                if (C > 16) v += dpp_u64<0x142>(v);     // row_bcast:15 (row r's lane 15 -> row r+1)
+                if ((lane & (C - 1)) == C - 1 && wi < total_words) lds[wi - (C - 1)] = v;
             }
             __syncthreads();
         }
@@ -286,9 +350,9 @@ __global__ __launch_bounds__(kBlock) void hist_era_kernel(HistArgs a) {
     }  // work items
 }
 
-template <int FT, int P>
+template <int FT, int P, bool NIB>
 hipError_t launch_ft(const HistArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
-    const void* fn = reinterpret_cast<const void*>(&hist_era_kernel<FT, P>);
+    const void* fn = reinterpret_cast<const void*>(&hist_era_kernel<FT, P, NIB>);
     if (lds_bytes > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds_bytes);
@@ -302,39 +366,48 @@ hipError_t launch_ft(const HistArgs& a, int grid, size_t lds_bytes, hipStream_t 
         const int64_t want = (int64_t)std::max(1, per_cu) * a.resident_cus * std::max(1, a.rounds);
         grid = (int)std::max<int64_t>(8, std::min<int64_t>(grid, want) / 8 * 8);
     }
-    hipLaunchKernelGGL((hist_era_kernel<FT, P>), dim3(grid), dim3(kBlock), lds_bytes, s, a);
+    hipLaunchKernelGGL((hist_era_kernel<FT, P, NIB>), dim3(grid), dim3(kBlock), lds_bytes, s, a);
     return hipGetLastError();
 }
 
-}  // namespace
-
-hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s) {
+template <bool NIB>
+hipError_t launch_layout(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s) {
     if (pairs == 3) {
         switch (a.ftile) {
-            case 3: return launch_ft<3, 3>(a, grid, lds_bytes, s);
-            case 6: return launch_ft<6, 3>(a, grid, lds_bytes, s);
-            case 12: return launch_ft<12, 3>(a, grid, lds_bytes, s);
+            case 3: return launch_ft<3, 3, NIB>(a, grid, lds_bytes, s);
+            case 6: return launch_ft<6, 3, NIB>(a, grid, lds_bytes, s);
+            case 12: return launch_ft<12, 3, NIB>(a, grid, lds_bytes, s);
             default: return hipErrorInvalidValue;
         }
     }
     if (pairs == 2) {
         switch (a.ftile) {
-            case 2: return launch_ft<2, 2>(a, grid, lds_bytes, s);
-            case 4: return launch_ft<4, 2>(a, grid, lds_bytes, s);
-            case 8: return launch_ft<8, 2>(a, grid, lds_bytes, s);
-            case 16: return launch_ft<16, 2>(a, grid, lds_bytes, s);
-            case 32: return launch_ft<32, 2>(a, grid, lds_bytes, s);
+            case 2: return launch_ft<2, 2, NIB>(a, grid, lds_bytes, s);
+            case 4: return launch_ft<4, 2, NIB>(a, grid, lds_bytes, s);
+            case 8: return launch_ft<8, 2, NIB>(a, grid, lds_bytes, s);
+            case 16: return launch_ft<16, 2, NIB>(a, grid, lds_bytes, s);
+            case 32: return launch_ft<32, 2, NIB>(a, grid, lds_bytes, s);
             default: return hipErrorInvalidValue;
         }
     }
     switch (a.ftile) {
-        case 1: return launch_ft<1, 1>(a, grid, lds_bytes, s);
-        case 2: return launch_ft<2, 1>(a, grid, lds_bytes, s);
-        case 4: return launch_ft<4, 1>(a, grid, lds_bytes, s);
-        case 8: return launch_ft<8, 1>(a, grid, lds_bytes, s);
-        case 16: return launch_ft<16, 1>(a, grid, lds_bytes, s);
+        case 1: return launch_ft<1, 1, NIB>(a, grid, lds_bytes, s);
+        case 2: return launch_ft<2, 1, NIB>(a, grid, lds_bytes, s);
+        case 4: return launch_ft<4, 1, NIB>(a, grid, lds_bytes, s);
+        case 8: return launch_ft<8, 1, NIB>(a, grid, lds_bytes, s);
+        case 16: return launch_ft<16, 1, NIB>(a, grid, lds_bytes, s);
         default: return hipErrorInvalidValue;
     }
+}
+
+}  // namespace
+
+hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s) {
+    if (a.nibble) {
+        if (a.nb > 16) return hipErrorInvalidValue;
+        return launch_layout<true>(a, pairs, grid, lds_bytes, s);
+    }
+    return launch_layout<false>(a, pairs, grid, lds_bytes, s);
 }
 
 }  // namespace pb

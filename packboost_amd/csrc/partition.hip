@@ -17,7 +17,8 @@ namespace {
 constexpr int kMaxRulesLds = 2048;
 
 __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __restrict__ bins,
-                                                       int64_t ld, int64_t rows_padded,
+                                                       int64_t ld, int32_t nibble,
+                                                       int64_t rows_padded,
                                                        const SplitRule* __restrict__ rules,
                                                        const Frontier* st, int32_t depth,
                                                        uint16_t* __restrict__ nid,
@@ -47,7 +48,13 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
                 n2[j] = PB_INACTIVE;
                 continue;
             }
-            const uint32_t bin = bins[(int64_t)rr.feature * ld + r + j];
+            const int64_t row = r + j;
+            const uint8_t* colp = bins + (int64_t)rr.feature * ld;
+            // nibble layout: 4 bytes per 8 rows, row i of a group in byte i & 3, high nibble
+            // for i >= 4
+            const uint32_t bin = nibble ? ((uint32_t)colp[(row >> 3) * 4 + (row & 3)] >>
+                                           (uint32_t)((row & 4) ? 4 : 0)) & 0xfu
+                                        : (uint32_t)colp[row];
             const uint32_t side = bin > (uint32_t)rr.threshold ? 1u : 0u;
             t2[j] = (uint32_t)rr.left_id + side;
             n2[j] = rr.next_slot[side];
@@ -136,12 +143,12 @@ int grid_for(int64_t work, int per_block, int cap) {
 
 }  // namespace
 
-hipError_t launch_partition(const uint8_t* bins, int64_t ld, int64_t rows_padded,
+hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s) {
     const int grid = grid_for(rows_padded / 2, kBlock, 8192);
-    hipLaunchKernelGGL(partition_kernel, dim3(grid), dim3(kBlock), 0, s, bins, ld, rows_padded,
-                       rules, st, depth, nid, tnode);
+    hipLaunchKernelGGL(partition_kernel, dim3(grid), dim3(kBlock), 0, s, bins, ld, nibble,
+                       rows_padded, rules, st, depth, nid, tnode);
     return hipGetLastError();
 }
 

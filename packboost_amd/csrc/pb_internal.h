@@ -41,7 +41,8 @@ struct HistArgs {
     int32_t resident_cus;  // > 0: loop work items over a resident grid on this many CUs
     int32_t rounds;        // resident grids' worth of workgroups (1 = one per slot)
     const uint8_t* bins;
-    int64_t ld;
+    int64_t ld;            // byte stride between columns of `bins`
+    int32_t nibble;        // 1: two rows per byte (nb <= 16), 0: one uint8 per row
     const float* grad;
     const uint16_t* nid;
     const int32_t* era_off;
@@ -107,7 +108,7 @@ hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal*
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
                          hipStream_t s);
-hipError_t launch_partition(const uint8_t* bins, int64_t ld, int64_t rows_padded,
+hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s);
 hipError_t launch_round_begin(const float* preds, const float* y, float* grad, uint16_t* nid,
@@ -116,6 +117,8 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
 hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s);
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
                             float lr, float* preds, int64_t N, hipStream_t s);
+hipError_t launch_pack_bins4(const uint8_t* bins, int64_t n, int64_t ld, int32_t F, uint8_t* out,
+                             hipStream_t s);
 hipError_t launch_quantile_edges(const float* sorted, int64_t n, int64_t ld, int32_t F,
                                  const double* q, int32_t nq, float* edges, int32_t edge_stride,
                                  hipStream_t s);

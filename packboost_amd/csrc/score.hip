@@ -393,7 +393,6 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
     // pair and selected), so the divide sequences of all pairs interleave.
     auto produce = [&](int chunk) {
         const int e0 = chunk * kPcEras;
-        const int ne = min(kPcEras, a.E - e0);
         float4* buf = ring + (chunk & 1) * kPcEras * kWave;
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {

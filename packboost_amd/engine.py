@@ -73,7 +73,9 @@ class DeviceFit:
 
     def __init__(self, bins_fm: torch.Tensor, num_rows: int, y: torch.Tensor,
                  era_offsets: np.ndarray, cfg: PackBoostConfig, *,
-                 stream: torch.cuda.Stream | None = None) -> None:
+                 stream: torch.cuda.Stream | None = None, bin_layout: str = "auto") -> None:
+        """bin_layout: "u8" (the histogram reads bins_fm), "nibble" (a two-rows-per-byte copy,
+        pb_pack_bins4, max_bins <= 16) or "auto" (nibble whenever max_bins <= 16)."""
         lib = _hip.load()
         if bins_fm.dtype != torch.uint8 or bins_fm.dim() != 2 or not bins_fm.is_cuda:
             raise ValueError("bins_fm must be a CUDA uint8 tensor [F, ld]")
@@ -98,6 +100,15 @@ class DeviceFit:
         self.bins = bins_fm
         self.rows_padded = padded_rows(N)
         dev = self.device
+        if bin_layout not in ("auto", "u8", "nibble"):
+            raise ValueError(f"bin_layout must be 'auto', 'u8' or 'nibble', got {bin_layout!r}")
+        if bin_layout == "nibble" and self.nb > 16:
+            raise ValueError("the nibble bin layout needs max_bins <= 16")
+        self.bins4 = None
+        if bin_layout == "nibble" or (bin_layout == "auto" and self.nb <= 16):
+            self.bins4 = torch.empty((self.F, self.ld // 2), dtype=torch.uint8, device=dev)
+            _hip.check(lib.pb_pack_bins4(bins_fm.data_ptr(), N, self.ld, self.F, self.bins4.data_ptr(),
+                                         _hip.stream_ptr(self.stream)), "pb_pack_bins4")
 
         dims = _hip.PbDims(num_rows=N, ld=self.ld, num_features=self.F, num_eras=self.E,
                            max_bins=self.nb, max_depth=self.D, max_feats=self.K,
@@ -144,6 +155,7 @@ class DeviceFit:
         self.preds_snap = torch.zeros_like(self.preds)
         b = _hip.PbFitBuffers()
         b.bins_dev = self.bins.data_ptr()
+        b.bins4_dev = None if self.bins4 is None else self.bins4.data_ptr()
         b.y_dev = self.y.data_ptr()
         b.preds_dev = self.preds.data_ptr()
         b.grad_dev = self.grad.data_ptr()

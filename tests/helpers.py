@@ -55,7 +55,7 @@ class GpuDepth:
     """Runs hist -> score -> decide -> partition for one teacher-forced depth."""
 
     def __init__(self, hip, p: dict, K: int, *, msl: int, depth: int | None = None,
-                 max_depth: int | None = None):
+                 max_depth: int | None = None, layout: str = "u8"):
         import torch
 
         self.torch = torch
@@ -77,6 +77,12 @@ class GpuDepth:
         bfm = np.zeros((F, self.ld), dtype=np.uint8)
         bfm[:, :N] = p["bins"].T
         self.bins = torch.from_numpy(bfm).to(dev)
+        if layout == "nibble":  # the histogram and partition read the packed copy
+            packed = torch.empty((F, self.ld // 2), dtype=torch.uint8, device=dev)
+            hip.check(self.lib.pb_pack_bins4(self.bins.data_ptr(), N, self.ld, F, packed.data_ptr(),
+                                             hip.stream_ptr()), "pb_pack_bins4")
+            hip.check(self.lib.pb_set_bin_layout(ctx, 1), "pb_set_bin_layout")
+            self.bins = packed
         rp = self.ld
         self.grad = torch.zeros(rp, dtype=torch.float32, device=dev)
         preds = torch.zeros(rp, dtype=torch.float32, device=dev)

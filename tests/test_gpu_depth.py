@@ -42,10 +42,15 @@ def _abs_mass(p, U):
     return m
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"case{c[0]}" for c in CASES])
-def test_depth_parity(hip, oracle_mod, case):
+# the nibble bin layout (max_bins <= 16) runs every case it applies to
+LAYOUT_CASES = [(c, "u8") for c in CASES] + [(c, "nibble") for c in CASES if c[4] <= 16]
+
+
+@pytest.mark.parametrize("case,layout", LAYOUT_CASES,
+                         ids=[f"case{c[0]}-{lay}" for c, lay in LAYOUT_CASES])
+def test_depth_parity(hip, oracle_mod, case, layout):
     seed, N, F, E, nb, U, K, msl, lam, dro, dw, alpha = case
-    print(f"[depth parity] seed={seed} N={N} F={F} E={E} nb={nb} U={U} K={K}", flush=True)
+    print(f"[depth parity] seed={seed} N={N} F={F} E={E} nb={nb} U={U} K={K} {layout}", flush=True)
     p = make_problem(seed, N, F, E, nb, U, empty_era=(seed % 2 == 0))
     rng = np.random.default_rng(seed + 100)
     feats = rng.permutation(F)[:K].astype(np.int32)
@@ -53,7 +58,7 @@ def test_depth_parity(hip, oracle_mod, case):
               min_samples_leaf=msl)
     ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb,
                                  want_planes=True, want_cands=True, **kw)
-    g = GpuDepth(hip, p, K, msl=msl)
+    g = GpuDepth(hip, p, K, msl=msl, layout=layout)
     try:
         g.hist(feats)
         cnt, gp = g.planes()
@@ -162,5 +167,28 @@ def test_exact_ties_pick_largest_threshold(hip, oracle_mod, nb, hi):
         assert np.all(s0.view(np.uint32) == s0[0].view(np.uint32))
         assert (dec["feature"][0], dec["threshold"][0]) == (ref.feature[0], ref.threshold[0]), \
             (dec["feature"][0], dec["threshold"][0], ref.feature[0], ref.threshold[0])
+    finally:
+        g.close()
+
+
+@pytest.mark.parametrize("pairs", [1, 2, 3])
+@pytest.mark.parametrize("copies", [1, 2, 4, 8, 16, 32])
+def test_hist_copies(hip, oracle_mod, monkeypatch, pairs, copies):
+    """Every histogram replication count (the copies are folded by DPP lane shifts) and joint
+    width gives the oracle's planes: counts bit-exact, grads within the per-cell mass bar."""
+    monkeypatch.setenv("PB_HIST_COPIES", str(copies))
+    monkeypatch.setenv("PB_HIST_PAIRS", str(pairs))
+    print(f"[hist copies] C={copies} P={pairs}", flush=True)
+    p = make_problem(40 + copies, 9000, 14, 5, 5, 2, empty_era=True)
+    feats = np.random.default_rng(copies).permutation(14)[:13].astype(np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, 5, want_planes=True)
+    g = GpuDepth(hip, p, 13, msl=3, layout="nibble" if copies % 2 == 0 else "u8")
+    try:
+        g.hist(feats)
+        cnt, gp = g.planes()
+        np.testing.assert_array_equal(cnt, ref.planes[0])
+        mass = _abs_mass(p, 2)[:, :, None, None]
+        err = np.abs(gp.astype(np.float64) - ref.planes[1].astype(np.float64))
+        assert np.all(err <= 1e-5 * np.maximum(mass, 1.0))
     finally:
         g.close()
