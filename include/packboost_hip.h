@@ -115,8 +115,9 @@ int32_t pb_device_available(void);
  * Replaces the per-call context build of frontier_cpu.cpp:142-209. */
 int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out);
 int pb_ctx_destroy(pb_ctx* ctx);
-/* Bytes of the two histogram planes (counts int32, grad float32) pb_hist_build writes
- * for a depth with up to `max_nodes` active nodes: E * max_nodes * K * nb * 4 each. */
+/* 4-byte elements each of the two histogram buffers (counts, grads) pb_hist_build fills for
+ * a depth with up to `max_nodes` active nodes and K = max_feats: round_up(C, 64) + E * max_nodes
+ * with C = E * max_nodes * K * (nb - 1) (layout at pb_hist_build). */
 int64_t pb_hist_plane_elems(const pb_ctx* ctx, int32_t max_nodes);
 /* Largest active-node count the frontier can reach at `depth`. */
 int32_t pb_max_nodes(const pb_ctx* ctx, int32_t depth);
@@ -134,9 +135,13 @@ int pb_round_begin(pb_ctx* ctx, const float* preds_dev, const float* y_dev, floa
 /* Kernel 1 — histogram build. Replaces the per-feature histogram + scan of
  * find_best_splits_batched_cpu (frontier_cpu.cpp:261-321) and the histogram part of
  * cuda_find_best_splits_kernel (frontier_cuda.cu:441-498). For every active node u,
- * era e, sampled feature k and bin b writes, into [E][max_nodes][K][nb] planes:
- *   cnt[e][u][k][b] = rows with bin <= b (b < nb-1), total rows at b = nb-1
- *   grad[e][u][k][b] = float32 running sum over bins of the per-bin grad sums.
+ * era e, sampled feature k and threshold t < nb-1 it writes the prefix over bins 0..t, and
+ * per (e, u) the era total (the reference's running sum at bin nb-1, the same for every
+ * feature because the sums are exact). With T = nb - 1, C = E * max_nodes * K * T and
+ * O = round_up(C, 64):
+ *   hist_cnt_dev  as uint16 [E][max_nodes][K][T]: rows with bin <= t (an era holds at most
+ *                 65535 rows); as int32, elements O .. O + E*max_nodes: era totals [E][max_nodes]
+ *   hist_grad_dev float32 [E][max_nodes][K][T]: prefix grad sums; elements O ..: era totals.
  * feats_dev: int32 [K] feature ids; `depth` selects the frontier's active-node count. */
 int pb_hist_build(pb_ctx* ctx, const uint8_t* bins_dev, const float* grad_dev,
                   const uint16_t* nid_dev, const int32_t* feats_dev, int32_t K, int32_t depth,

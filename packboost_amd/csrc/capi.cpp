@@ -220,7 +220,7 @@ int pb_ctx_destroy(pb_ctx* ctx) {
 
 int64_t pb_hist_plane_elems(const pb_ctx* c, int32_t max_nodes) {
     if (!c) return -1;
-    return (int64_t)c->d.num_eras * max_nodes * c->d.max_feats * c->d.max_bins;
+    return pb::plane_elems(c->d.num_eras, max_nodes, c->d.max_feats, c->d.max_bins);
 }
 
 int32_t pb_max_nodes(const pb_ctx* c, int32_t depth) {
@@ -256,8 +256,9 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     if (max_nodes < max_nodes_at(c, depth))
         return fail(PB_ERR_INVALID, "pb_hist_build: max_nodes below the frontier bound of this depth");
     if ((reinterpret_cast<uintptr_t>(bins) & 15) || (reinterpret_cast<uintptr_t>(grad) & 15) ||
-        (reinterpret_cast<uintptr_t>(nid) & 7))
-        return fail(PB_ERR_INVALID, "pb_hist_build: bins/grad must be 16-byte and nid 8-byte aligned");
+        (reinterpret_cast<uintptr_t>(nid) & (nibble ? 15 : 7)))
+        return fail(PB_ERR_INVALID,
+                    "pb_hist_build: bins/grad must be 16-byte and nid 8-byte (nibble bins: 16-byte) aligned");
     if (c->max_era_rows > pb::kMaxEraRowsDirect)
         return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: eras above 65535 rows are not supported yet");
 
@@ -330,8 +331,13 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     a.clog2 = clog2;
     a.st = c->st;
     a.depth = depth;
-    a.out_cnt = hist_cnt;
-    a.out_g = hist_grad;
+    {
+        const int64_t to = pb::plane_tot_off(c->d.num_eras, max_nodes, K, c->d.max_bins);
+        a.out_cnt = reinterpret_cast<uint16_t*>(hist_cnt);
+        a.out_tot_cnt = hist_cnt + to;
+        a.out_g = hist_grad;
+        a.out_tot_g = hist_grad + to;
+    }
     const int eras8 = (a.E + 7) / 8 * 8;
     const int64_t grid = (int64_t)eras8 * a.ntiles * node_tiles;
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: grid too large");
@@ -385,7 +391,9 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     const int full = std::max(1, nb - 1);
     const int32_t* thr_tab = nullptr;
     if (p->k_cuts > 0 && p->k_cuts < full) {
-        PB_HIP(pb::launch_kcuts(hist_cnt, c->d.num_eras, max_nodes, K, nb, p->k_cuts,
+        PB_HIP(pb::launch_kcuts(reinterpret_cast<const uint16_t*>(hist_cnt),
+                                hist_cnt + pb::plane_tot_off(c->d.num_eras, max_nodes, K, nb),
+                                c->d.num_eras, max_nodes, K, nb, p->k_cuts,
                                 p->cut_selection == 1 ? 1 : 0, c->st, depth, c->thr_tab,
                                 (hipStream_t)stream),
                "kcuts launch");
@@ -396,9 +404,17 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     const int64_t grid = (int64_t)sh.ntiles * max_nodes_at(c, depth);
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_des_score: grid too large");
     if (sh.ntiles * sh.wpt > c->wmax) return fail(PB_ERR_INVALID, "pb_des_score: candidate buffer too small");
+    // the scorer addresses one chunk of eras' plane cells with 31-bit offsets
+    if ((int64_t)(pb::kScoreChunkEras + 1) * max_nodes * K * std::max(1, nb - 1) >= (int64_t(1) << 31))
+        return fail(PB_ERR_UNSUPPORTED, "pb_des_score: max_nodes x K x bins too large for one era chunk");
     pb::ScoreArgs a;
-    a.cnt = hist_cnt;
-    a.g = hist_grad;
+    {
+        const int64_t to = pb::plane_tot_off(c->d.num_eras, max_nodes, K, nb);
+        a.cnt = reinterpret_cast<const uint16_t*>(hist_cnt);
+        a.tot_cnt = hist_cnt + to;
+        a.g = hist_grad;
+        a.tot_g = hist_grad + to;
+    }
     a.E = c->d.num_eras;
     a.U = max_nodes;
     a.K = K;

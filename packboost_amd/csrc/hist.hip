@@ -3,8 +3,9 @@
 // Reference semantics: frontier_cpu.cpp:261-321 builds, for each sampled feature,
 // count[n][e][b] (int64) and grad[n][e][b] (float32, summed in row order), then a float32
 // running sum over bins gives prefix[b < nb-1] and the era total. This kernel produces the
-// same prefix/total planes for all sampled features of a depth at once; the counts are
-// exact and the grad prefixes are exact fixed-point sums rounded once to float32.
+// same prefixes for all sampled features of a depth at once, plus one era total per node
+// (the compact planes of pb_internal.h); the counts are exact and the grad prefixes are exact
+// fixed-point sums rounded once to float32, so the total is the same for every feature.
 //
 // Design (gfx950):
 //  * One workgroup owns one (era, feature tile). Rows are era-major, so an era is a
@@ -16,7 +17,8 @@
 //    and the grad sum (high 48 bits) accumulate in a single ds_add_u64. Integer addition is
 //    order-independent, so the result is deterministic run to run; grad is quantised as
 //    round(g * 2^s) with max|g| * 2^s < 2^30, far finer than float32 rounding of the
-//    reference's row-order sum.
+//    reference's row-order sum. (A per-round 8-byte addend array instead of the 4-byte
+//    gradient measured slower: the row-side loads are re-read by every feature tile.)
 //  * Joint bins (P = 2 for nb <= 16, P = 3 for nb <= 6): the P features of a group share one
 //    atomic on the joint cell (b1 * nb + b2, or (b1 * nb + b2) * nb + b3). The joint index is
 //    below 256, so for 4 rows it comes from byte-wise multiply-adds of the packed bin dwords.
@@ -45,6 +47,17 @@ namespace {
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
+// floor(n / d) for n, d < 2^16 as one multiply-high by m = ceil(2^32 / d): with e = m - 2^32 / d
+// in [0, 1), n * m / 2^32 = n / d + n * e / 2^32 and n * e / 2^32 < 1 / d, so the floor is exact.
+// d == 1 (m would be 2^32) returns n.
+struct DivU16 {
+    uint32_t m;
+    bool one;
+    __device__ explicit DivU16(int d)
+        : m((uint32_t)(0xFFFFFFFFull / (unsigned long long)d + 1ull)), one(d == 1) {}
+    __device__ uint32_t div(uint32_t n) const { return one ? n : __umulhi(n, m); }
+};
+
 // v moved across lanes by the DPP control CTRL (both 32-bit halves); lanes with no source in
 // range read 0 (bound_ctrl).
 template <int CTRL>
@@ -65,11 +78,17 @@ __device__ __forceinline__ uint32_t mad_bytes(uint32_t x, uint32_t m, uint32_t y
     return __builtin_bit_cast(uint32_t, (u16x2)(a * mm + b));
 }
 
-// Six waves per SIMD (at most 80 VGPRs): more loads in flight per CU (measured 6% faster over
-// the depths of a 2.4M-row, 5-bin round than the unconstrained 104-VGPR, 4-wave build).
+// Waves per SIMD: six (at most 80 VGPRs) for more loads in flight per CU (measured 6% faster
+// over the depths of a 2.4M-row, 5-bin round than the unconstrained 4-wave build); five for the
+// 16-feature pair tile (measured).
+template <int FT, int P>
+constexpr int hist_waves_per_eu() {
+    return (P == 2 && FT >= 16) ? 5 : 6;
+}
+
 template <int FT, int P, bool NIB>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) void hist_era_kernel(
-    HistArgs a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(hist_waves_per_eu<FT, P>())))
+void hist_era_kernel(HistArgs a) {
     static_assert(FT % P == 0, "feature tile must hold whole groups");
     constexpr int RL = NIB ? 8 : 4;  // rows per lane per pass (rows per bin dword)
     constexpr int G = FT / P;  // atomic groups (single features or feature pairs) per tile
@@ -81,11 +100,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
     const int C = 1 << a.clog2;
     const int UT = a.node_tile;                      // nodes held in LDS per work item
     const int words_group = UT * cells_node * C;     // LDS words per group
-    const float gmax = __uint_as_float(a.st->gmax_bits);
-    int ex = 0;
-    (void)frexpf(gmax, &ex);
-    // scale 2^sh with max|g| * 2^sh < 2^30; capped so that 2^sh stays a finite float
-    const int sh = (gmax > 0.f) ? min(kGradScaleLog2 - ex, 127) : 0;
+    const int sh = grad_scale_log2(a.st);  // rows add round(grad * 2^sh)
     const float scale = ldexpf(1.0f, sh);
     const uint32_t copy = threadIdx.x & (C - 1);
     const uint32_t bin_shift = (uint32_t)a.clog2 + 3u;  // cell -> byte offset of its C copies
@@ -181,7 +196,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
             const float g4[4] = {gg[h].x, gg[h].y, gg[h].z, gg[h].w};
             uint32_t base[4];  // byte offset of (node, cell 0, this lane's copy) in a group's block
             unsigned long long qv[4];
-            uint32_t keep = 0u;  // 0xff in byte j iff row c+4h+j is counted; other bytes read as bin 0
+            uint32_t keep = 0u;  // uint8 bins: 0xff in byte j iff row c+4h+j is counted
+            bool any = false;    // some row of the quad is counted
     #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int r = c + 4 * h + j;
@@ -191,7 +207,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
                 base[j] = (__umul24(nj, cells_c) + copy) * 8u;  // nj < 2^16, cells_c < 2^24
                 const long long q = (long long)__float2int_rn(g4[j] * scale);
                 qv[j] = ok ? (((unsigned long long)q << kCountBits) + 1ull) : 0ull;
-                keep |= ok ? (0xffu << (8 * j)) : 0u;
+                if (!NIB) keep |= ok ? (0xffu << (8 * j)) : 0u;
+                any = any || ok;
             }
             // this quad's byte-per-row bin dwords. uint8 columns: bytes of uncounted rows are
             // masked to bin 0 (the caller's padding rows may hold anything). Nibble columns: every
@@ -201,7 +218,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
             auto wq = [&](int kk) -> uint32_t {
                 return NIB ? ((w[kk] >> (4 * h)) & 0x0f0f0f0fu) : (w[kk] & kmask);
             };
-            if (keep != 0u) {  // lanes without a counted row skip the atomics
+            if (any) {  // lanes without a counted row skip the atomics
     #pragma unroll
                 for (int gi = 0; gi < G; ++gi) {
                     const int kk = gi * P;
@@ -265,10 +282,22 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
         // grad) over the feature's bins 0..bb, converted once: the count exactly, the grad as the
         // float32 rounding of the exact sum.
         const double inv_scale = ldexp(1.0, -sh);
+        // Element it = (u * nf + kk) * nb + bb. Its digits come from two exact multiply-high
+        // divisions by the uniform nb and nf (a runtime integer division is a long VALU sequence
+        // and the flush decodes every element).
+        struct Digits {
+            int u, kk, bb;
+        };
+        const DivU16 div_nb(nb), div_nf(nf);
+        auto split = [&](int it) -> Digits {
+            const uint32_t q = div_nb.div((uint32_t)it);
+            const uint32_t u = div_nf.div(q);
+            return Digits{(int)u, (int)(q - u * (uint32_t)nf), (int)((uint32_t)it - q * (uint32_t)nb)};
+        };
         if (P == 1) {
             // single features own their cells: prefix them in place, one thread per (node, feature)
             for (int p = threadIdx.x; p < nf * Un; p += kBlock) {
-                const int u = p / nf;
+                const int u = (int)div_nf.div((uint32_t)p);
                 const int kk = p - u * nf;
                 unsigned long long* hc = lds + ((int64_t)kk * words_group + (int64_t)u * cells_node * C);
                 unsigned long long run = 0ull;
@@ -279,18 +308,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
             }
             __syncthreads();
         }
-        const int run_len = nf * nb;
-        const int items = Un * run_len;
-        // marginal of element (u, kk, bb) alone (P == 1: the prefix, already in place)
-        auto marginal = [&](int it, bool prefix) -> unsigned long long {
-            const int u = it / run_len;
-            const int rem = it - u * run_len;
-            const int kk = rem / nb;
-            const int bb = rem - kk * nb;
-            const int gi = kk / P;
-            const int side = kk - gi * P;  // which feature of the group (b1, b2, b3)
+        const int items = Un * nf * nb;
+        // marginal of element (u, kk, bb) alone, or (prefix) its bins 0..bb; P == 1: the prefix,
+        // already in place
+        auto marginal = [&](const Digits& d, bool prefix) -> unsigned long long {
+            const int gi = d.kk / P;
+            const int side = d.kk - gi * P;  // which feature of the group (b1, b2, b3)
             const unsigned long long* hc =
-                lds + ((int64_t)gi * words_group + (int64_t)u * cells_node * C);
+                lds + ((int64_t)gi * words_group + (int64_t)d.u * cells_node * C);
+            const int bb = d.bb;
             const int b_lo = prefix ? 0 : bb;
             unsigned long long tot = 0ull;
             if (P == 3) {
@@ -310,18 +336,30 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
             }
             return tot;
         };
-        auto emit = [&](int it, unsigned long long tot) {
-            const int u = it / run_len;
-            const int rem = it - u * run_len;
+        // compact planes: prefixes t < nb-1 per (node, feature); the era total (bin nb-1) once
+        // per node, from the depth's first feature
+        const int pt = nb - 1;
+        const int64_t row0 = ((int64_t)era * a.U + u0) * a.K + k0;  // (node u0, feature k0)
+        auto emit = [&](const Digits& d, unsigned long long tot) {
             const uint32_t cnt = (uint32_t)(tot & ((1ull << kCountBits) - 1ull));
             const long long Q = ((long long)(tot - cnt)) >> kCountBits;
-            const int64_t o = ((int64_t)era * a.U + u0 + u) * a.K * nb + (int64_t)k0 * nb + rem;
-            a.out_cnt[o] = (int32_t)cnt;
-            a.out_g[o] = (float)((double)Q * inv_scale);
+            const float gs = (float)((double)Q * inv_scale);
+            if (d.bb < pt) {
+                const int64_t o = (row0 + (int64_t)d.u * a.K + d.kk) * pt + d.bb;
+                a.out_cnt[o] = (uint16_t)cnt;
+                a.out_g[o] = gs;
+            } else if (k0 + d.kk == 0) {
+                const int64_t o = (int64_t)era * a.U + u0 + d.u;
+                a.out_tot_cnt[o] = (int32_t)cnt;
+                a.out_tot_g[o] = gs;
+            }
         };
         constexpr int kMaxItems = 16;  // marginals a thread holds in registers
         if (P == 1) {
-            for (int it = threadIdx.x; it < items; it += kBlock) emit(it, marginal(it, false));
+            for (int it = threadIdx.x; it < items; it += kBlock) {
+                const Digits d = split(it);
+                emit(d, marginal(d, false));
+            }
         } else if (items <= kMaxItems * kBlock) {
             // marginals into registers, then compact them over the (no longer needed) joint cells
             // and prefix from there: nb reads per element instead of (bb + 1) * nb
@@ -329,7 +367,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
     #pragma unroll
             for (int i = 0; i < kMaxItems; ++i) {
                 const int it = (int)threadIdx.x + i * kBlock;
-                m[i] = (it < items) ? marginal(it, false) : 0ull;
+                m[i] = (it < items) ? marginal(split(it), false) : 0ull;
             }
             __syncthreads();
     #pragma unroll
@@ -339,13 +377,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6))) voi
             }
             __syncthreads();
             for (int it = threadIdx.x; it < items; it += kBlock) {
-                const int bb = (it % run_len) % nb;
+                const Digits d = split(it);
                 unsigned long long tot = 0ull;
-                for (int b = it - bb; b <= it; ++b) tot += lds[b];
-                emit(it, tot);
+                for (int b = it - d.bb; b <= it; ++b) tot += lds[b];
+                emit(d, tot);
             }
         } else {
-            for (int it = threadIdx.x; it < items; it += kBlock) emit(it, marginal(it, true));
+            for (int it = threadIdx.x; it < items; it += kBlock) {
+                const Digits d = split(it);
+                emit(d, marginal(d, true));
+            }
         }
     }  // work items
 }

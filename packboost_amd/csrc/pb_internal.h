@@ -24,6 +24,15 @@ struct Frontier {
     int32_t reserved[6];
 };
 
+// Exponent sh of the round's fixed-point gradient scale 2^sh: max|g| * 2^sh < 2^kGradScaleLog2,
+// capped so that 2^sh stays a finite float.
+__device__ __forceinline__ int grad_scale_log2(const Frontier* st) {
+    const float gmax = __uint_as_float(st->gmax_bits);
+    int ex = 0;
+    (void)frexpf(gmax, &ex);
+    return (gmax > 0.f) ? min(kGradScaleLog2 - ex, 127) : 0;
+}
+
 // Per active node of the current depth, read by the partition kernel.
 struct SplitRule {
     int32_t feature;    // -1: node did not split
@@ -58,13 +67,35 @@ struct HistArgs {
     int32_t clog2;  // log2 of LDS histogram copies
     const Frontier* st;
     int32_t depth;
-    int32_t* out_cnt;
+    uint16_t* out_cnt;     // compact planes (plane_cells / plane_tot_off)
+    int32_t* out_tot_cnt;
     float* out_g;
+    float* out_tot_g;
 };
 
+// Histogram planes (compact form). For T = nb - 1 thresholds of U node slots and K features:
+//   count buffer: uint16 [E][U][K][T] prefix counts (rows with bin <= t; an era holds at most
+//                 65535 rows), then int32 [E][U] era totals at element plane_tot_off;
+//   grad buffer:  float  [E][U][K][T] prefix grads, then float [E][U] era totals at the same
+//                 element offset.
+// The totals are the same for every feature (exact fixed-point sums), so they are stored once.
+__host__ __device__ inline int64_t plane_cells(int64_t E, int64_t U, int64_t K, int64_t nb) {
+    return E * U * K * (nb - 1);
+}
+__host__ __device__ inline int64_t plane_tot_off(int64_t E, int64_t U, int64_t K, int64_t nb) {
+    return (plane_cells(E, U, K, nb) + 63) / 64 * 64;  // 4-byte elements into either buffer
+}
+__host__ __device__ inline int64_t plane_elems(int64_t E, int64_t U, int64_t K, int64_t nb) {
+    return plane_tot_off(E, U, K, nb) + E * U;
+}
+
+constexpr int kScoreChunkEras = 24;  // eras whose plane cells a scorer chunk stages at once
+
 struct ScoreArgs {
-    const int32_t* cnt;
-    const float* g;
+    const uint16_t* cnt;     // prefix counts [E][U][K][nb-1]
+    const int32_t* tot_cnt;  // [E][U]
+    const float* g;          // prefix grads [E][U][K][nb-1]
+    const float* tot_g;      // [E][U]
     int32_t E;
     int32_t U;
     int32_t K;
@@ -100,7 +131,8 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
 // Launchers (defined in the .hip files; all return hipError_t of the launch).
 hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s);
-hipError_t launch_kcuts(const int32_t* cnt, int32_t E, int32_t U, int32_t K, int32_t nb,
+hipError_t launch_kcuts(const uint16_t* cnt, const int32_t* tot_cnt, int32_t E, int32_t U, int32_t K,
+                        int32_t nb,
                         int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                         int32_t* thr_tab, hipStream_t s);
 hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal* ntot,

@@ -138,7 +138,8 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     const float alpha = a.era_alpha;
     const bool use_dir = a.dir_w != 0.0f;
     const bool unit_w = !(alpha > 0.0f);
-    const int64_t ustride = (int64_t)a.K * nb;
+    const int pt = nb - 1;  // prefix cells per (node, feature) in the compact planes
+    const int64_t ustride = (int64_t)a.K * pt;
     const int64_t estride = (int64_t)a.U * ustride;
     const int64_t node_off = (int64_t)u * ustride;
     const int nchunks = (a.E + EC - 1) / EC;
@@ -161,9 +162,10 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                 const int t = c - kk * T;
                 const int k = k0 + kk;
                 const int thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
-                const int64_t off = (int64_t)(e0 + el) * estride + node_off + (int64_t)k * nb;
-                pin[i].ctot = a.cnt[off + nb - 1];
-                pin[i].Gt = a.g[off + nb - 1];
+                const int64_t off = (int64_t)(e0 + el) * estride + node_off + (int64_t)k * pt;
+                const int64_t to = (int64_t)(e0 + el) * a.U + u;
+                pin[i].ctot = a.tot_cnt[to];
+                pin[i].Gt = a.tot_g[to];
                 pin[i].L = a.cnt[off + thr];
                 pin[i].GL = a.g[off + thr];
             }
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
 // One barrier per chunk hands a buffer from the producers to the consumer, so the
 // consumer's sequential chain (the part that cannot be parallelised without changing the
 // reference's float order) runs at full wavefront width while its inputs are made alongside.
-constexpr int kPcEras = 24;            // eras per chunk
+constexpr int kPcEras = kScoreChunkEras;  // eras per chunk
 constexpr int kPcProducers = kBlock - kWave;
 constexpr int kPcPairs = (kPcEras * kWave + kPcProducers - 1) / kPcProducers;
 
@@ -340,7 +342,8 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
     const float alpha = a.era_alpha;
     const bool use_dir = a.dir_w != 0.0f;
     const bool unit_w = !(alpha > 0.0f);
-    const int64_t ustride = (int64_t)a.K * nb;
+    const int pt = nb - 1;  // prefix cells per (node, feature) in the compact planes
+    const int64_t ustride = (int64_t)a.K * pt;
     const int64_t estride = (int64_t)a.U * ustride;
     const int64_t node_off = (int64_t)u * ustride;
     const int nchunks = (a.E + kPcEras - 1) / kPcEras;
@@ -352,8 +355,10 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
     // Only the first `np` slots can hold a record (workgroup-uniform): fewer candidates per
     // workgroup mean fewer pairs per producer lane.
     const int np = (kPcEras * ncand + kPcProducers - 1) / kPcProducers;
-    int slot_el[kPcPairs], slot_c[kPcPairs], slot_thr[kPcPairs];
-    int64_t slot_off[kPcPairs];
+    int slot_el[kPcPairs], slot_c[kPcPairs];
+    // plane element of the slot's (era in chunk, candidate) relative to the chunk's first era,
+    // threshold included (the host checks that it fits 31 bits)
+    int32_t slot_off[kPcPairs];
 #pragma unroll
     for (int i = 0; i < kPcPairs; ++i) {
         const int pidx = ptid + i * kPcProducers;
@@ -364,8 +369,8 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
         const int k = k0 + kk;
         slot_el[i] = (pidx >= 0 && pidx < kPcEras * ncand) ? el : kPcEras;  // kPcEras: unused
         slot_c[i] = c;
-        slot_thr[i] = a.thr_tab ? a.thr_tab[k * T + t] : t;
-        slot_off[i] = (int64_t)el * estride + node_off + (int64_t)k * nb;
+        const int thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
+        slot_off[i] = (int32_t)((int64_t)el * estride + node_off + (int64_t)k * pt + thr);
     }
 
     PairIn pin[kPcPairs];
@@ -382,17 +387,17 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
             pin[i].GL = 0.0f;
             if (chunk < nchunks && slot_el[i] < ne) {
                 const int64_t off = eoff + slot_off[i];
-                pin[i].ctot = a.cnt[off + nb - 1];
-                pin[i].Gt = a.g[off + nb - 1];
-                pin[i].L = a.cnt[off + slot_thr[i]];
-                pin[i].GL = a.g[off + slot_thr[i]];
+                const int64_t to = (int64_t)(e0 + slot_el[i]) * a.U + u;  // era total
+                pin[i].ctot = a.tot_cnt[to];
+                pin[i].Gt = a.tot_g[to];
+                pin[i].L = a.cnt[off];
+                pin[i].GL = a.g[off];
             }
         }
     };
     // Branch-free per pair (the same float operations as the reference, evaluated for every
     // pair and selected), so the divide sequences of all pairs interleave.
     auto produce = [&](int chunk) {
-        const int e0 = chunk * kPcEras;
         float4* buf = ring + (chunk & 1) * kPcEras * kWave;
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
@@ -600,7 +605,8 @@ __device__ void even_cuts(int nb, int k, int32_t* out) {
     while (m < kk) { out[m] = out[m - 1]; ++m; }
 }
 
-__global__ void kcuts_kernel(const int32_t* cnt, int32_t E, int32_t U, int32_t K, int32_t nb,
+__global__ void kcuts_kernel(const uint16_t* cnt, const int32_t* tot_cnt, int32_t E, int32_t U,
+                             int32_t K, int32_t nb,
                              int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                              int32_t* thr_tab) {
     const int kf = blockIdx.x * blockDim.x + threadIdx.x;
@@ -615,13 +621,15 @@ __global__ void kcuts_kernel(const int32_t* cnt, int32_t E, int32_t U, int32_t K
         return;
     }
     const int Ua = st->u_active[depth];
-    // cdf[b] = sum over nodes, eras of count of bin b (planes hold running sums over bins)
+    // cdf[b] = sum over nodes, eras of count of bin b (planes hold running sums over bins;
+    // bin nb-1's running sum is the era total)
     long long cdf[256];
     for (int b = 0; b < nb; ++b) cdf[b] = 0;
     for (int e = 0; e < E; ++e)
         for (int u = 0; u < Ua; ++u) {
-            const int32_t* p = cnt + (((int64_t)e * U + u) * K + kf) * nb;
-            for (int b = 0; b < nb; ++b) cdf[b] += p[b];
+            const uint16_t* p = cnt + (((int64_t)e * U + u) * K + kf) * (nb - 1);
+            for (int b = 0; b < nb - 1; ++b) cdf[b] += p[b];
+            cdf[nb - 1] += tot_cnt[(int64_t)e * U + u];
         }
     const long long total = cdf[nb - 1];
     if (total <= 0) {
@@ -866,13 +874,13 @@ hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStrea
     return hipGetLastError();
 }
 
-hipError_t launch_kcuts(const int32_t* cnt, int32_t E, int32_t U, int32_t K, int32_t nb,
-                        int32_t k, int32_t mass, const Frontier* st, int32_t depth,
+hipError_t launch_kcuts(const uint16_t* cnt, const int32_t* tot_cnt, int32_t E, int32_t U, int32_t K,
+                        int32_t nb, int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                         int32_t* thr_tab, hipStream_t s) {
     const int threads = 64;
     const int grid = (K + threads - 1) / threads;
-    hipLaunchKernelGGL(kcuts_kernel, dim3(grid), dim3(threads), 0, s, cnt, E, U, K, nb, k, mass,
-                       st, depth, thr_tab);
+    hipLaunchKernelGGL(kcuts_kernel, dim3(grid), dim3(threads), 0, s, cnt, tot_cnt, E, U, K, nb, k,
+                       mass, st, depth, thr_tab);
     return hipGetLastError();
 }
 

@@ -44,6 +44,22 @@ def node_era_rows(p: dict) -> list[list[np.ndarray]]:
     return out
 
 
+def decode_planes(cnt_raw: np.ndarray, g_raw: np.ndarray, E: int, M: int, K: int, nb: int):
+    """Compact histogram planes (uint16 prefix counts and float32 prefix grads [E][M][K][nb-1],
+    era totals [E][M] at element round_up(E*M*K*(nb-1), 64) of each buffer) expanded to the
+    reference's [E][M][K][nb] prefix form (bin nb-1 = era total, repeated per feature)."""
+    cells = E * M * K * (nb - 1)
+    tot = (cells + 63) // 64 * 64
+    cnt_raw = np.ascontiguousarray(cnt_raw, dtype=np.int32)
+    c16 = cnt_raw.view(np.uint16)[:cells].reshape(E, M, K, nb - 1)
+    ct = cnt_raw[tot: tot + E * M].reshape(E, M)
+    g = np.asarray(g_raw, dtype=np.float32)[:cells].reshape(E, M, K, nb - 1)
+    gt = np.asarray(g_raw, dtype=np.float32)[tot: tot + E * M].reshape(E, M)
+    c = np.concatenate([c16.astype(np.int32), np.repeat(ct[:, :, None, None], K, axis=2)], axis=3)
+    gg = np.concatenate([g, np.repeat(gt[:, :, None, None], K, axis=2)], axis=3)
+    return c, gg
+
+
 def depth_for(U: int) -> int:
     d = 0
     while (1 << d) < U:
@@ -115,23 +131,42 @@ class GpuDepth:
         self.values = torch.zeros(1 << (D + 1), dtype=torch.float32, device=dev)
         self.dec = torch.zeros(((1 << D) - 1) * 64, dtype=torch.uint8, device=dev)
 
-    def planes(self):
+    def _plane_layout(self):
         p = self.p
-        shape = (p["E"], self.max_nodes, self.K, p["nb"])
-        n = int(np.prod(shape))
-        c = self.cnt[:n].cpu().numpy().reshape(shape)[:, : p["U"]]
-        g = self.g[:n].cpu().numpy().reshape(shape)[:, : p["U"]]
-        return c, g
+        E, M, K, nb = p["E"], self.max_nodes, self.K, p["nb"]
+        cells = E * M * K * (nb - 1)
+        return E, M, K, nb, cells, (cells + 63) // 64 * 64
+
+    def planes(self):
+        """The device planes in the reference's [E][U][K][nb] prefix form."""
+        E, M, K, nb, _, _ = self._plane_layout()
+        c, g = decode_planes(self.cnt.cpu().numpy(), self.g.cpu().numpy(), E, M, K, nb)
+        U = self.p["U"]
+        return c[:, :U], g[:, :U]
 
     def load_planes(self, cnt: np.ndarray, g: np.ndarray) -> None:
-        """Writes [E][U][K][nb] planes into the device buffers (node stride max_nodes)."""
+        """Writes [E][U][K][nb] prefix planes into the compact device layout. The era totals are
+        stored once per (era, node): they are taken from feature 0."""
         torch = self.torch
-        E, U, K, nb = cnt.shape
-        fc = np.zeros((E, self.max_nodes, K, nb), np.int32)
-        fg = np.zeros((E, self.max_nodes, K, nb), np.float32)
-        fc[:, :U], fg[:, :U] = cnt, g
-        self.cnt[: fc.size].copy_(torch.from_numpy(fc.reshape(-1)))
-        self.g[: fg.size].copy_(torch.from_numpy(fg.reshape(-1)))
+        E, M, K, nb, cells, tot = self._plane_layout()
+        U = cnt.shape[1]
+        assert cnt[..., : nb - 1].max(initial=0) <= 0xFFFF
+        c16 = np.zeros((E, M, K, nb - 1), np.uint16)
+        c16[:, :U] = cnt[..., : nb - 1]
+        ct = np.zeros((E, M), np.int32)
+        ct[:, :U] = cnt[:, :, 0, nb - 1]
+        gp = np.zeros((E, M, K, nb - 1), np.float32)
+        gp[:, :U] = g[..., : nb - 1]
+        gt = np.zeros((E, M), np.float32)
+        gt[:, :U] = g[:, :, 0, nb - 1]
+        craw = np.zeros(self.cnt.numel(), np.int32)
+        craw.view(np.uint16)[:cells] = c16.reshape(-1)
+        craw[tot: tot + E * M] = ct.reshape(-1)
+        graw = np.zeros(self.g.numel(), np.float32)
+        graw[:cells] = gp.reshape(-1)
+        graw[tot: tot + E * M] = gt.reshape(-1)
+        self.cnt.copy_(torch.from_numpy(craw))
+        self.g.copy_(torch.from_numpy(graw))
 
     def hist(self, feats: np.ndarray) -> None:
         self.feats = self.torch.from_numpy(np.ascontiguousarray(feats, np.int32)).to("cuda")

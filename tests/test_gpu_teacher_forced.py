@@ -27,7 +27,7 @@ def _run(hip, oracle_mod, X, y, era_codes, kw, rounds):
     from packboost_amd import PackBoostConfig
     from packboost_amd.data import preprocess_features
     from packboost_amd.engine import split_params, subset_size
-    from tests.helpers import PB_INACTIVE
+    from tests.helpers import PB_INACTIVE, decode_planes
 
     cfg = PackBoostConfig(**kw)
     bins = preprocess_features(X, cfg.max_bins).bins
@@ -114,9 +114,8 @@ def _run(hip, oracle_mod, X, y, era_codes, kw, rounds):
                                              cfg.lambda_l2, cfg.lambda_dro, cfg.direction_weight,
                                              cfg.era_alpha, cfg.min_samples_leaf, want_planes=True,
                                              want_cands=True)
-                shape = (E, maxn[d], K, cfg.max_bins)
-                n = int(np.prod(shape))
-                c_got = cnt[:n].cpu().numpy().reshape(shape)[:, :U]
+                c_got = decode_planes(cnt.cpu().numpy(), gp.cpu().numpy(), E, maxn[d], K,
+                                      cfg.max_bins)[0][:, :U]
                 np.testing.assert_array_equal(c_got, ref.planes[0], err_msg=f"round {r} depth {d} counts")
                 hip.check(lib.pb_des_score(ctx, cnt.data_ptr(), gp.data_ptr(), feats.data_ptr(), K, d,
                                            maxn[d], ctypes.byref(params), None, s), "score")
