@@ -34,6 +34,7 @@ struct pb_ctx {
     int32_t force_copies;
     int32_t force_ftile;
     int32_t force_pairs;
+    int32_t hist_block;  // 0: by LDS size, else 128 or 256 threads
     int32_t score_wgs;  // workgroups the producer/consumer scorer aims for
     int32_t num_cus;        // compute units of the device
     int32_t hist_resident;  // histogram: loop work items over a resident grid
@@ -179,7 +180,8 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
                                                         c->score_wgs);
             c->wmax = std::max(c->wmax, sh.ntiles * sh.wpt);
         }
-    c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 26 * 1024);
+    c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 20000);
+    c->hist_block = (int32_t)env_int("PB_HIST_BLOCK", 0);
     c->force_pairs = (int32_t)env_int("PB_HIST_PAIRS", 0);
     c->bin_layout = 0;
     c->force_copies = (int32_t)env_int("PB_HIST_COPIES", 0);
@@ -264,7 +266,7 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
 
     const int nb = c->d.max_bins;
     // Launch shape, from sweeps on MI355X at the 2.4M x 2376 x 5-bin panel: feature pairs (or
-    // triples) share one atomic on joint bins when nb * nb <= 256; the LDS per workgroup stays near 26 KiB
+    // triples) share one atomic on joint bins when nb * nb <= 256; the LDS per workgroup stays near 20 KB
     // (occupancy beats copies), the largest feature tile that fits comes first, then as many
     // histogram copies as fit in half of that.
     int P = (nb <= 16 && K >= 2) ? 2 : 1;
@@ -316,6 +318,8 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     a.bins = bins;
     a.ld = ld_bytes;
     a.nibble = nibble;
+    a.block = (c->hist_block == 128 || c->hist_block == 256) ? c->hist_block
+                                                             : (lds_bytes <= 24 * 1024 ? 128 : 256);
     a.grad = grad;
     a.nid = nid;
     a.era_off = c->era_off_dev;

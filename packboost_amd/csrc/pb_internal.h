@@ -52,6 +52,7 @@ struct HistArgs {
     const uint8_t* bins;
     int64_t ld;            // byte stride between columns of `bins`
     int32_t nibble;        // 1: two rows per byte (nb <= 16), 0: one uint8 per row
+    int32_t block;         // threads per workgroup: 128 or 256
     const float* grad;
     const uint16_t* nid;
     const int32_t* era_off;

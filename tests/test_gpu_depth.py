@@ -177,14 +177,17 @@ def test_exact_ties_pick_largest_threshold(hip, oracle_mod, nb, hi):
         g.close()
 
 
+@pytest.mark.parametrize("block", [128, 256])
 @pytest.mark.parametrize("pairs", [1, 2, 3])
 @pytest.mark.parametrize("copies", [1, 2, 4, 8, 16, 32])
-def test_hist_copies(hip, oracle_mod, monkeypatch, pairs, copies):
-    """Every histogram replication count (the copies are folded by DPP lane shifts) and joint
-    width gives the oracle's planes: counts bit-exact, grads within the per-cell mass bar."""
+def test_hist_copies(hip, oracle_mod, monkeypatch, pairs, copies, block):
+    """Every histogram replication count (the copies are folded by DPP lane shifts), joint
+    width and workgroup size gives the oracle's planes: counts bit-exact, grads within the
+    per-cell mass bar."""
     monkeypatch.setenv("PB_HIST_COPIES", str(copies))
     monkeypatch.setenv("PB_HIST_PAIRS", str(pairs))
-    print(f"[hist copies] C={copies} P={pairs}", flush=True)
+    monkeypatch.setenv("PB_HIST_BLOCK", str(block))
+    print(f"[hist copies] C={copies} P={pairs} block={block}", flush=True)
     p = make_problem(40 + copies, 9000, 14, 5, 5, 2, empty_era=True)
     feats = np.random.default_rng(copies).permutation(14)[:13].astype(np.int32)
     ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, 5, want_planes=True)
