@@ -180,7 +180,7 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
                                                         c->score_wgs);
             c->wmax = std::max(c->wmax, sh.ntiles * sh.wpt);
         }
-    c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 20000);
+    c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 0);  // 0: by frontier width
     c->hist_block = (int32_t)env_int("PB_HIST_BLOCK", 0);
     c->force_pairs = (int32_t)env_int("PB_HIST_PAIRS", 0);
     c->bin_layout = 0;
@@ -266,9 +266,9 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
 
     const int nb = c->d.max_bins;
     // Launch shape, from sweeps on MI355X at the 2.4M x 2376 x 5-bin panel: feature pairs (or
-    // triples) share one atomic on joint bins when nb * nb <= 256; the LDS per workgroup stays near 20 KB
-    // (occupancy beats copies), the largest feature tile that fits comes first, then as many
-    // histogram copies as fit in half of that.
+    // triples) share one atomic on joint bins when nb * nb <= 256; the LDS per workgroup stays
+    // within a small budget (occupancy beats copies), the largest feature tile that fits comes
+    // first, then as many histogram copies as fit in half of that.
     int P = (nb <= 16 && K >= 2) ? 2 : 1;
     // feature triples while their joint histogram stays small (at most 512 cells per copy:
     // depths 0-2 at 5 bins), where a third fewer atomics beat the larger flush
@@ -277,7 +277,10 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
         (c->force_pairs == 3 && nb <= 6 && K >= 3))
         P = c->force_pairs;
     const int64_t cells_node = (P == 3 ? nb * nb * nb : P == 2 ? nb * nb : nb);
-    int64_t cap = std::max<int64_t>(c->lds_budget, 4 * 1024);
+    // budget: 20 KB for narrow frontiers (2-wave workgroups), 26 KB from 16 nodes on, where
+    // 16-feature pair tiles and 4-wave workgroups measured faster (config 3 depths 4-5)
+    const int64_t budget = c->lds_budget > 0 ? c->lds_budget : (max_nodes >= 16 ? 26 * 1024 : 20000);
+    int64_t cap = std::max<int64_t>(budget, 4 * 1024);
     // node tiles when one feature's node x bin histogram does not fit: single features, up
     // to 64 KiB of LDS, as many nodes per tile as fit
     int node_tile = max_nodes;
