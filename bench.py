@@ -297,16 +297,20 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1e3 / args.steps
     prof_ms, prof_n = read_profile()
-    # Untimed: every phase of a few more rounds, for the per-phase breakdown.
-    n_phase = min(args.steps, 20)
-    for log, _, _ in fit.rounds(rng, n_phase, profile_every=1, profile_mode=1):
+    # Untimed: the per-phase breakdown, every phase bracketed by events, on a fresh fit that
+    # replays the first rounds of the same seed (later rounds can grow smaller trees).
+    fit.close()
+    n_phase = min(args.warmup + args.steps, 20)
+    fit = DeviceFit(bins, N, y, off, cfg)
+    for log, _, _ in fit.rounds(torch.Generator().manual_seed(42), n_phase, profile_every=1,
+                                profile_mode=1):
         tree_arrays_from_log(log, cfg, N)
     torch.cuda.synchronize()
     phase_raw, _ = read_profile()
 
     # histogram roofline: algorithmic bytes per launch = rows of active nodes x K bin bytes
     # (1 per row, 1/2 in the nibble layout) + rows x 6 (grad f32 + node id u16) + written
-    # planes U x E x K x nb x 8, summed over the profiled rounds
+    # compact planes U x E x (K x (nb-1) x 6 + 8), summed over the profiled rounds
     K, E, nb = fit.K, fit.E, fit.nb
     bin_bytes = 0.5 if fit.bins4 is not None else 1.0
     phase_ms = {name: float(phase_raw[i].sum()) for i, name in
@@ -321,7 +325,7 @@ def main() -> int:
                 continue
             base = (1 << d) - 1
             rows = int(log.decisions[base: base + u]["node_count"].astype(np.int64).sum())
-            hist_bytes += rows * K * bin_bytes + rows * 6 + u * E * K * nb * 8
+            hist_bytes += rows * K * bin_bytes + rows * 6 + u * E * (K * (nb - 1) * 6 + 8)
     hist_ms = float(prof_ms[0].sum())
     n_hist = int(prof_n[0].sum())
     achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
@@ -364,7 +368,7 @@ def main() -> int:
             "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
         },
         "profiled_rounds": {"hist_events": f"every {PROFILE_EVERY}th timed round",
-                            "phase_breakdown": f"{n_phase} untimed rounds"},
+                            "phase_breakdown": f"first {n_phase} rounds replayed untimed"},
         "phase_ms_per_round": {k: round(v / n_phase, 4) for k, v in phase_ms.items()},
         "hist_ms_per_depth": [round(float(prof_ms[0, d]) / max(1, int(prof_n[0, d])), 4)
                               for d in range(D)],

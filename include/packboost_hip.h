@@ -215,6 +215,17 @@ typedef struct {
 int pb_grow_round(pb_ctx* ctx, const pb_fit_buffers* buffers, const int32_t* feats_dev, int32_t K,
                   pb_decision* decisions_dev, pb_round_header* header_dev, void* stream);
 
+/* Feature subsets of the next round without waiting for this one. The reference draws one
+ * subset per depth while the frontier has active nodes (booster.py:516-519, 787-792), so the
+ * next round's D subsets are the D draws that follow the previous round's own draws, whose
+ * count the host learns only from that round's header. Given window_dev = int32 [2D][K]: the
+ * previous round's D draws followed by D more, this writes feats_dev[j] = window_dev[off + j]
+ * (j < D) with off = the number of depths of prev_header_dev with active nodes (0 when it is
+ * NULL). Enqueued between two pb_grow_round calls, it lets the host run a round ahead without
+ * redoing a round that stopped early. */
+int pb_select_subsets(const pb_round_header* prev_header_dev, const int32_t* window_dev, int32_t D,
+                      int32_t K, int32_t* feats_dev, void* stream);
+
 /* GPU time of the phases of pb_grow_round, from HIP events recorded on the launch stream
  * around each depth's hist / score / decide / partition launches (the device-side analogue of
  * the per-depth hist_ms / scan_ms / score_ms / partition_ms instrumentation,

@@ -29,7 +29,7 @@ EXPORTED_SYMBOLS = (
     "pb_profile_read", "pb_frontier_set", "pb_frontier_counts", "pb_predict_pack",
     "pb_predict_forest", "pb_predict_bins", "pb_era_corr", "pb_quantile_edges", "pb_apply_bins",
     "pb_forest_create", "pb_forest_predict", "pb_forest_destroy", "pb_pack_bins4",
-    "pb_set_bin_layout",
+    "pb_set_bin_layout", "pb_select_subsets",
 )
 
 
@@ -112,6 +112,7 @@ _SIGNATURES = {
     "pb_apply_bins": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _I32, _I32, _VP, _VP, _I64, _VP]),
     "pb_pack_bins4": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _VP]),
     "pb_set_bin_layout": (ctypes.c_int, [_VP, _I32]),
+    "pb_select_subsets": (ctypes.c_int, [_VP, _VP, _I32, _I32, _VP, _VP]),
     "pb_profile_read": (ctypes.c_int, [_VP, _VP, _VP]),
     "pb_frontier_set": (ctypes.c_int, [_VP, _I32, _I32, _VP, _I32, _VP]),
     "pb_frontier_counts": (ctypes.c_int, [_VP, _VP, _VP, _VP]),

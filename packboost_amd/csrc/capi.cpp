@@ -536,6 +536,15 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
                         stream);
 }
 
+int pb_select_subsets(const pb_round_header* prev_header, const int32_t* window, int32_t D,
+                      int32_t K, int32_t* feats, void* stream) {
+    if (!window || !feats) return fail(PB_ERR_INVALID, "pb_select_subsets: null argument");
+    if (D < 1 || D > PB_MAX_DEPTH || K < 1) return fail(PB_ERR_INVALID, "pb_select_subsets: bad D or K");
+    PB_HIP(pb::launch_select_subsets(prev_header, D, K, window, feats, (hipStream_t)stream),
+           "select subsets launch");
+    return PB_OK;
+}
+
 int pb_profile_enable(pb_ctx* c, int32_t enable) {
     if (!c) return fail(PB_ERR_INVALID, "pb_profile_enable: null context");
     if (enable < 0 || enable > 2) return fail(PB_ERR_INVALID, "pb_profile_enable: mode must be 0, 1 or 2");

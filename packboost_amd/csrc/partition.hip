@@ -110,6 +110,18 @@ __global__ __launch_bounds__(kBlock) void round_begin_kernel(const float* __rest
     }
 }
 
+// feats[j][k] = window[off + j][k] for j < D, where off is the number of feature subsets the
+// previous round drew: the depths whose frontier had active nodes (booster.py:516-519). The
+// caller's window holds that round's draws and the D after each possible count.
+__global__ void select_subsets_kernel(const pb_round_header* prev, int32_t D, int32_t K,
+                                      const int32_t* __restrict__ window, int32_t* __restrict__ feats) {
+    int off = 0;
+    if (prev)
+        while (off < D && prev->u_active[off] > 0) ++off;
+    const int64_t n = (int64_t)D * K;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) feats[i] = window[(int64_t)off * K + i];
+}
+
 // pack_sum[r] = sum_{t<B} value[leaf(r)] in float32, tree order (booster.py:586-598, the
 // B trees are identical); preds += float32(lr) * pack_sum as two rounded float32 ops
 // (torch: tmp = lr * pack_sum; preds += tmp).
@@ -149,6 +161,12 @@ hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int
     const int grid = grid_for(rows_padded / 2, kBlock, 8192);
     hipLaunchKernelGGL(partition_kernel, dim3(grid), dim3(kBlock), 0, s, bins, ld, nibble,
                        rows_padded, rules, st, depth, nid, tnode);
+    return hipGetLastError();
+}
+
+hipError_t launch_select_subsets(const pb_round_header* prev, int32_t D, int32_t K,
+                                 const int32_t* window, int32_t* feats, hipStream_t s) {
+    hipLaunchKernelGGL(select_subsets_kernel, dim3(1), dim3(kBlock), 0, s, prev, D, K, window, feats);
     return hipGetLastError();
 }
 

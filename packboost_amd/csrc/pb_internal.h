@@ -141,6 +141,8 @@ hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal*
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
                          hipStream_t s);
+hipError_t launch_select_subsets(const pb_round_header* prev, int32_t D, int32_t K,
+                                 const int32_t* window, int32_t* feats, hipStream_t s);
 hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s);

@@ -68,6 +68,39 @@ class RoundLog:
     depths_drawn: int         # feature subsets the reference would have drawn
 
 
+class _DrawStream:
+    """The feature-subset draws of a fit as one indexed stream: draw i is
+    torch.randperm(F, generator=rng)[:K] taken after draws 0..i-1, materialised on demand,
+    with the generator state before each draw kept so the generator can be left exactly
+    where the consumed draws end."""
+
+    def __init__(self, rng: torch.Generator, F: int, K: int) -> None:
+        self.rng, self.F, self.K = rng, F, K
+        self.base = 0                        # absolute index of draws[0]
+        self.draws: list[np.ndarray] = []
+        self.states = [rng.get_state()]      # states[i]: before draw base + i
+
+    def window(self, lo: int, n: int) -> np.ndarray:
+        while self.base + len(self.draws) < lo + n:
+            self.draws.append(torch.randperm(self.F, generator=self.rng)[: self.K].numpy()
+                              .astype(np.int32))
+            self.states.append(self.rng.get_state())
+        i = lo - self.base
+        return np.stack(self.draws[i: i + n])
+
+    def release(self, lo: int) -> None:
+        """Forgets draws before absolute index lo."""
+        k = lo - self.base
+        if k > 0:
+            del self.draws[:k]
+            del self.states[:k]
+            self.base = lo
+
+    def rewind_to(self, pos: int) -> None:
+        """Leaves the generator as if exactly draws 0..pos-1 had been taken."""
+        self.rng.set_state(self.states[pos - self.base])
+
+
 class DeviceFit:
     """One fit's device state and round driver (all B trees of a pack share one frontier)."""
 
@@ -151,6 +184,11 @@ class DeviceFit:
                                 for _ in range(2)]
         self._feats_slot_host = [torch.zeros((self.D, self.K), dtype=torch.int32).pin_memory()
                                  for _ in range(2)]
+        # pipelined rounds: each round's window of 2D subset draws (pb_select_subsets)
+        self._win_dev = [torch.zeros((2 * self.D, self.K), dtype=torch.int32, device=dev)
+                         for _ in range(2)]
+        self._win_host = [torch.zeros((2 * self.D, self.K), dtype=torch.int32).pin_memory()
+                          for _ in range(2)]
         self._log_ready = [None, None]
         self.preds_snap = torch.zeros_like(self.preds)
         b = _hip.PbFitBuffers()
@@ -260,6 +298,31 @@ class DeviceFit:
             ev.record(self.stream)
         self._log_ready[slot] = ev
 
+    def _hdr_ptr(self, slot: int) -> int:
+        return self._log_dev[slot].data_ptr() + self._n_dec * _hip.DECISION_DTYPE.itemsize
+
+    def enqueue_grow_window(self, window: np.ndarray, slot: int, prev_slot: int | None) -> None:
+        """Like enqueue_grow, with the round's subsets picked on the device from `window`
+        ([2D][K] draws) by the previous round's header in log slot `prev_slot`
+        (pb_select_subsets), so the host need not know how many subsets that round drew."""
+        wh = self._win_host[slot]
+        wh.numpy()[: len(window)] = window
+        log_dev = self._log_dev[slot]
+        dec_ptr = log_dev.data_ptr()
+        sp = _hip.stream_ptr(self.stream)
+        with torch.cuda.stream(self.stream):
+            self._win_dev[slot].copy_(wh, non_blocking=True)
+            _hip.check(self.lib.pb_select_subsets(
+                None if prev_slot is None else self._hdr_ptr(prev_slot), self._win_dev[slot].data_ptr(),
+                self.D, self.K, self._feats_slot_dev[slot].data_ptr(), sp), "pb_select_subsets")
+            _hip.check(self.lib.pb_grow_round(self.ctx, ctypes.byref(self._bufs),
+                                              self._feats_slot_dev[slot].data_ptr(), self.K,
+                                              dec_ptr, self._hdr_ptr(slot), sp), "pb_grow_round")
+            self._log_host[slot].copy_(log_dev, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(self.stream)
+        self._log_ready[slot] = ev
+
     def read_slot(self, slot: int) -> RoundLog:
         """Waits for the log copy of `slot` (not for later work on the stream) and parses it."""
         self._log_ready[slot].synchronize()
@@ -303,9 +366,14 @@ class DeviceFit:
                 on = profile_mode if r % profile_every == 0 else 0
                 _hip.check(self.lib.pb_profile_enable(self.ctx, on), "pb_profile_enable")
 
-        subs, states = self.draw_subsets(rng)
+        # Round r draws subsets [p_r, p_r + d_r) of the generator's stream (d_r: its depths with
+        # active nodes). Round r + 1 is enqueued before round r's log is read, with the window
+        # [p_r, p_r + 2D): the device picks its D subsets at offset d_r from round r's header.
+        draws = _DrawStream(rng, self.F, self.K)
+        D = self.D
+        p = 0
         set_profile(0)
-        self.enqueue_grow(subs, 0)
+        self.enqueue_grow_window(draws.window(0, 2 * D), 0, None)
         for r in range(num_rounds):
             slot = r & 1
             ahead = r + 1 < num_rounds
@@ -313,28 +381,18 @@ class DeviceFit:
                 with torch.cuda.stream(self.stream):
                     self.preds_snap.copy_(self.preds)
                 ready = now()
-                subs_n, states_n = self.draw_subsets(rng)
                 set_profile(r + 1)
-                self.enqueue_grow(subs_n, slot ^ 1)
+                self.enqueue_grow_window(draws.window(p, 2 * D), slot ^ 1, slot)
             log = self.read_slot(slot)
-            if log.depths_drawn < self.D:
-                # round r drew fewer subsets than assumed: rewind and redo round r + 1
-                rng.set_state(states[log.depths_drawn])
-                if ahead:
-                    self.stream.synchronize()
-                    with torch.cuda.stream(self.stream):
-                        self.preds.copy_(self.preds_snap)
-                    subs_n, states_n = self.draw_subsets(rng)
-                    set_profile(r + 1)
-                    self.enqueue_grow(subs_n, slot ^ 1)
+            p += log.depths_drawn
+            draws.release(p)
             if ahead:
                 yield log, self.preds_snap, ready
             else:
+                draws.rewind_to(p)
                 if profile_every > 0:
                     _hip.check(self.lib.pb_profile_enable(self.ctx, 0), "pb_profile_enable")
                 yield log, self.preds, now()
-            if ahead:
-                states = states_n
 
     def _root_value_if_inactive(self) -> None:
         # Root below capacity (N < 2*msl): the tree is a single leaf -G/(N+lambda)
