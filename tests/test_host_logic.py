@@ -118,3 +118,36 @@ def test_prebinned_detection_and_range(max_bins):
     res = preprocess_features(X, max_bins)
     np.testing.assert_array_equal(res.bins, X.astype(np.uint8))
     assert res.bins.dtype == np.uint8
+
+
+def test_draw_window_matches_sequential_draws():
+    """Round r+1's subsets are window(p_r, 2D)[d_r : d_r + D] (what pb_select_subsets picks),
+    equal to drawing sequentially with the generator left after round r's d_r draws; the final
+    rewind leaves the generator exactly after the consumed draws."""
+    import torch
+
+    from packboost_amd.engine import _DrawStream
+
+    F, K, D = 37, 5, 4
+    depths = [4, 2, 4, 1, 3, 4, 1]  # subsets each round drew
+    # sequential: each round looks at D draws, then keeps only the d it took
+    seq = torch.Generator().manual_seed(11)
+    expected_rounds = []
+    for d in depths:
+        state = seq.get_state()
+        subs = [torch.randperm(F, generator=seq)[:K].numpy() for _ in range(D)]
+        expected_rounds.append(np.stack(subs))
+        seq.set_state(state)
+        for _ in range(d):
+            torch.randperm(F, generator=seq)
+    rng = torch.Generator().manual_seed(11)
+    ds = _DrawStream(rng, F, K)
+    p, prev = 0, 0
+    for r, d in enumerate(depths):
+        start = p - prev  # window of round r begins at p_{r-1}; offset prev = d_{r-1}
+        win = ds.window(start, 2 * D)
+        np.testing.assert_array_equal(win[prev: prev + D], expected_rounds[r])
+        p, prev = p + d, d
+        ds.release(p - d)
+    ds.rewind_to(p)
+    assert torch.equal(rng.get_state(), seq.get_state())
