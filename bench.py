@@ -8,9 +8,13 @@ boosting round (gradient, 6 depths of histogram -> DES score -> decide -> partit
 aggregation, decision read-back and host tree build), the same span as the reference's
 round_seconds (booster.py:495, 654).
 
-Also reported: the histogram kernel's achieved HBM GB/s (algorithmic bytes / average launch
-time from HIP events on the fit's stream) against the 8 TB/s peak, and the CPU oracle
-(restated reference CPU frontier, C/OpenMP) timed on a bounded row sample on the host.
+Also reported: the histogram kernel's achieved GB/s (algorithmic bytes / average launch
+time from HIP events on the fit's stream) against the 8 TB/s HBM peak, where the algorithmic
+bytes use the per-unit figures of the reference's formats (one byte per bin code, grad f32 and a
+4-byte node id per row, 4-byte count and grad per histogram cell; hess is never moved); beside it
+the bytes this build's layouts move (nibble bins, 2-byte node ids, compact planes) and the HBM
+traffic rocprofv3 measured; and the CPU oracle (restated reference CPU frontier, C/OpenMP) timed
+on a bounded row sample on the host.
 """
 
 from __future__ import annotations
@@ -308,11 +312,14 @@ def main() -> int:
     torch.cuda.synchronize()
     phase_raw, _ = read_profile()
 
-    # histogram roofline: algorithmic bytes per launch = rows of active nodes x K bin bytes
-    # (1 per row, 1/2 in the nibble layout) + rows x 6 (grad f32 + node id u16) + written
-    # compact planes U x E x (K x (nb-1) x 6 + 8), summed over the profiled rounds
+    # histogram roofline, summed over the profiled rounds. Algorithmic bytes per launch, with the
+    # reference formats' per-unit figures: rows of active nodes x K (one byte per bin code)
+    # + rows x 8 (grad f32, node id 4 B) + cells U x E x K x nb x 8 (count i32 + grad f32);
+    # hess is not moved by this build, so it is not counted. Moved bytes: what this build's
+    # layouts carry (K/2 or K bin bytes per row, grad 4 B + node id 2 B, compact planes).
     K, E, nb = fit.K, fit.E, fit.nb
     bin_bytes = 0.5 if fit.bins4 is not None else 1.0
+    moved_bytes = 0.0
     phase_ms = {name: float(phase_raw[i].sum()) for i, name in
                 enumerate(("hist", "score", "decide", "partition"))}
     hist_bytes = 0.0
@@ -325,7 +332,8 @@ def main() -> int:
                 continue
             base = (1 << d) - 1
             rows = int(log.decisions[base: base + u]["node_count"].astype(np.int64).sum())
-            hist_bytes += rows * K * bin_bytes + rows * 6 + u * E * (K * (nb - 1) * 6 + 8)
+            hist_bytes += rows * K + rows * 8 + u * E * K * nb * 8
+            moved_bytes += rows * K * bin_bytes + rows * 6 + u * E * (K * (nb - 1) * 6 + 8)
     hist_ms = float(prof_ms[0].sum())
     n_hist = int(prof_n[0].sum())
     achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
@@ -366,6 +374,9 @@ def main() -> int:
             "bin_layout": "nibble" if fit.bins4 is not None else "u8",
             "avg_launch_ms": round(hist_ms / max(n_hist, 1), 4),
             "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
+            "algorithmic_bytes": "rows*K*1 + rows*8 + U*E*K*nb*8 per depth (reference formats, no hess)",
+            "moved_bytes_per_launch": round(moved_bytes / max(n_hist, 1)),
+            "moved_gbs": round(moved_bytes / (hist_ms * 1e-3) / 1e9, 1) if hist_ms > 0 else 0.0,
         },
         "profiled_rounds": {"hist_events": f"every {PROFILE_EVERY}th timed round",
                             "phase_breakdown": f"first {n_phase} rounds replayed untimed"},

@@ -12,8 +12,8 @@
  *   - `stream` is a hipStream_t passed as void* (NULL = the default stream). Work is
  *     enqueued asynchronously; no entry point synchronises the device unless stated.
  *   - Row-indexed device arrays (grad, node ids, ...) must hold `rows_padded`
- *     (= N rounded up to a multiple of 16) elements; the pad rows must carry
- *     node id PB_INACTIVE and grad 0. Bins are column-major uint8 [F][ld] with
+ *     (= N rounded up to a multiple of 16) elements from a 16-byte aligned base; the pad
+ *     rows must carry node id PB_INACTIVE and grad 0. Bins are column-major uint8 [F][ld] with
  *     ld % 16 == 0, ld >= N, 16-byte aligned base, and rows sorted era-major so
  *     era e occupies rows [era_off[e], era_off[e+1]).
  *

@@ -356,8 +356,8 @@ int partition(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble, 
               uint16_t* nid, uint16_t* tnode, void* stream) {
     if (!c || !bins || !nid || !tnode) return fail(PB_ERR_INVALID, "pb_partition: null argument");
     if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_partition: depth out of range");
-    if ((reinterpret_cast<uintptr_t>(nid) & 3) || (reinterpret_cast<uintptr_t>(tnode) & 3))
-        return fail(PB_ERR_INVALID, "pb_partition: nid/tnode must be 4-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(nid) & 15) || (reinterpret_cast<uintptr_t>(tnode) & 15))
+        return fail(PB_ERR_INVALID, "pb_partition: nid/tnode must be 16-byte aligned");
     PB_HIP(pb::launch_partition(bins, ld_bytes, nibble, c->rows_padded, c->rules, c->st, depth, nid,
                                 tnode, (hipStream_t)stream),
            "partition launch");

@@ -31,38 +31,59 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
         for (int u = threadIdx.x; u < Ua; u += kBlock) s_rules[u] = rules[u];
         __syncthreads();
     }
-    const int64_t stride = (int64_t)gridDim.x * kBlock * 2;
-    for (int64_t r = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 2; r < rows_padded; r += stride) {
-        const uint32_t nn = *reinterpret_cast<const uint32_t*>(nid + r);
-        const uint32_t tt = *reinterpret_cast<const uint32_t*>(tnode + r);
-        uint32_t n2[2] = {nn & 0xffffu, nn >> 16};
-        uint32_t t2[2] = {tt & 0xffffu, tt >> 16};
-        bool changed = false;
+    // 8 rows per thread (rows_padded is a multiple of 16): one 16-byte load of their node ids,
+    // then their bin gathers all in flight before any result is needed.
+    const int64_t stride = (int64_t)gridDim.x * kBlock * 8;
+    for (int64_t r = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8; r < rows_padded; r += stride) {
+        const uint4 nn = *reinterpret_cast<const uint4*>(nid + r);
+        uint32_t nw[4] = {nn.x, nn.y, nn.z, nn.w};
+        uint32_t n8[8];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t u = n2[j];
-            if (u >= (uint32_t)Ua) continue;  // PB_INACTIVE or stale
-            const SplitRule rr = in_lds ? s_rules[u] : rules[u];
-            changed = true;
-            if (rr.feature < 0) {
-                n2[j] = PB_INACTIVE;
-                continue;
-            }
+        for (int q = 0; q < 4; ++q) {
+            n8[q * 2] = nw[q] & 0xffffu;
+            n8[q * 2 + 1] = nw[q] >> 16;
+        }
+        bool any = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) any = any || n8[j] < (uint32_t)Ua;
+        if (!any) continue;  // PB_INACTIVE or stale rows only
+        const uint4 tt = *reinterpret_cast<const uint4*>(tnode + r);
+        uint32_t tw[4] = {tt.x, tt.y, tt.z, tt.w};
+        SplitRule rr[8];
+        uint32_t bin[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t u = n8[j];
+            bin[j] = 0u;
+            if (u >= (uint32_t)Ua) continue;
+            rr[j] = in_lds ? s_rules[u] : rules[u];
+            if (rr[j].feature < 0) continue;
             const int64_t row = r + j;
-            const uint8_t* colp = bins + (int64_t)rr.feature * ld;
+            const uint8_t* colp = bins + (int64_t)rr[j].feature * ld;
             // nibble layout: 4 bytes per 8 rows, row i of a group in byte i & 3, high nibble
             // for i >= 4
-            const uint32_t bin = nibble ? ((uint32_t)colp[(row >> 3) * 4 + (row & 3)] >>
-                                           (uint32_t)((row & 4) ? 4 : 0)) & 0xfu
-                                        : (uint32_t)colp[row];
-            const uint32_t side = bin > (uint32_t)rr.threshold ? 1u : 0u;
-            t2[j] = (uint32_t)rr.left_id + side;
-            n2[j] = rr.next_slot[side];
+            bin[j] = nibble ? ((uint32_t)colp[(row >> 3) * 4 + (row & 3)] >> (uint32_t)((row & 4) ? 4 : 0)) & 0xfu
+                            : (uint32_t)colp[row];
         }
-        if (changed) {
-            *reinterpret_cast<uint32_t*>(nid + r) = n2[0] | (n2[1] << 16);
-            *reinterpret_cast<uint32_t*>(tnode + r) = t2[0] | (t2[1] << 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t u = n8[j];
+            if (u >= (uint32_t)Ua) continue;
+            const int q = j >> 1, sh = (j & 1) * 16;
+            uint32_t nv, tv;
+            if (rr[j].feature < 0) {
+                nv = PB_INACTIVE;
+                tv = (tw[q] >> sh) & 0xffffu;
+            } else {
+                const uint32_t side = bin[j] > (uint32_t)rr[j].threshold ? 1u : 0u;
+                tv = (uint32_t)rr[j].left_id + side;
+                nv = rr[j].next_slot[side];
+            }
+            nw[q] = (nw[q] & ~(0xffffu << sh)) | (nv << sh);
+            tw[q] = (tw[q] & ~(0xffffu << sh)) | (tv << sh);
         }
+        *reinterpret_cast<uint4*>(nid + r) = make_uint4(nw[0], nw[1], nw[2], nw[3]);
+        *reinterpret_cast<uint4*>(tnode + r) = make_uint4(tw[0], tw[1], tw[2], tw[3]);
     }
 }
 
@@ -158,7 +179,7 @@ int grid_for(int64_t work, int per_block, int cap) {
 hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s) {
-    const int grid = grid_for(rows_padded / 2, kBlock, 8192);
+    const int grid = grid_for(rows_padded / 8, kBlock, 8192);
     hipLaunchKernelGGL(partition_kernel, dim3(grid), dim3(kBlock), 0, s, bins, ld, nibble,
                        rows_padded, rules, st, depth, nid, tnode);
     return hipGetLastError();
