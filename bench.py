@@ -141,6 +141,27 @@ def copy_probe(mib: int) -> int:
     return 0
 
 
+def copy_peak_gbs(mib: int = 1024, reps: int = 10) -> float:
+    """HBM bytes per second (read + write) of a plain device copy of `mib` MiB, the measured
+    ceiling on this box that the histogram rate is also compared with."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * n * 4 * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return gbs
+
+
 def make_float_data(c: dict, seed: int = 42):
     """Configs 2 and 4: float features generated in HBM (config 2: N(0,1) with 10 columns
     correlated at 0.6, sparse-linear + tanh target with per-era shifts; config 4: half N(0,1),
@@ -267,6 +288,7 @@ def main() -> int:
     if args.rows:
         c["rows"] = args.rows
     torch.cuda.set_device(0)
+    copy_gbs = copy_peak_gbs()
     if args.config == 5:
         return bench_predict(args, c)
     bins, y, off = make_float_data(c) if c.get("float_features") else make_device_data(c)
@@ -369,6 +391,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "copy_peak_gbs": round(copy_gbs, 1),
+            "frac_of_copy_peak": round(achieved / copy_gbs, 4) if copy_gbs > 0 else None,
             "traffic": profiled_traffic(args.config, N),
             "kernel": "hist_era_kernel",
             "bin_layout": "nibble" if fit.bins4 is not None else "u8",
