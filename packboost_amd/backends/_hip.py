@@ -18,6 +18,11 @@ PKG_DIR = Path(__file__).resolve().parent.parent
 LIB_PATH = Path(os.environ.get("PACKBOOST_HIP_LIB", PKG_DIR / "libpackboost_hip.so"))
 
 PB_OK = 0
+PB_ERR_INVALID = -1
+PB_ERR_RANGE = -2
+PB_ERR_HIP = -3
+PB_ERR_UNSUPPORTED = -4
+PB_ERR_NOMEM = -5
 PB_INACTIVE = 0xFFFF
 PB_MAX_DEPTH = 16
 

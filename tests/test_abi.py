@@ -132,3 +132,16 @@ def test_product_path_has_no_cpu_fallback():
     X = np.random.default_rng(0).integers(0, 4, size=(64, 3)).astype(np.uint8)
     with pytest.raises(RuntimeError):
         PackBoost(PackBoostConfig(max_bins=4)).fit(X, np.zeros(64, np.float32), None, num_rounds=1)
+
+
+def test_error_codes_match_header():
+    import re
+
+    from packboost_amd.backends import _hip
+
+    text = (Path(__file__).resolve().parents[1] / "include" / "packboost_hip.h").read_text()
+    codes = {m.group(1): int(m.group(2)) for m in
+             re.finditer(r"#define (PB_(?:OK|ERR_\w+))\s+\(?(-?\d+)\)?", text)}
+    assert codes["PB_OK"] == 0 and len(codes) >= 6
+    for name, value in codes.items():
+        assert getattr(_hip, name) == value, name

@@ -1,0 +1,177 @@
+"""Edge shapes of the HIP path against the oracle: the largest era the 16-bit count field
+holds (65535 rows) and the clean rejection above it, a thousand eras of 0-5 rows, minimal
+shapes (one feature, two bins, depth 1), deep trees whose frontiers need node tiles, and a
+255-bin fit.
+
+Bars as in test_gpu_fit / test_gpu_depth: counts bit-exact, grads within 1e-5 of the per-cell
+mass; tree structure identical, leaf values and predictions within 1e-5.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.helpers import GpuDepth, make_problem, node_era_rows
+from tests.test_gpu_fit import _compare_rounds
+
+pytestmark = pytest.mark.gpu
+
+
+def _abs_mass(p, U):
+    nid = p["nid"].astype(np.int64)
+    m = np.zeros((p["E"], U))
+    act = nid < U
+    np.add.at(m, (p["era"][act], nid[act]), np.abs(p["grad"][act].astype(np.float64)))
+    return m
+
+
+@pytest.mark.parametrize("layout", ["u8", "nibble"])
+def test_largest_era(hip, oracle_mod, layout):
+    """An era of exactly 65535 rows (all in one node): every count reaches the top of the
+    16-bit count field of the LDS addend without carrying into the grad bits."""
+    print(f"[largest era] {layout}", flush=True)
+    N, F, E, nb, U = 65535 + 1000, 6, 2, 5, 1
+    p = make_problem(3, N, F, E, nb, U, ragged=False, inactive_frac=0.0)
+    offs = np.array([0, 65535, N], np.int32)
+    p["era_off"] = offs
+    p["era"] = np.repeat(np.arange(E), np.diff(offs))
+    p["bins"][:65535, 0] = 2  # one bin holds the whole era for feature 0
+    feats = np.arange(F, dtype=np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, want_planes=True)
+    g = GpuDepth(hip, p, F, msl=1, layout=layout)
+    try:
+        g.hist(feats)
+        cnt, gp = g.planes()
+        np.testing.assert_array_equal(cnt, ref.planes[0])
+        assert cnt[0, 0, 0, nb - 1] == 65535
+        err = np.abs(gp.astype(np.float64) - ref.planes[1].astype(np.float64))
+        assert np.all(err <= 1e-5 * np.maximum(_abs_mass(p, U)[:, :, None, None], 1.0))
+    finally:
+        g.close()
+
+
+def test_era_above_count_field_is_rejected(hip):
+    import ctypes
+
+    lib = hip.load()
+    N = 65536 + 16
+    dims = hip.PbDims(num_rows=N, ld=N, num_features=2, num_eras=2, max_bins=5, max_depth=2,
+                      max_feats=2, min_samples_leaf=1)
+    offs = np.array([0, 65536, N], np.int32)
+    ctx = ctypes.c_void_p()
+    hip.check(lib.pb_ctx_create(ctypes.byref(dims), offs.ctypes.data, ctypes.byref(ctx)), "ctx")
+    try:
+        import torch
+
+        dev = torch.device("cuda")
+        bins = torch.zeros((2, N), dtype=torch.uint8, device=dev)
+        grad = torch.zeros(N, device=dev)
+        nid = torch.zeros(N, dtype=torch.int16, device=dev)
+        tn = torch.zeros(N, dtype=torch.int16, device=dev)
+        hip.check(lib.pb_round_begin(ctx, grad.data_ptr(), grad.data_ptr(), grad.data_ptr(),
+                                     nid.data_ptr(), tn.data_ptr(), None), "round_begin")
+        feats = torch.arange(2, dtype=torch.int32, device=dev)
+        plane = int(lib.pb_hist_plane_elems(ctx, 1))
+        cnt = torch.zeros(plane, dtype=torch.int32, device=dev)
+        gp = torch.zeros(plane, device=dev)
+        rc = lib.pb_hist_build(ctx, bins.data_ptr(), grad.data_ptr(), nid.data_ptr(), feats.data_ptr(),
+                               2, 0, 1, cnt.data_ptr(), gp.data_ptr(), None)
+        assert rc == hip.PB_ERR_UNSUPPORTED
+        assert "65535" in hip.last_error()
+        torch.cuda.synchronize()
+    finally:
+        lib.pb_ctx_destroy(ctx)
+
+
+def _fit_vs_oracle(oracle_mod, bins, y, era, rounds, **cfg_kw):
+    from packboost_amd import PackBoost, PackBoostConfig
+
+    cfg = PackBoostConfig(**cfg_kw, prebinned=True)
+    model = PackBoost(cfg).fit(bins, y, era, num_rounds=rounds)
+    ref = oracle_mod.fit(bins, y, None if era is None else era.astype(np.int64), num_rounds=rounds,
+                         **cfg_kw)
+    _compare_rounds(model._rounds, ref.rounds)
+    np.testing.assert_allclose(model._train_preds.cpu().numpy(), ref.preds, atol=1e-5, rtol=0)
+    return model, ref
+
+
+def _target(rng, bins, k=3):
+    """A linear target in O(1) units (bins scaled to [0, 1]) plus noise."""
+    cols = rng.choice(bins.shape[1], size=min(k, bins.shape[1]), replace=False)
+    x = bins[:, cols].astype(np.float32) / max(1, int(bins.max()))
+    y = x @ rng.standard_normal(len(cols)).astype(np.float32)
+    return (y + 0.1 * rng.standard_normal(len(y))).astype(np.float32)
+
+
+@pytest.mark.parametrize("layout", ["u8", "nibble"])
+def test_tiny_eras(hip, oracle_mod, layout):
+    """1000 eras of 0-5 rows: era starts fall anywhere inside the 4- and 8-row load groups.
+    Planes (counts bit-exact) and partition against the oracle; fits on such data are full of
+    exact and near ties, which the parity bar lets flip, so the check stays at one depth."""
+    print(f"[tiny eras] {layout}", flush=True)
+    p = make_problem(8, 3000, 9, 1000, 7, 3)
+    sizes = np.diff(p["era_off"])  # the last era takes the rounding remainder
+    assert (sizes[:-1] <= 6).all() and (sizes == 0).any()
+    feats = np.arange(9, dtype=np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, 7, want_planes=True,
+                                 min_samples_leaf=1)
+    g = GpuDepth(hip, p, 9, msl=1, layout=layout)
+    try:
+        g.hist(feats)
+        cnt, gp = g.planes()
+        np.testing.assert_array_equal(cnt, ref.planes[0])
+        err = np.abs(gp.astype(np.float64) - ref.planes[1].astype(np.float64))
+        assert np.all(err <= 1e-5 * np.maximum(_abs_mass(p, 3)[:, :, None, None], 1.0))
+    finally:
+        g.close()
+
+
+@pytest.mark.parametrize("F,nb,D", [(1, 2, 1), (1, 2, 3), (2, 3, 2)])
+def test_minimal_shapes_fit(hip, oracle_mod, F, nb, D):
+    print(f"[minimal] F={F} nb={nb} D={D}", flush=True)
+    rng = np.random.default_rng(F * 10 + nb + D)
+    N = 800
+    bins = rng.integers(0, nb, size=(N, F)).astype(np.int8)
+    y = _target(rng, bins, k=F)
+    era = np.repeat(np.arange(4), N // 4).astype(np.int16)
+    _fit_vs_oracle(oracle_mod, bins, y, era, 3, pack_size=1, max_depth=D, learning_rate=0.3,
+                   lambda_l2=1.0, lambda_dro=0.2, min_samples_leaf=5, max_bins=nb, random_state=2)
+
+
+@pytest.mark.parametrize("nb", [16, 40])
+def test_deep_tree_fit(hip, oracle_mod, nb):
+    """Depth 9 on 60k rows: frontiers of up to 256 nodes, whose joint-bin (nb 16) or
+    single-feature (nb 40) histograms exceed the LDS and run in node tiles. (Leaves of at least
+    12 rows and a noisy target keep near-ties, which the parity bar allows to flip, unlikely.)"""
+    print(f"[deep] nb={nb}", flush=True)
+    rng = np.random.default_rng(nb)
+    N, F = 60000, 10
+    bins = rng.integers(0, nb, size=(N, F)).astype(np.int8)
+    y = (_target(rng, bins, k=6) + 0.3 * rng.standard_normal(N).astype(np.float32)).astype(np.float32)
+    era = np.repeat(np.arange(6), N // 6).astype(np.int16)
+    model, ref = _fit_vs_oracle(oracle_mod, bins, y, era, 2, pack_size=2, max_depth=9,
+                                learning_rate=0.1, lambda_l2=0.1, lambda_dro=0.1,
+                                min_samples_leaf=12, max_bins=nb, random_state=6)
+    assert max(int(np.count_nonzero(~np.asarray(r["is_leaf"]))) for r in ref.rounds) > 128
+
+
+def test_255_bins_fit(hip, oracle_mod):
+    """Float features quantile-binned into 255 bins on the device (uint8 layout, one feature
+    per LDS atomic) against the oracle on NumPy-binned data."""
+    from packboost_amd import PackBoost, PackBoostConfig
+    from packboost_amd.data import preprocess_features
+
+    print("[255 bins]", flush=True)
+    rng = np.random.default_rng(255)
+    N, F = 6000, 8
+    X = rng.standard_normal((N, F)).astype(np.float32)
+    y = (X[:, 0] - 0.5 * X[:, 3] + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    era = np.repeat(np.arange(5), N // 5).astype(np.int16)
+    kw = dict(pack_size=2, max_depth=4, learning_rate=0.1, lambda_l2=1.0, lambda_dro=0.4,
+              min_samples_leaf=10, max_bins=255, random_state=9)
+    model = PackBoost(PackBoostConfig(**kw)).fit(X, y, era, num_rounds=3)
+    bins = preprocess_features(X, 255).bins
+    ref = oracle_mod.fit(bins, y, era.astype(np.int64), num_rounds=3, **kw)
+    _compare_rounds(model._rounds, ref.rounds)
+    np.testing.assert_allclose(model.predict(X), oracle_mod.predict(ref.rounds, 2, 0.1, bins), atol=1e-5)
