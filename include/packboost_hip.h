@@ -139,10 +139,13 @@ int pb_round_begin(pb_ctx* ctx, const float* preds_dev, const float* y_dev, floa
  * per (e, u) the era total (the reference's running sum at bin nb-1, the same for every
  * feature because the sums are exact). With T = nb - 1, C = E * max_nodes * K * T and
  * O = round_up(C, 64):
- *   hist_cnt_dev  as uint16 [E][max_nodes][K][T]: rows with bin <= t (an era holds at most
- *                 65535 rows); as int32, elements O .. O + E*max_nodes: era totals [E][max_nodes]
+ *   hist_cnt_dev  as uint16 [E][max_nodes][K][T]: rows with bin <= t (as uint32 when an era
+ *                 holds more than 65535 rows); as int32, elements O .. O + E*max_nodes: era
+ *                 totals [E][max_nodes]
  *   hist_grad_dev float32 [E][max_nodes][K][T]: prefix grad sums; elements O ..: era totals.
- * feats_dev: int32 [K] feature ids; `depth` selects the frontier's active-node count. */
+ * feats_dev: int32 [K] feature ids; `depth` selects the frontier's active-node count.
+ * Eras of any size: an era above 16384 rows is built in parts whose exact sums are added up
+ * before the planes are written, so the planes do not depend on the split. */
 int pb_hist_build(pb_ctx* ctx, const uint8_t* bins_dev, const float* grad_dev,
                   const uint16_t* nid_dev, const int32_t* feats_dev, int32_t K, int32_t depth,
                   int32_t max_nodes, int32_t* hist_cnt_dev, float* hist_grad_dev, void* stream);

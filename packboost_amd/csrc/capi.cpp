@@ -29,6 +29,16 @@ struct pb_ctx {
     pb_candidate* node_best;
     int32_t* ids[2];
     int32_t* thr_tab;
+    // histogram work segments (eras above seg_rows rows split into parts; see HistArgs)
+    int32_t S;
+    int32_t* seg_off_dev;
+    int32_t* seg_era_dev;
+    int32_t n_acc;          // eras split into several segments
+    int32_t* acc_slot_dev;  // [E] slot of a split era, else -1
+    int32_t* acc_era_dev;   // [n_acc]
+    uint32_t* acc_cnt;      // [n_acc][umax][max_feats][nb]
+    unsigned long long* acc_g;
+    bool cnt32;             // planes carry 32-bit counts (an era above 65535 rows)
     int32_t last_w;
     int64_t lds_budget;
     int32_t force_copies;
@@ -109,6 +119,12 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->ids[0]);
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
+    (void)hipFree(c->seg_off_dev);
+    (void)hipFree(c->seg_era_dev);
+    (void)hipFree(c->acc_slot_dev);
+    (void)hipFree(c->acc_era_dev);
+    (void)hipFree(c->acc_cnt);
+    (void)hipFree(c->acc_g);
     for (auto& p : c->ev_pending)
         for (hipEvent_t e : p.second)
             if (e) c->ev_free.push_back(e);
@@ -187,7 +203,57 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     c->force_copies = (int32_t)env_int("PB_HIST_COPIES", 0);
     c->force_ftile = (int32_t)env_int("PB_HIST_FTILE", 0);
 
+    // work segments: an era above seg_rows rows is split into equal parts of at most seg_rows
+    // (<= 65535, the LDS count field) whose exact sums are added up per era
+    const int64_t seg_rows = std::min<int64_t>(65535, std::max<int64_t>(256, env_int("PB_HIST_SEG_ROWS", 16384)));
+    std::vector<int32_t> seg_off{0}, seg_era, acc_slot(d.num_eras, -1), acc_era;
+    for (int e = 0; e < d.num_eras; ++e) {
+        const int64_t len = era_off_host[e + 1] - era_off_host[e];
+        const int64_t parts = len > seg_rows ? (len + seg_rows - 1) / seg_rows : 1;
+        if (parts > 1) {
+            acc_slot[e] = (int32_t)acc_era.size();
+            acc_era.push_back(e);
+        }
+        for (int64_t j = 1; j <= parts; ++j) {
+            seg_off.push_back((int32_t)(era_off_host[e] + len * j / parts));
+            seg_era.push_back(e);
+        }
+    }
+    c->S = (int32_t)seg_era.size();
+    c->n_acc = (int32_t)acc_era.size();
+    c->cnt32 = max_era > pb::kMaxEraRowsDirect;
+    const size_t acc_cells = (size_t)c->n_acc * c->umax * d.max_feats * d.max_bins;
+
     int rc = PB_OK;
+    if ((rc = dev_alloc(&c->seg_off_dev, seg_off.size(), "alloc segments")) ||
+        (rc = dev_alloc(&c->seg_era_dev, std::max<size_t>(1, seg_era.size()), "alloc segments")) ||
+        (rc = dev_alloc(&c->acc_slot_dev, std::max(1, d.num_eras), "alloc segment slots")) ||
+        (rc = dev_alloc(&c->acc_era_dev, std::max<size_t>(1, acc_era.size()), "alloc segment slots")) ||
+        (rc = dev_alloc(&c->acc_cnt, std::max<size_t>(1, acc_cells), "alloc segment sums")) ||
+        (rc = dev_alloc(&c->acc_g, std::max<size_t>(1, acc_cells), "alloc segment sums"))) {
+        free_ctx(c);
+        return rc;
+    }
+    {
+        hipError_t e1 = hipMemcpy(c->seg_off_dev, seg_off.data(), sizeof(int32_t) * seg_off.size(),
+                                  hipMemcpyHostToDevice);
+        if (e1 == hipSuccess && !seg_era.empty())
+            e1 = hipMemcpy(c->seg_era_dev, seg_era.data(), sizeof(int32_t) * seg_era.size(),
+                           hipMemcpyHostToDevice);
+        if (e1 == hipSuccess && d.num_eras > 0)
+            e1 = hipMemcpy(c->acc_slot_dev, acc_slot.data(), sizeof(int32_t) * acc_slot.size(),
+                           hipMemcpyHostToDevice);
+        if (e1 == hipSuccess && !acc_era.empty())
+            e1 = hipMemcpy(c->acc_era_dev, acc_era.data(), sizeof(int32_t) * acc_era.size(),
+                           hipMemcpyHostToDevice);
+        if (e1 == hipSuccess && acc_cells > 0) e1 = hipMemset(c->acc_cnt, 0, sizeof(uint32_t) * acc_cells);
+        if (e1 == hipSuccess && acc_cells > 0)
+            e1 = hipMemset(c->acc_g, 0, sizeof(unsigned long long) * acc_cells);
+        if (e1 != hipSuccess) {
+            free_ctx(c);
+            return hip_fail(e1, "copy segments");
+        }
+    }
     if ((rc = dev_alloc(&c->era_off_dev, d.num_eras + 1, "alloc era offsets")) ||
         (rc = dev_alloc(&c->st, 1, "alloc frontier")) ||
         (rc = dev_alloc(&c->rules, c->umax, "alloc split rules")) ||
@@ -261,8 +327,6 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
         (reinterpret_cast<uintptr_t>(nid) & (nibble ? 15 : 7)))
         return fail(PB_ERR_INVALID,
                     "pb_hist_build: bins/grad must be 16-byte and nid 8-byte (nibble bins: 16-byte) aligned");
-    if (c->max_era_rows > pb::kMaxEraRowsDirect)
-        return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: eras above 65535 rows are not supported yet");
 
     const int nb = c->d.max_bins;
     // Launch shape, from sweeps on MI355X at the 2.4M x 2376 x 5-bin panel: feature pairs (or
@@ -341,14 +405,39 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     {
         const int64_t to = pb::plane_tot_off(c->d.num_eras, max_nodes, K, c->d.max_bins);
         a.out_cnt = reinterpret_cast<uint16_t*>(hist_cnt);
+        a.out_cnt32 = c->cnt32 ? reinterpret_cast<uint32_t*>(hist_cnt) : nullptr;
         a.out_tot_cnt = hist_cnt + to;
         a.out_g = hist_grad;
         a.out_tot_g = hist_grad + to;
     }
-    const int eras8 = (a.E + 7) / 8 * 8;
+    a.seg_off = c->seg_off_dev;
+    a.seg_era = c->seg_era_dev;
+    a.S = c->S;
+    a.acc_slot = c->n_acc > 0 ? c->acc_slot_dev : nullptr;
+    a.acc_cnt = c->acc_cnt;
+    a.acc_g = c->acc_g;
+    const int eras8 = (a.S + 7) / 8 * 8;  // segments, a multiple of the 8 XCDs
     const int64_t grid = (int64_t)eras8 * a.ntiles * node_tiles;
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: grid too large");
     PB_HIP(pb::launch_hist(a, P, (int)grid, lds_bytes, (hipStream_t)stream), "hist launch");
+    if (c->n_acc > 0) {
+        pb::FinalizeArgs f;
+        f.acc_cnt = c->acc_cnt;
+        f.acc_g = c->acc_g;
+        f.acc_era = c->acc_era_dev;
+        f.n_acc = c->n_acc;
+        f.U = max_nodes;
+        f.K = K;
+        f.nb = nb;
+        f.st = c->st;
+        f.depth = depth;
+        f.out_cnt = a.out_cnt;
+        f.out_cnt32 = a.out_cnt32;
+        f.out_tot_cnt = a.out_tot_cnt;
+        f.out_g = a.out_g;
+        f.out_tot_g = a.out_tot_g;
+        PB_HIP(pb::launch_finalize(f, (hipStream_t)stream), "finalize launch");
+    }
     return PB_OK;
 }
 
@@ -399,6 +488,7 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     const int32_t* thr_tab = nullptr;
     if (p->k_cuts > 0 && p->k_cuts < full) {
         PB_HIP(pb::launch_kcuts(reinterpret_cast<const uint16_t*>(hist_cnt),
+                                c->cnt32 ? reinterpret_cast<const uint32_t*>(hist_cnt) : nullptr,
                                 hist_cnt + pb::plane_tot_off(c->d.num_eras, max_nodes, K, nb),
                                 c->d.num_eras, max_nodes, K, nb, p->k_cuts,
                                 p->cut_selection == 1 ? 1 : 0, c->st, depth, c->thr_tab,
@@ -418,6 +508,7 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     {
         const int64_t to = pb::plane_tot_off(c->d.num_eras, max_nodes, K, nb);
         a.cnt = reinterpret_cast<const uint16_t*>(hist_cnt);
+        a.cnt32 = c->cnt32 ? reinterpret_cast<const uint32_t*>(hist_cnt) : nullptr;
         a.tot_cnt = hist_cnt + to;
         a.g = hist_grad;
         a.tot_g = hist_grad + to;

@@ -105,30 +105,33 @@ void hist_era_kernel(HistArgs a) {
     const uint32_t copy = threadIdx.x & (C - 1);
     const uint32_t bin_shift = (uint32_t)a.clog2 + 3u;  // cell -> byte offset of its C copies
 
-    // Work items (era, feature tile), XCD-aware: item i goes to XCD i % 8, and all tiles of an
-    // era share one XCD. The grid is a multiple of 8, so a workgroup's items stay on its XCD;
-    // looping lets a workgroup's plane stores drain while it already builds its next item.
+    // Work items (segment, feature tile), XCD-aware: item i goes to XCD i % 8, and all tiles of
+    // a segment share one XCD. A segment is an era, or part of one above the host's segment
+    // size. The grid is a multiple of 8, so a workgroup's items stay on its XCD; looping lets a
+    // workgroup's plane stores drain while it already builds its next item.
     const int per_era = a.ntiles * a.node_tiles;
-    const int n_items = ((a.E + 7) / 8) * 8 * per_era;
+    const int n_items = ((a.S + 7) / 8) * 8 * per_era;
     for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
         const int xcd = item & 7;
         const int i = item >> 3;
-        const int era = (i / per_era) * 8 + xcd;
+        const int seg = (i / per_era) * 8 + xcd;
         const int rem_i = i - (i / per_era) * per_era;
         const int tile = rem_i / a.node_tiles;
         const int u0 = (rem_i - tile * a.node_tiles) * UT;  // first node of this item
         const int Un = min(UT, Ua - u0);                    // its nodes, UT or fewer
         const int k0 = tile * FT;
         const int nf = min(FT, a.K - k0);
-        if (era >= a.E || nf <= 0 || Un <= 0) continue;  // uniform over the workgroup
+        if (seg >= a.S || nf <= 0 || Un <= 0) continue;  // uniform over the workgroup
+        const int era = a.seg_era[seg];
+        const int slot = a.acc_slot ? a.acc_slot[era] : -1;  // >= 0: add into the era's sums
 
         const int ng = (nf + P - 1) / P;
         const int words = ng * words_group;
         __syncthreads();  // the previous item's flush is done with the LDS
         for (int x = threadIdx.x; x < words; x += BS) lds[x] = 0ull;
 
-        const int r0 = a.era_off[era];
-        const int r1 = a.era_off[era + 1];
+        const int r0 = a.seg_off[seg];
+        const int r1 = a.seg_off[seg + 1];
         const int a0 = r0 & ~(RL - 1);
 
         const uint8_t* col[FT];
@@ -294,7 +297,7 @@ void hist_era_kernel(HistArgs a) {
             const uint32_t u = div_nf.div(q);
             return Digits{(int)u, (int)(q - u * (uint32_t)nf), (int)((uint32_t)it - q * (uint32_t)nb)};
         };
-        if (P == 1) {
+        if (P == 1 && slot < 0) {
             // single features own their cells: prefix them in place, one thread per (node, feature)
             for (int p = threadIdx.x; p < nf * Un; p += BS) {
                 const int u = (int)div_nf.div((uint32_t)p);
@@ -339,6 +342,22 @@ void hist_era_kernel(HistArgs a) {
         // compact planes: prefixes t < nb-1 per (node, feature); the era total (bin nb-1) once
         // per node, from the depth's first feature
         const int pt = nb - 1;
+        if (slot >= 0) {
+            // part of a split era: add this segment's per-bin cells, exact integers, into the
+            // era's sums (integer adds: the order of the segments does not matter)
+            const int64_t srow0 = ((int64_t)slot * a.U + u0) * a.K + k0;
+            for (int it = threadIdx.x; it < items; it += BS) {
+                const Digits d = split(it);
+                const unsigned long long m = marginal(d, false);
+                const uint32_t cnt = (uint32_t)(m & ((1ull << kCountBits) - 1ull));
+                if (cnt == 0u) continue;
+                const long long Q = ((long long)(m - cnt)) >> kCountBits;
+                const int64_t o = (srow0 + (int64_t)d.u * a.K + d.kk) * nb + d.bb;
+                atomicAdd(a.acc_cnt + o, cnt);
+                atomicAdd(a.acc_g + o, (unsigned long long)Q);
+            }
+            continue;
+        }
         const int64_t row0 = ((int64_t)era * a.U + u0) * a.K + k0;  // (node u0, feature k0)
         auto emit = [&](const Digits& d, unsigned long long tot) {
             const uint32_t cnt = (uint32_t)(tot & ((1ull << kCountBits) - 1ull));
@@ -346,7 +365,10 @@ void hist_era_kernel(HistArgs a) {
             const float gs = (float)((double)Q * inv_scale);
             if (d.bb < pt) {
                 const int64_t o = (row0 + (int64_t)d.u * a.K + d.kk) * pt + d.bb;
-                a.out_cnt[o] = (uint16_t)cnt;
+                if (a.out_cnt32)
+                    a.out_cnt32[o] = cnt;
+                else
+                    a.out_cnt[o] = (uint16_t)cnt;
                 a.out_g[o] = gs;
             } else if (k0 + d.kk == 0) {
                 const int64_t o = (int64_t)era * a.U + u0 + d.u;
@@ -451,7 +473,54 @@ hipError_t launch_layout(const HistArgs& a, int pairs, int grid, size_t lds_byte
     }
 }
 
+// One thread per (split era, node, feature): prefix over the bins of the exact sums, the same
+// conversion as the histogram flush (count exact, grad rounded once to float32), then the
+// sums are cleared for the next depth.
+__global__ __launch_bounds__(kBlock) void finalize_kernel(FinalizeArgs f) {
+    const int Ua = f.st->u_active[f.depth];
+    const int64_t n = (int64_t)f.n_acc * Ua * f.K;
+    const double inv_scale = ldexp(1.0, -grad_scale_log2(f.st));
+    const int pt = f.nb - 1;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < n; t += stride) {
+        const int64_t sk = t / f.K;
+        const int k = (int)(t - sk * f.K);
+        const int slot = (int)(sk / Ua);
+        const int u = (int)(sk - (int64_t)slot * Ua);
+        const int era = f.acc_era[slot];
+        uint32_t* ac = f.acc_cnt + (((int64_t)slot * f.U + u) * f.K + k) * f.nb;
+        unsigned long long* ag = f.acc_g + (((int64_t)slot * f.U + u) * f.K + k) * f.nb;
+        const int64_t o = (((int64_t)era * f.U + u) * f.K + k) * pt;
+        uint32_t c = 0u;
+        long long q = 0;
+        for (int b = 0; b < f.nb; ++b) {
+            c += ac[b];
+            q += (long long)ag[b];
+            ac[b] = 0u;
+            ag[b] = 0ull;
+            const float gs = (float)((double)q * inv_scale);
+            if (b < pt) {
+                if (f.out_cnt32)
+                    f.out_cnt32[o + b] = c;
+                else
+                    f.out_cnt[o + b] = (uint16_t)c;
+                f.out_g[o + b] = gs;
+            } else if (k == 0) {
+                f.out_tot_cnt[(int64_t)era * f.U + u] = (int32_t)c;
+                f.out_tot_g[(int64_t)era * f.U + u] = gs;
+            }
+        }
+    }
+}
+
 }  // namespace
+
+hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s) {
+    const int64_t n = (int64_t)f.n_acc * f.U * f.K;
+    const int grid = (int)std::max<int64_t>(1, std::min<int64_t>((n + kBlock - 1) / kBlock, 4096));
+    hipLaunchKernelGGL(finalize_kernel, dim3(grid), dim3(kBlock), 0, s, f);
+    return hipGetLastError();
+}
 
 hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s) {
     if (a.nibble) {

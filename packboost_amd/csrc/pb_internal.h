@@ -68,11 +68,40 @@ struct HistArgs {
     int32_t clog2;  // log2 of LDS histogram copies
     const Frontier* st;
     int32_t depth;
-    uint16_t* out_cnt;     // compact planes (plane_cells / plane_tot_off)
+    uint16_t* out_cnt;     // compact planes (plane_cells / plane_tot_off), 16-bit counts
+    uint32_t* out_cnt32;   // the same with 32-bit counts (an era above 65535 rows), or null
+    int32_t* out_tot_cnt;
+    float* out_g;
+    float* out_tot_g;
+    // Work segments: rows [seg_off[s], seg_off[s+1]) of era seg_era[s], at most 65535 rows. An
+    // era of several segments (acc_slot[era] >= 0) is summed exactly over its segments in
+    // acc_cnt / acc_g ([slot][U][K][nb], raw per-bin counts and fixed-point grads) and
+    // turned into planes by finalize_kernel; other eras write their planes directly.
+    const int32_t* seg_off;
+    const int32_t* seg_era;
+    int32_t S;
+    const int32_t* acc_slot;
+    uint32_t* acc_cnt;
+    unsigned long long* acc_g;
+};
+
+// Planes of the eras split into several segments (see HistArgs): prefix over bins of the
+// exact sums, then the same rounding and layout as the histogram kernel's own flush.
+struct FinalizeArgs {
+    uint32_t* acc_cnt;
+    unsigned long long* acc_g;
+    const int32_t* acc_era;  // [n_acc] era of each slot
+    int32_t n_acc;
+    int32_t U, K, nb;
+    const Frontier* st;
+    int32_t depth;
+    uint16_t* out_cnt;
+    uint32_t* out_cnt32;
     int32_t* out_tot_cnt;
     float* out_g;
     float* out_tot_g;
 };
+hipError_t launch_finalize(const FinalizeArgs& f, hipStream_t s);
 
 // Histogram planes (compact form). For T = nb - 1 thresholds of U node slots and K features:
 //   count buffer: uint16 [E][U][K][T] prefix counts (rows with bin <= t; an era holds at most
@@ -94,6 +123,7 @@ constexpr int kScoreChunkEras = 24;  // eras whose plane cells a scorer chunk st
 
 struct ScoreArgs {
     const uint16_t* cnt;     // prefix counts [E][U][K][nb-1]
+    const uint32_t* cnt32;   // the same as 32-bit counts (eras above 65535 rows), or null
     const int32_t* tot_cnt;  // [E][U]
     const float* g;          // prefix grads [E][U][K][nb-1]
     const float* tot_g;      // [E][U]
@@ -132,7 +162,8 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
 // Launchers (defined in the .hip files; all return hipError_t of the launch).
 hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s);
-hipError_t launch_kcuts(const uint16_t* cnt, const int32_t* tot_cnt, int32_t E, int32_t U, int32_t K,
+hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt, int32_t E,
+                        int32_t U, int32_t K,
                         int32_t nb,
                         int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                         int32_t* thr_tab, hipStream_t s);

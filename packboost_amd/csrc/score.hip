@@ -109,6 +109,8 @@ struct PairIn {
     float Gt, GL;
 };
 
+// C32: the planes carry 32-bit counts (an era above 65535 rows)
+template <bool C32>
 __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     extern __shared__ unsigned char smem[];
     const int tid = threadIdx.x;
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                 const int64_t to = (int64_t)(e0 + el) * a.U + u;
                 pin[i].ctot = a.tot_cnt[to];
                 pin[i].Gt = a.tot_g[to];
-                pin[i].L = a.cnt[off + thr];
+                pin[i].L = C32 ? (int)a.cnt32[off + thr] : (int)a.cnt[off + thr];
                 pin[i].GL = a.g[off + thr];
             }
         }
@@ -318,6 +320,7 @@ constexpr int kPcEras = kScoreChunkEras;  // eras per chunk
 constexpr int kPcProducers = kBlock - kWave;
 constexpr int kPcPairs = (kPcEras * kWave + kPcProducers - 1) / kPcProducers;
 
+template <bool C32>
 __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
     extern __shared__ unsigned char smem[];
     const int tid = threadIdx.x;
@@ -390,7 +393,7 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
                 const int64_t to = (int64_t)(e0 + slot_el[i]) * a.U + u;  // era total
                 pin[i].ctot = a.tot_cnt[to];
                 pin[i].Gt = a.tot_g[to];
-                pin[i].L = a.cnt[off];
+                pin[i].L = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
                 pin[i].GL = a.g[off];
             }
         }
@@ -605,8 +608,8 @@ __device__ void even_cuts(int nb, int k, int32_t* out) {
     while (m < kk) { out[m] = out[m - 1]; ++m; }
 }
 
-__global__ void kcuts_kernel(const uint16_t* cnt, const int32_t* tot_cnt, int32_t E, int32_t U,
-                             int32_t K, int32_t nb,
+__global__ void kcuts_kernel(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt,
+                             int32_t E, int32_t U, int32_t K, int32_t nb,
                              int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                              int32_t* thr_tab) {
     const int kf = blockIdx.x * blockDim.x + threadIdx.x;
@@ -627,8 +630,8 @@ __global__ void kcuts_kernel(const uint16_t* cnt, const int32_t* tot_cnt, int32_
     for (int b = 0; b < nb; ++b) cdf[b] = 0;
     for (int e = 0; e < E; ++e)
         for (int u = 0; u < Ua; ++u) {
-            const uint16_t* p = cnt + (((int64_t)e * U + u) * K + kf) * (nb - 1);
-            for (int b = 0; b < nb - 1; ++b) cdf[b] += p[b];
+            const int64_t base = (((int64_t)e * U + u) * K + kf) * (nb - 1);
+            for (int b = 0; b < nb - 1; ++b) cdf[b] += cnt32 ? cnt32[base + b] : cnt[base + b];
             cdf[nb - 1] += tot_cnt[(int64_t)e * U + u];
         }
     const long long total = cdf[nb - 1];
@@ -859,28 +862,33 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
     return sh;
 }
 
-hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
-    const void* fn = (a.T < kWave) ? reinterpret_cast<const void*>(&des_score_pc_kernel)
-                                    : reinterpret_cast<const void*>(&des_score_kernel);
+template <bool C32>
+hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+    const void* fn = (a.T < kWave) ? reinterpret_cast<const void*>(&des_score_pc_kernel<C32>)
+                                    : reinterpret_cast<const void*>(&des_score_kernel<C32>);
     if (lds_bytes > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds_bytes);
         if (e != hipSuccess) return e;
     }
     if (a.T < kWave)
-        hipLaunchKernelGGL(des_score_pc_kernel, dim3(grid), dim3(kBlock), lds_bytes, s, a);
+        hipLaunchKernelGGL(des_score_pc_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
     else
-        hipLaunchKernelGGL(des_score_kernel, dim3(grid), dim3(kBlock), lds_bytes, s, a);
+        hipLaunchKernelGGL(des_score_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
     return hipGetLastError();
 }
 
-hipError_t launch_kcuts(const uint16_t* cnt, const int32_t* tot_cnt, int32_t E, int32_t U, int32_t K,
-                        int32_t nb, int32_t k, int32_t mass, const Frontier* st, int32_t depth,
-                        int32_t* thr_tab, hipStream_t s) {
+hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+    return a.cnt32 ? launch_score_c<true>(a, grid, lds_bytes, s) : launch_score_c<false>(a, grid, lds_bytes, s);
+}
+
+hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt, int32_t E,
+                        int32_t U, int32_t K, int32_t nb, int32_t k, int32_t mass, const Frontier* st,
+                        int32_t depth, int32_t* thr_tab, hipStream_t s) {
     const int threads = 64;
     const int grid = (K + threads - 1) / threads;
-    hipLaunchKernelGGL(kcuts_kernel, dim3(grid), dim3(threads), 0, s, cnt, tot_cnt, E, U, K, nb, k,
-                       mass, st, depth, thr_tab);
+    hipLaunchKernelGGL(kcuts_kernel, dim3(grid), dim3(threads), 0, s, cnt, cnt32, tot_cnt, E, U, K,
+                       nb, k, mass, st, depth, thr_tab);
     return hipGetLastError();
 }
 

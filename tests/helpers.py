@@ -44,18 +44,20 @@ def node_era_rows(p: dict) -> list[list[np.ndarray]]:
     return out
 
 
-def decode_planes(cnt_raw: np.ndarray, g_raw: np.ndarray, E: int, M: int, K: int, nb: int):
-    """Compact histogram planes (uint16 prefix counts and float32 prefix grads [E][M][K][nb-1],
-    era totals [E][M] at element round_up(E*M*K*(nb-1), 64) of each buffer) expanded to the
-    reference's [E][M][K][nb] prefix form (bin nb-1 = era total, repeated per feature)."""
+def decode_planes(cnt_raw: np.ndarray, g_raw: np.ndarray, E: int, M: int, K: int, nb: int,
+                  cnt32: bool = False):
+    """Compact histogram planes (uint16 prefix counts, uint32 when an era holds more than 65535
+    rows, and float32 prefix grads [E][M][K][nb-1]; era totals [E][M] at element
+    round_up(E*M*K*(nb-1), 64) of each buffer) expanded to the reference's [E][M][K][nb]
+    prefix form (bin nb-1 = era total, repeated per feature)."""
     cells = E * M * K * (nb - 1)
     tot = (cells + 63) // 64 * 64
     cnt_raw = np.ascontiguousarray(cnt_raw, dtype=np.int32)
-    c16 = cnt_raw.view(np.uint16)[:cells].reshape(E, M, K, nb - 1)
+    c16 = (cnt_raw.view(np.uint32) if cnt32 else cnt_raw.view(np.uint16))[:cells].reshape(E, M, K, nb - 1)
     ct = cnt_raw[tot: tot + E * M].reshape(E, M)
     g = np.asarray(g_raw, dtype=np.float32)[:cells].reshape(E, M, K, nb - 1)
     gt = np.asarray(g_raw, dtype=np.float32)[tot: tot + E * M].reshape(E, M)
-    c = np.concatenate([c16.astype(np.int32), np.repeat(ct[:, :, None, None], K, axis=2)], axis=3)
+    c = np.concatenate([c16.astype(np.int64), np.repeat(ct[:, :, None, None].astype(np.int64), K, axis=2)], axis=3)
     gg = np.concatenate([g, np.repeat(gt[:, :, None, None], K, axis=2)], axis=3)
     return c, gg
 
@@ -140,7 +142,8 @@ class GpuDepth:
     def planes(self):
         """The device planes in the reference's [E][U][K][nb] prefix form."""
         E, M, K, nb, _, _ = self._plane_layout()
-        c, g = decode_planes(self.cnt.cpu().numpy(), self.g.cpu().numpy(), E, M, K, nb)
+        cnt32 = int(np.diff(self.offs).max(initial=0)) > 0xFFFF
+        c, g = decode_planes(self.cnt.cpu().numpy(), self.g.cpu().numpy(), E, M, K, nb, cnt32)
         U = self.p["U"]
         return c[:, :U], g[:, :U]
 
@@ -150,6 +153,7 @@ class GpuDepth:
         torch = self.torch
         E, M, K, nb, cells, tot = self._plane_layout()
         U = cnt.shape[1]
+        assert int(np.diff(self.offs).max(initial=0)) <= 0xFFFF, "writes the 16-bit count layout"
         assert cnt[..., : nb - 1].max(initial=0) <= 0xFFFF
         c16 = np.zeros((E, M, K, nb - 1), np.uint16)
         c16[:, :U] = cnt[..., : nb - 1]

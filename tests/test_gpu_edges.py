@@ -1,5 +1,6 @@
 """Edge shapes of the HIP path against the oracle: the largest era the 16-bit count field
-holds (65535 rows) and the clean rejection above it, a thousand eras of 0-5 rows, minimal
+holds (65535 rows), eras split into segments (up to 100k rows, and a fit without eras), a
+thousand eras of 0-5 rows, minimal
 shapes (one feature, two bins, depth 1), deep trees whose frontiers need node tiles, and a
 255-bin fit.
 
@@ -51,37 +52,37 @@ def test_largest_era(hip, oracle_mod, layout):
         g.close()
 
 
-def test_era_above_count_field_is_rejected(hip):
-    import ctypes
-
-    lib = hip.load()
-    N = 65536 + 16
-    dims = hip.PbDims(num_rows=N, ld=N, num_features=2, num_eras=2, max_bins=5, max_depth=2,
-                      max_feats=2, min_samples_leaf=1)
-    offs = np.array([0, 65536, N], np.int32)
-    ctx = ctypes.c_void_p()
-    hip.check(lib.pb_ctx_create(ctypes.byref(dims), offs.ctypes.data, ctypes.byref(ctx)), "ctx")
+@pytest.mark.parametrize("sizes,nb,U,layout", [
+    ((100_000, 7_000), 5, 2, "u8"),           # above the 16-bit count field: 32-bit planes
+    ((100_000, 7_000), 5, 2, "nibble"),
+    ((20_000, 41_000, 9_000, 16_385), 9, 3, "nibble"),  # split eras, 16-bit planes
+    ((70_001,), 200, 2, "u8"),                # one big era, single-feature histograms
+], ids=["big-u8", "big-nibble", "split", "one-era-200bins"])
+def test_split_eras(hip, oracle_mod, sizes, nb, U, layout):
+    """Eras above the segment size are built in parts whose exact sums are added up before the
+    planes are written: the planes equal the oracle's whatever the split."""
+    print(f"[split eras] {sizes} nb={nb} U={U} {layout}", flush=True)
+    N, F, E = int(sum(sizes)), 5, len(sizes)
+    p = make_problem(len(sizes) * 7 + nb, N, F, E, nb, U, ragged=False)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    p["era_off"] = offs
+    p["era"] = np.repeat(np.arange(E), sizes)
+    feats = np.arange(F, dtype=np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, want_planes=True)
+    g = GpuDepth(hip, p, F, msl=1, layout=layout)
     try:
-        import torch
-
-        dev = torch.device("cuda")
-        bins = torch.zeros((2, N), dtype=torch.uint8, device=dev)
-        grad = torch.zeros(N, device=dev)
-        nid = torch.zeros(N, dtype=torch.int16, device=dev)
-        tn = torch.zeros(N, dtype=torch.int16, device=dev)
-        hip.check(lib.pb_round_begin(ctx, grad.data_ptr(), grad.data_ptr(), grad.data_ptr(),
-                                     nid.data_ptr(), tn.data_ptr(), None), "round_begin")
-        feats = torch.arange(2, dtype=torch.int32, device=dev)
-        plane = int(lib.pb_hist_plane_elems(ctx, 1))
-        cnt = torch.zeros(plane, dtype=torch.int32, device=dev)
-        gp = torch.zeros(plane, device=dev)
-        rc = lib.pb_hist_build(ctx, bins.data_ptr(), grad.data_ptr(), nid.data_ptr(), feats.data_ptr(),
-                               2, 0, 1, cnt.data_ptr(), gp.data_ptr(), None)
-        assert rc == hip.PB_ERR_UNSUPPORTED
-        assert "65535" in hip.last_error()
-        torch.cuda.synchronize()
+        g.hist(feats)
+        cnt, gp = g.planes()
+        np.testing.assert_array_equal(cnt, ref.planes[0])
+        err = np.abs(gp.astype(np.float64) - ref.planes[1].astype(np.float64))
+        assert np.all(err <= 1e-5 * np.maximum(_abs_mass(p, U)[:, :, None, None], 1.0))
+        # the split-era sums are cleared for the next build: a second build gives the same planes
+        g.hist(feats)
+        cnt2, gp2 = g.planes()
+        np.testing.assert_array_equal(cnt2, cnt)
+        np.testing.assert_array_equal(gp2, gp)
     finally:
-        lib.pb_ctx_destroy(ctx)
+        g.close()
 
 
 def _fit_vs_oracle(oracle_mod, bins, y, era, rounds, **cfg_kw):
@@ -154,6 +155,17 @@ def test_deep_tree_fit(hip, oracle_mod, nb):
                                 learning_rate=0.1, lambda_l2=0.1, lambda_dro=0.1,
                                 min_samples_leaf=12, max_bins=nb, random_state=6)
     assert max(int(np.count_nonzero(~np.asarray(r["is_leaf"]))) for r in ref.rounds) > 128
+
+
+def test_fit_without_eras_large(hip, oracle_mod):
+    """era=None puts all 150k rows in one era: built in segments, 32-bit counts."""
+    print("[no eras, 150k rows]", flush=True)
+    rng = np.random.default_rng(15)
+    N, F = 150_000, 8
+    bins = rng.integers(0, 12, size=(N, F)).astype(np.int8)
+    y = (_target(rng, bins, k=4) + 0.3 * rng.standard_normal(N).astype(np.float32)).astype(np.float32)
+    _fit_vs_oracle(oracle_mod, bins, y, None, 3, pack_size=2, max_depth=5, learning_rate=0.1,
+                   lambda_l2=1.0, lambda_dro=0.0, min_samples_leaf=50, max_bins=12, random_state=3)
 
 
 def test_255_bins_fit(hip, oracle_mod):
