@@ -345,6 +345,57 @@ int pb_predict_bins(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
                     const float* value_dev, const uint8_t* is_leaf_dev, int32_t num_nodes,
                     float* out_dev, void* stream);
 
+/* ---- row lists ---------------------------------------------------------------------- */
+/* The reference's CUDA backend takes the rows of each frontier node as per-era lists:
+ * rows_index int32 [R] with node_row_splits int32 [S+1] and node_era_splits int32 [S][E+1];
+ * segment (s, e) is rows_index[node_row_splits[s] + node_era_splits[s][e] ..
+ * node_row_splits[s] + node_era_splits[s][e+1]) (frontier_cuda.cu:576-598, 719-726). Bins are
+ * feature-major uint8 [F][ld] with N rows (the reference's int8 [F][N], booster.py:419-426).
+ *
+ * These entry points are fully asynchronous and check every index on the device: after the
+ * stream has run them, work_dev[0..3] are nonzero if a segment lay outside [0, R), a row id
+ * outside [0, N), a feature outside [0, F), or an output would pass its capacity (nothing is
+ * read or written out of range; results are then unspecified). work_dev: int32
+ * [pb_rowlist_work_elems(nodes, E)], the nodes of the call. */
+int64_t pb_rowlist_work_elems(int32_t num_nodes, int32_t num_eras);
+
+/* partition_frontier_cuda (frontier_cuda.cu:719-851; the CPU path's stable per-era split,
+ * frontier_cpu.cpp:446-497): every segment (s, e) splits stably into its rows with
+ * bin[feat[s]][row] <= thr[s] (left) and the rest (right), in list order. left_index and
+ * right_index receive the node-major, era-minor concatenation (capacity entries each; R
+ * suffices for disjoint segments); left_splits / right_splits int32 [S][E+1] are absolute
+ * offsets into them (entry [S-1][E] = the total). */
+int pb_rowlist_partition(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
+                         const int32_t* rows_dev, int64_t R, const int32_t* node_row_splits_dev,
+                         const int32_t* node_era_splits_dev, int32_t S, int32_t E,
+                         const int32_t* feat_dev, const int32_t* thr_dev, int32_t* left_index_dev,
+                         int32_t* right_index_dev, int64_t capacity, int32_t* left_splits_dev,
+                         int32_t* right_splits_dev, int32_t* work_dev, void* stream);
+
+/* The row-gathering half of find_best_splits_batched_cuda (frontier_cuda.cu:576-716, which
+ * reads bins[f][rows_index[i]] and grad[i] per list position): the listed rows of nodes
+ * [node_begin, node_end) in era-major order (era, then node, then list order), the layout
+ * pb_hist_build reads. Position d receives out_bins[k][d] = bins[feats[k]][row] (k < K),
+ * out_values[d] = values[i] (values: float32 [R] per list position, e.g. grad) and
+ * out_slot[d] = node - node_begin; era_off_dev int32 [E+1] receives the era boundaries
+ * (era_off[E] = the rows gathered, at most out_ld). Positions past era_off[E] are not
+ * written. Up to 65534 nodes per call. */
+int pb_rowlist_gather(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
+                      const int32_t* feats_dev, int32_t K, const float* values_dev,
+                      const int32_t* rows_dev, int64_t R, const int32_t* node_row_splits_dev,
+                      const int32_t* node_era_splits_dev, int32_t node_begin, int32_t node_end,
+                      int32_t E, uint8_t* out_bins_dev, int64_t out_ld, float* out_values_dev,
+                      uint16_t* out_slot_dev, int32_t* era_off_dev, int32_t* work_dev, void* stream);
+
+/* The per-(node, feature) pick of find_best_splits_batched_cuda (frontier_cuda.cu:537-560)
+ * over candidate records cand_dev [M][K][T] (pb_des_score's cand_all_dev, thresholds in
+ * order): the best valid score wins; within 1e-12 of it the larger left count, then the
+ * larger threshold. No valid candidate, or a non-finite best, gives score -inf (or the best),
+ * threshold -1 and zero sums. Outputs [M][K]: left_hess = left count (squared loss). */
+int pb_best_thresholds(const pb_candidate* cand_dev, int32_t M, int32_t K, int32_t T,
+                       float* scores_dev, int32_t* thresholds_dev, float* left_grad_dev,
+                       float* left_hess_dev, int64_t* left_count_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,7 +34,8 @@ EXPORTED_SYMBOLS = (
     "pb_profile_read", "pb_frontier_set", "pb_frontier_counts", "pb_predict_pack",
     "pb_predict_forest", "pb_predict_bins", "pb_era_corr", "pb_quantile_edges", "pb_apply_bins",
     "pb_forest_create", "pb_forest_predict", "pb_forest_destroy", "pb_pack_bins4",
-    "pb_set_bin_layout", "pb_select_subsets",
+    "pb_set_bin_layout", "pb_select_subsets", "pb_rowlist_work_elems", "pb_rowlist_partition",
+    "pb_rowlist_gather", "pb_best_thresholds",
 )
 
 
@@ -127,6 +128,12 @@ _SIGNATURES = {
                                          _I32, _I32, _F32, _VP, _VP]),
     "pb_predict_bins": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _I32,
                                        _VP, _VP]),
+    "pb_rowlist_work_elems": (_I64, [_I32, _I32]),
+    "pb_rowlist_partition": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I64, _VP, _VP, _I32, _I32, _VP,
+                                            _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP]),
+    "pb_rowlist_gather": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I32, _VP, _VP, _I64, _VP, _VP,
+                                         _I32, _I32, _I32, _VP, _I64, _VP, _VP, _VP, _VP, _VP]),
+    "pb_best_thresholds": (ctypes.c_int, [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -3,9 +3,11 @@
 The reference's CUDA path hands its split finder and partition per-node, per-era row lists
 (`rows_index` with `node_row_splits` / `node_era_splits`, frontier_cuda.cu:576-716, 719-851;
 callers booster.py:1414-1431, 1485-1492, 2027-2034). This backend grows trees from per-row
-node ids over era-major rows instead (pb_hist_build / pb_des_score), so these adapters gather
-the listed rows of the requested features into that layout, run the HIP histogram and DES
-scorer, and return the reference's schemas:
+node ids over era-major rows instead (pb_hist_build / pb_des_score). The adapters orchestrate
+HIP entry points only (torch allocates the buffers): pb_rowlist_gather moves the listed rows of
+the requested features into that layout, pb_hist_build / pb_des_score score them,
+pb_best_thresholds picks per (node, feature), and pb_rowlist_partition splits the lists. They
+return the reference's schemas:
 
   find_best_splits_batched_rowlist -> {scores f32 [M,K] (-inf: no valid threshold),
       thresholds i32 [M,K] (-1), left_grad f32, left_hess f32, left_count i64 [M,K], kernel_ms}
@@ -47,12 +49,31 @@ def _era_alpha(era_weights: torch.Tensor, counts: torch.Tensor) -> float:
     return float(alpha[0])
 
 
-def _segments(node_row_splits: torch.Tensor, node_era_splits: torch.Tensor):
-    """Per concatenated row position: its node and era (rows are node-major, era-minor)."""
-    counts = (node_era_splits[:, 1:] - node_era_splits[:, :-1]).to(torch.int64)  # [M, E]
-    M, E = counts.shape
-    seg = torch.repeat_interleave(torch.arange(M * E, device=counts.device), counts.reshape(-1))
-    return counts, seg // E, seg % E
+_STATUS = ("a (node, era) segment lies outside rows_index", "a row id lies outside [0, N)",
+           "a feature id lies outside [0, F)", "an output would pass its capacity")
+
+
+def _check_status(work: torch.Tensor, what: str) -> None:
+    st = work[:4].cpu().tolist()
+    bad = [msg for flag, msg in zip(st, _STATUS) if flag]
+    if bad:
+        raise RuntimeError(f"{what}: " + "; ".join(bad))
+
+
+def _bins_fm(bins: torch.Tensor):
+    """Feature-major uint8 bins [F][N] (the reference's int8 [F][N]) and their row stride."""
+    if bins.dim() != 2:
+        raise ValueError("bins must be a 2-D feature-major [F, N] tensor")
+    b = bins.view(torch.uint8) if bins.dtype == torch.int8 else bins
+    if b.dtype != torch.uint8:
+        raise TypeError("bins must be int8 or uint8")
+    if b.stride(1) != 1:
+        b = b.contiguous()
+    return b, int(b.shape[0]), int(b.shape[1]), int(b.stride(0))
+
+
+def _i32(t: torch.Tensor, dev) -> torch.Tensor:
+    return t.to(device=dev, dtype=torch.int32).contiguous()
 
 
 def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_splits, node_era_splits,
@@ -70,66 +91,71 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
         raise ValueError("max_bins must lie in [2, 255]")
     if bool((hess.to(torch.float32) != 1.0).any()):
         raise RuntimeError("HIP backend supports squared loss only (hess == 1)")
-    counts, node_of, era_of = _segments(node_row_splits.to(dev), node_era_splits.to(dev))
-    E = int(counts.shape[1])
+    b_fm, F, N, ld_in = _bins_fm(bins)
+    rows = _i32(rows_index, dev)
+    nrs = _i32(node_row_splits, dev)
+    nes = _i32(node_era_splits, dev)
+    E = int(nes.shape[1]) - 1
+    if E < 1:
+        raise ValueError("node_era_splits must have at least 2 columns")
+    counts = nes[:, 1:] - nes[:, :-1]  # [M, E]
     alpha = _era_alpha(era_weights, counts)
     K = int(feature_ids.numel())
-    feats_all = feature_ids.to(device=dev, dtype=torch.int64)
+    fid = _i32(feature_ids, dev)
+    vals = grad.to(device=dev, dtype=torch.float32).contiguous()
+    R = int(rows.numel())
     T = k_cuts if 0 < int(k_cuts) < nb - 1 else nb - 1
     out_s = torch.full((M, K), float("-inf"), dtype=torch.float32, device=dev)
     out_t = torch.full((M, K), -1, dtype=torch.int32, device=dev)
     out_g = torch.zeros((M, K), dtype=torch.float32, device=dev)
     out_h = torch.zeros((M, K), dtype=torch.float32, device=dev)
     out_c = torch.zeros((M, K), dtype=torch.int64, device=dev)
+    if K == 0:
+        return {"scores": out_s, "thresholds": out_t, "left_grad": out_g, "left_hess": out_h,
+                "left_count": out_c, "kernel_ms": 0.0}
     p = _hip.PbSplitParams(lambda_l2=float(lambda_l2), lambda_dro=float(lambda_dro),
                            direction_weight=float(direction_weight), era_alpha=alpha,
                            min_samples_leaf=int(min_samples_leaf), k_cuts=int(k_cuts),
                            cut_selection=1 if str(cut_selection) == "mass" else 0, reserved=0)
+    # rows listed per node (the gather places exactly these when the segments are consistent)
+    node_rows = (nes[:, E] - nes[:, 0]).to(torch.int64).clamp_min(0).cpu()
+    s = _hip.stream_ptr()
     t0 = time.perf_counter()
-    pos_all = torch.arange(int(rows_index.numel()), device=dev)
     for m0 in range(0, M, _NODE_CHUNK):
         m1 = min(M, m0 + _NODE_CHUNK)
-        sel = (node_of >= m0) & (node_of < m1)
-        pos = pos_all[sel]
-        # era-major, then node, then list order: the rows of era e are contiguous
-        key = era_of[sel] * (m1 - m0) + (node_of[sel] - m0)
-        order = torch.sort(key, stable=True).indices
-        pos = pos[order]
-        node = (node_of[pos] - m0).to(torch.int32)
-        R = int(pos.numel())
-        if R == 0:
-            continue
-        era_sizes = torch.bincount(era_of[pos], minlength=E)
-        era_off = np.zeros(E + 1, dtype=np.int32)
-        era_off[1:] = np.cumsum(era_sizes.cpu().numpy())
-        if int(era_sizes.max()) > 65535:
-            raise RuntimeError("HIP backend: an era holds more than 65535 rows of the listed nodes")
-        ld = (R + 15) // 16 * 16
-        rows = rows_index.to(dev, torch.int64)[pos]
-        b = torch.zeros((K, ld), dtype=torch.uint8, device=dev)
-        b[:, :R] = bins.index_select(0, feats_all).index_select(1, rows).view(torch.uint8) \
-            if bins.dtype in (torch.int8, torch.uint8) else \
-            bins.index_select(0, feats_all).index_select(1, rows).to(torch.uint8)
-        preds = torch.zeros(ld, dtype=torch.float32, device=dev)
-        preds[:R] = grad.to(dev, torch.float32)[pos]
-        zeros = torch.zeros(ld, dtype=torch.float32, device=dev)
-        g = torch.zeros(ld, dtype=torch.float32, device=dev)
-        nid = torch.full((ld,), -1, dtype=torch.int16, device=dev)   # 0xFFFF: pad rows
-        tnode = torch.zeros(ld, dtype=torch.int16, device=dev)
         U = m1 - m0
+        cap = int(node_rows[m0:m1].sum())
+        if cap == 0:
+            continue
+        ld = (cap + 15) // 16 * 16
+        b = torch.zeros((K, ld), dtype=torch.uint8, device=dev)
+        preds = torch.zeros(ld, dtype=torch.float32, device=dev)
+        nid = torch.full((ld,), -1, dtype=torch.int16, device=dev)  # 0xFFFF: rows in no node
+        era_off_dev = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        work = torch.empty(int(lib.pb_rowlist_work_elems(U, E)), dtype=torch.int32, device=dev)
+        _hip.check(lib.pb_rowlist_gather(b_fm.data_ptr(), N, ld_in, F, fid.data_ptr(), K, vals.data_ptr(),
+                                         rows.data_ptr(), R, nrs.data_ptr(), nes.data_ptr(), m0, m1, E,
+                                         b.data_ptr(), ld, preds.data_ptr(), nid.data_ptr(),
+                                         era_off_dev.data_ptr(), work.data_ptr(), s), "pb_rowlist_gather")
+        _check_status(work, "find_best_splits_batched_cuda")
+        era_off = np.ascontiguousarray(era_off_dev.cpu().numpy())
+        Rc = int(era_off[E])
+        if Rc == 0:
+            continue
+        zeros = torch.zeros(ld, dtype=torch.float32, device=dev)
+        g = torch.empty(ld, dtype=torch.float32, device=dev)
+        nid_root = torch.empty(ld, dtype=torch.int16, device=dev)  # pb_round_begin's root ids, unused
+        tnode = torch.empty(ld, dtype=torch.int16, device=dev)
         depth = max(0, math.ceil(math.log2(U)))
-        dims = _hip.PbDims(num_rows=R, ld=ld, num_features=K, num_eras=E, max_bins=nb,
-                           max_depth=depth + 1, max_feats=K, min_samples_leaf=1)
+        dims = _hip.PbDims(num_rows=Rc, ld=ld, num_features=K, num_eras=E, max_bins=nb,
+                           max_depth=depth + 1, max_feats=K, min_samples_leaf=0)
         ctx = ctypes.c_void_p()
         _hip.check(lib.pb_ctx_create(ctypes.byref(dims), era_off.ctypes.data, ctypes.byref(ctx)),
                    "pb_ctx_create")
         try:
-            s = _hip.stream_ptr()
-            # grad = preds - 0 (exact), max|grad| for the fixed-point scale
+            # grad = values - 0 (exact) and max|grad| for the histogram's fixed-point scale
             _hip.check(lib.pb_round_begin(ctx, preds.data_ptr(), zeros.data_ptr(), g.data_ptr(),
-                                          nid.data_ptr(), tnode.data_ptr(), s), "pb_round_begin")
-            nid[:R] = node.to(torch.int16)
-            nid[R:] = -1
+                                          nid_root.data_ptr(), tnode.data_ptr(), s), "pb_round_begin")
             _hip.check(lib.pb_frontier_set(ctx, depth, U, None, U, s), "pb_frontier_set")
             mx = int(lib.pb_max_nodes(ctx, depth))
             if mx < U:
@@ -141,35 +167,16 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
             _hip.check(lib.pb_hist_build(ctx, b.data_ptr(), g.data_ptr(), nid.data_ptr(),
                                          local.data_ptr(), K, depth, mx, cnt.data_ptr(), gp.data_ptr(),
                                          s), "pb_hist_build")
-            cand = torch.zeros(mx * K * T * _hip.CANDIDATE_DTYPE.itemsize, dtype=torch.uint8, device=dev)
-            fid = feature_ids.to(dev, torch.int32).contiguous()
+            cand = torch.empty(mx * K * T * _hip.CANDIDATE_DTYPE.itemsize, dtype=torch.uint8, device=dev)
             _hip.check(lib.pb_des_score(ctx, cnt.data_ptr(), gp.data_ptr(), fid.data_ptr(), K, depth,
                                         mx, ctypes.byref(p), cand.data_ptr(), s), "pb_des_score")
-            rec = cand.view(torch.int32).reshape(mx, K, T, 8)[:U]
+            _hip.check(lib.pb_best_thresholds(cand.data_ptr(), U, K, T, out_s[m0].data_ptr(),
+                                              out_t[m0].data_ptr(), out_g[m0].data_ptr(),
+                                              out_h[m0].data_ptr(), out_c[m0].data_ptr(), s),
+                       "pb_best_thresholds")
         finally:
             torch.cuda.synchronize(dev)
             lib.pb_ctx_destroy(ctx)
-        score = rec[..., 0].view(torch.float32)
-        lt = rec[..., 1].to(torch.int64)
-        lg = rec[..., 2].view(torch.float32)
-        thr = rec[..., 4]
-        valid = rec[..., 5] != 0
-        # per (node, feature): the CUDA path's tie-break over thresholds
-        s_ok = torch.where(valid, score, torch.full_like(score, float("-inf")))
-        best = s_ok.max(dim=2, keepdim=True).values
-        elig = valid & (s_ok >= best - 1e-12)
-        lt_e = torch.where(elig, lt, torch.full_like(lt, -1))
-        lt_best = lt_e.max(dim=2, keepdim=True).values
-        elig = elig & (lt == lt_best)
-        thr_e = torch.where(elig, thr, torch.full_like(thr, -1))
-        pick = thr_e.argmax(dim=2, keepdim=True)
-        has = elig.any(dim=2)
-        out_s[m0:m1] = torch.where(has, s_ok.gather(2, pick)[..., 0], out_s[m0:m1])
-        out_t[m0:m1] = torch.where(has, thr.gather(2, pick)[..., 0], out_t[m0:m1])
-        out_g[m0:m1] = torch.where(has, lg.gather(2, pick)[..., 0], out_g[m0:m1])
-        cnt_pick = lt.gather(2, pick)[..., 0]
-        out_c[m0:m1] = torch.where(has, cnt_pick, out_c[m0:m1])
-        out_h[m0:m1] = torch.where(has, cnt_pick.to(torch.float32), out_h[m0:m1])
     kernel_ms = (time.perf_counter() - t0) * 1e3
     return {"scores": out_s, "thresholds": out_t, "left_grad": out_g, "left_hess": out_h,
             "left_count": out_c, "kernel_ms": kernel_ms}
@@ -177,6 +184,7 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
 
 def partition_frontier_rowlist(bins, rows_index, node_row_splits, node_era_splits, feat_per_node,
                                thr_per_node):
+    lib = _hip.load()
     dev = bins.device
     S = int(node_row_splits.numel()) - 1
     if S <= 0:
@@ -184,25 +192,25 @@ def partition_frontier_rowlist(bins, rows_index, node_row_splits, node_era_split
         return {"left_index": z, "right_index": z.clone(),
                 "left_splits": torch.empty((0, 0), dtype=torch.int32, device=dev),
                 "right_splits": torch.empty((0, 0), dtype=torch.int32, device=dev)}
-    counts, node, era = _segments(node_row_splits.to(dev), node_era_splits.to(dev))
-    E = int(counts.shape[1])
-    rows = rows_index.to(dev, torch.int64)
-    f = feat_per_node.to(dev, torch.int64)[node]
-    t = thr_per_node.to(dev, torch.int32)[node]
-    bv = bins.view(torch.uint8) if bins.dtype == torch.int8 else bins
-    go_left = bv[f, rows].to(torch.int32) <= t   # left iff bin <= threshold
-    left_index = rows_index.to(dev, torch.int32)[go_left]
-    right_index = rows_index.to(dev, torch.int32)[~go_left]
-    seg = node * E + era
-    lc = torch.zeros(S * E, dtype=torch.int64, device=dev).index_add_(0, seg, go_left.to(torch.int64))
-    lc = lc.reshape(S, E)
-    rc = counts - lc
-    zero = torch.zeros((S, 1), dtype=torch.int64, device=dev)
-
-    def absolute(c):
-        local = torch.cat([zero, c.cumsum(1)], 1)
-        base = torch.cat([zero[:1, 0], c.sum(1).cumsum(0)[:-1]])
-        return (local + base[:, None]).to(torch.int32)
-
-    return {"left_index": left_index, "right_index": right_index,
-            "left_splits": absolute(lc), "right_splits": absolute(rc)}
+    b_fm, F, N, ld_in = _bins_fm(bins)
+    rows = _i32(rows_index, dev)
+    nrs = _i32(node_row_splits, dev)
+    nes = _i32(node_era_splits, dev)
+    E = int(nes.shape[1]) - 1
+    R = int(rows.numel())
+    feat = _i32(feat_per_node, dev)
+    thr = _i32(thr_per_node, dev)
+    if feat.numel() < S or thr.numel() < S:
+        raise ValueError("feat_per_node and thr_per_node need one entry per node")
+    left = torch.empty(R, dtype=torch.int32, device=dev)
+    right = torch.empty(R, dtype=torch.int32, device=dev)
+    ls = torch.empty((S, E + 1), dtype=torch.int32, device=dev)
+    rs = torch.empty((S, E + 1), dtype=torch.int32, device=dev)
+    work = torch.empty(int(lib.pb_rowlist_work_elems(S, E)), dtype=torch.int32, device=dev)
+    _hip.check(lib.pb_rowlist_partition(b_fm.data_ptr(), N, ld_in, F, rows.data_ptr(), R, nrs.data_ptr(),
+                                        nes.data_ptr(), S, E, feat.data_ptr(), thr.data_ptr(),
+                                        left.data_ptr(), right.data_ptr(), R, ls.data_ptr(), rs.data_ptr(),
+                                        work.data_ptr(), _hip.stream_ptr()), "pb_rowlist_partition")
+    _check_status(work, "partition_frontier_cuda")
+    nl, nr = int(ls[-1, -1]), int(rs[-1, -1])
+    return {"left_index": left[:nl], "right_index": right[:nr], "left_splits": ls, "right_splits": rs}

@@ -19,7 +19,8 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libpackboost_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["hist.hip", "score.hip", "partition.hip", "predict.hip", "metrics.hip", "binning.hip", "capi.cpp"]
+SOURCES = ["hist.hip", "score.hip", "partition.hip", "predict.hip", "metrics.hip", "binning.hip", "rowlist.hip",
+           "capi.cpp"]
 ARCH = "gfx950"
 
 

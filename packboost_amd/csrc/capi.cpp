@@ -7,6 +7,7 @@
 #include <array>
 #include <utility>
 #include <cstdio>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -925,6 +926,72 @@ int pb_predict_bins(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const
     PB_HIP(pb::launch_predict_bins(bins, N, ld, F, feature, threshold, left, right, value, is_leaf,
                                    num_nodes, out, (hipStream_t)stream),
            "predict_bins launch");
+    return PB_OK;
+}
+
+/* ---- row lists ---------------------------------------------------------------------- */
+
+int64_t pb_rowlist_work_elems(int32_t num_nodes, int32_t num_eras) {
+    if (num_nodes < 0 || num_eras < 0) return -1;
+    return pb::rowlist_work_elems((int64_t)num_nodes * num_eras);
+}
+
+int pb_rowlist_partition(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const int32_t* rows,
+                         int64_t R, const int32_t* node_row_splits, const int32_t* node_era_splits,
+                         int32_t S, int32_t E, const int32_t* feat, const int32_t* thr,
+                         int32_t* left_index, int32_t* right_index, int64_t capacity,
+                         int32_t* left_splits, int32_t* right_splits, int32_t* work, void* stream) {
+    if (S < 0 || E < 0 || N < 0 || R < 0 || F < 0 || capacity < 0)
+        return fail(PB_ERR_INVALID, "pb_rowlist_partition: negative size");
+    if (N > ld) return fail(PB_ERR_INVALID, "pb_rowlist_partition: N must be <= ld");
+    if (R > INT32_MAX || capacity > INT32_MAX)
+        return fail(PB_ERR_RANGE, "pb_rowlist_partition: row lists above 2^31 - 1 entries");
+    if (S == 0) return PB_OK;
+    if (!bins || (!rows && R > 0) || !node_row_splits || !node_era_splits || !feat || !thr ||
+        (!left_index && capacity > 0) || (!right_index && capacity > 0) || !left_splits ||
+        !right_splits || !work)
+        return fail(PB_ERR_INVALID, "pb_rowlist_partition: null argument");
+    PB_HIP(pb::launch_rowlist_partition(bins, N, ld, F, rows, R, node_row_splits, node_era_splits, S, E,
+                                        feat, thr, left_index, right_index, capacity, left_splits,
+                                        right_splits, work, (hipStream_t)stream),
+           "rowlist partition launch");
+    return PB_OK;
+}
+
+int pb_rowlist_gather(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const int32_t* feats,
+                      int32_t K, const float* values, const int32_t* rows, int64_t R,
+                      const int32_t* node_row_splits, const int32_t* node_era_splits,
+                      int32_t node_begin, int32_t node_end, int32_t E, uint8_t* out_bins,
+                      int64_t out_ld, float* out_values, uint16_t* out_slot, int32_t* era_off,
+                      int32_t* work, void* stream) {
+    if (N < 0 || R < 0 || F < 0 || K < 0 || E < 1 || out_ld < 0)
+        return fail(PB_ERR_INVALID, "pb_rowlist_gather: negative size or no eras");
+    if (N > ld) return fail(PB_ERR_INVALID, "pb_rowlist_gather: N must be <= ld");
+    if (node_begin < 0 || node_end <= node_begin || node_end - node_begin >= PB_INACTIVE)
+        return fail(PB_ERR_INVALID, "pb_rowlist_gather: node range must hold 1 .. 65534 nodes");
+    if (R > INT32_MAX || out_ld > INT32_MAX)
+        return fail(PB_ERR_RANGE, "pb_rowlist_gather: row lists above 2^31 - 1 entries");
+    if (!bins || (!feats && K > 0) || (!values && R > 0) || (!rows && R > 0) || !node_row_splits ||
+        !node_era_splits || (!out_bins && K > 0 && out_ld > 0) || (!out_values && out_ld > 0) ||
+        (!out_slot && out_ld > 0) || !era_off || !work)
+        return fail(PB_ERR_INVALID, "pb_rowlist_gather: null argument");
+    PB_HIP(pb::launch_rowlist_gather(bins, N, ld, F, feats, K, values, rows, R, node_row_splits,
+                                     node_era_splits, node_begin, node_end, E, out_bins, out_ld,
+                                     out_values, out_slot, era_off, work, (hipStream_t)stream),
+           "rowlist gather launch");
+    return PB_OK;
+}
+
+int pb_best_thresholds(const pb_candidate* cand, int32_t M, int32_t K, int32_t T, float* scores,
+                       int32_t* thresholds, float* left_grad, float* left_hess, int64_t* left_count,
+                       void* stream) {
+    if (M < 0 || K < 0 || T < 0) return fail(PB_ERR_INVALID, "pb_best_thresholds: negative size");
+    if ((int64_t)M * K == 0) return PB_OK;
+    if (!cand || !scores || !thresholds || !left_grad || !left_hess || !left_count)
+        return fail(PB_ERR_INVALID, "pb_best_thresholds: null argument");
+    PB_HIP(pb::launch_best_thresholds(cand, M, K, T, scores, thresholds, left_grad, left_hess, left_count,
+                                      (hipStream_t)stream),
+           "best thresholds launch");
     return PB_OK;
 }
 

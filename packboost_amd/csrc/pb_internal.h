@@ -185,6 +185,24 @@ hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t 
                             float lr, float* preds, int64_t N, hipStream_t s);
 hipError_t launch_pack_bins4(const uint8_t* bins, int64_t n, int64_t ld, int32_t F, uint8_t* out,
                              hipStream_t s);
+// Row-list kernels (rowlist.hip). Workspace: rowlist_work_elems(segments) int32, whose first
+// four entries are status flags (segment, row id, feature, capacity) left set after the call.
+int64_t rowlist_work_elems(int64_t segments);
+hipError_t launch_rowlist_partition(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                                    const int32_t* rows, int64_t R, const int32_t* nrs,
+                                    const int32_t* nes, int32_t S, int32_t E, const int32_t* feat,
+                                    const int32_t* thr, int32_t* left_out, int32_t* right_out,
+                                    int64_t cap, int32_t* left_splits, int32_t* right_splits,
+                                    int32_t* work, hipStream_t s);
+hipError_t launch_rowlist_gather(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                                 const int32_t* feats, int32_t K, const float* values,
+                                 const int32_t* rows, int64_t R, const int32_t* nrs,
+                                 const int32_t* nes, int32_t m0, int32_t m1, int32_t E,
+                                 uint8_t* out_bins, int64_t out_ld, float* out_values,
+                                 uint16_t* out_slot, int32_t* era_off, int32_t* work, hipStream_t s);
+hipError_t launch_best_thresholds(const pb_candidate* cand, int32_t M, int32_t K, int32_t T,
+                                  float* score, int32_t* thr, float* left_grad, float* left_hess,
+                                  int64_t* left_count, hipStream_t s);
 hipError_t launch_quantile_edges(const float* sorted, int64_t n, int64_t ld, int32_t F,
                                  const double* q, int32_t nq, float* edges, int32_t edge_stride,
                                  hipStream_t s);
