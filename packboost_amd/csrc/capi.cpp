@@ -32,10 +32,9 @@ struct pb_ctx {
     int32_t* thr_tab;
     // histogram work segments (eras above seg_rows rows split into parts; see HistArgs)
     int32_t S;
-    int32_t* seg_off_dev;
-    int32_t* seg_era_dev;
+    int32_t* seg_info_dev;  // [S][4] per work segment: first row, end row, era, slot of a
+                            // split era (-1: the era is one segment)
     int32_t n_acc;          // eras split into several segments
-    int32_t* acc_slot_dev;  // [E] slot of a split era, else -1
     int32_t* acc_era_dev;   // [n_acc]
     uint32_t* acc_cnt;      // [n_acc][umax][max_feats][nb]
     unsigned long long* acc_g;
@@ -120,9 +119,7 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->ids[0]);
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
-    (void)hipFree(c->seg_off_dev);
-    (void)hipFree(c->seg_era_dev);
-    (void)hipFree(c->acc_slot_dev);
+    (void)hipFree(c->seg_info_dev);
     (void)hipFree(c->acc_era_dev);
     (void)hipFree(c->acc_cnt);
     (void)hipFree(c->acc_g);
@@ -207,28 +204,26 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     // work segments: an era above seg_rows rows is split into equal parts of at most seg_rows
     // (<= 65535, the LDS count field) whose exact sums are added up per era
     const int64_t seg_rows = std::min<int64_t>(65535, std::max<int64_t>(256, env_int("PB_HIST_SEG_ROWS", 16384)));
-    std::vector<int32_t> seg_off{0}, seg_era, acc_slot(d.num_eras, -1), acc_era;
+    std::vector<int32_t> seg_info, acc_era;
     for (int e = 0; e < d.num_eras; ++e) {
         const int64_t len = era_off_host[e + 1] - era_off_host[e];
         const int64_t parts = len > seg_rows ? (len + seg_rows - 1) / seg_rows : 1;
-        if (parts > 1) {
-            acc_slot[e] = (int32_t)acc_era.size();
-            acc_era.push_back(e);
-        }
-        for (int64_t j = 1; j <= parts; ++j) {
-            seg_off.push_back((int32_t)(era_off_host[e] + len * j / parts));
-            seg_era.push_back(e);
+        const int32_t slot = parts > 1 ? (int32_t)acc_era.size() : -1;
+        if (parts > 1) acc_era.push_back(e);
+        for (int64_t j = 0; j < parts; ++j) {
+            seg_info.push_back((int32_t)(era_off_host[e] + len * j / parts));
+            seg_info.push_back((int32_t)(era_off_host[e] + len * (j + 1) / parts));
+            seg_info.push_back(e);
+            seg_info.push_back(slot);
         }
     }
-    c->S = (int32_t)seg_era.size();
+    c->S = (int32_t)(seg_info.size() / 4);
     c->n_acc = (int32_t)acc_era.size();
     c->cnt32 = max_era > pb::kMaxEraRowsDirect;
     const size_t acc_cells = (size_t)c->n_acc * c->umax * d.max_feats * d.max_bins;
 
     int rc = PB_OK;
-    if ((rc = dev_alloc(&c->seg_off_dev, seg_off.size(), "alloc segments")) ||
-        (rc = dev_alloc(&c->seg_era_dev, std::max<size_t>(1, seg_era.size()), "alloc segments")) ||
-        (rc = dev_alloc(&c->acc_slot_dev, std::max(1, d.num_eras), "alloc segment slots")) ||
+    if ((rc = dev_alloc(&c->seg_info_dev, std::max<size_t>(4, seg_info.size()), "alloc segments")) ||
         (rc = dev_alloc(&c->acc_era_dev, std::max<size_t>(1, acc_era.size()), "alloc segment slots")) ||
         (rc = dev_alloc(&c->acc_cnt, std::max<size_t>(1, acc_cells), "alloc segment sums")) ||
         (rc = dev_alloc(&c->acc_g, std::max<size_t>(1, acc_cells), "alloc segment sums"))) {
@@ -236,13 +231,9 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
         return rc;
     }
     {
-        hipError_t e1 = hipMemcpy(c->seg_off_dev, seg_off.data(), sizeof(int32_t) * seg_off.size(),
-                                  hipMemcpyHostToDevice);
-        if (e1 == hipSuccess && !seg_era.empty())
-            e1 = hipMemcpy(c->seg_era_dev, seg_era.data(), sizeof(int32_t) * seg_era.size(),
-                           hipMemcpyHostToDevice);
-        if (e1 == hipSuccess && d.num_eras > 0)
-            e1 = hipMemcpy(c->acc_slot_dev, acc_slot.data(), sizeof(int32_t) * acc_slot.size(),
+        hipError_t e1 = hipSuccess;
+        if (!seg_info.empty())
+            e1 = hipMemcpy(c->seg_info_dev, seg_info.data(), sizeof(int32_t) * seg_info.size(),
                            hipMemcpyHostToDevice);
         if (e1 == hipSuccess && !acc_era.empty())
             e1 = hipMemcpy(c->acc_era_dev, acc_era.data(), sizeof(int32_t) * acc_era.size(),
@@ -386,8 +377,10 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     a.bins = bins;
     a.ld = ld_bytes;
     a.nibble = nibble;
-    a.block = (c->hist_block == 128 || c->hist_block == 256) ? c->hist_block
-                                                             : (lds_bytes <= 24 * 1024 ? 128 : 256);
+    // 4-wave workgroups: an era takes fewer passes, and each workgroup's fixed costs (segment
+    // set-up, flush) are shared by twice the rows (measured faster at every depth of a 2.4M-row,
+    // 5-bin round than 2-wave workgroups)
+    a.block = (c->hist_block == 128 || c->hist_block == 256) ? c->hist_block : 256;
     a.grad = grad;
     a.nid = nid;
     a.era_off = c->era_off_dev;
@@ -411,10 +404,8 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
         a.out_g = hist_grad;
         a.out_tot_g = hist_grad + to;
     }
-    a.seg_off = c->seg_off_dev;
-    a.seg_era = c->seg_era_dev;
+    a.seg_info = reinterpret_cast<const int4*>(c->seg_info_dev);
     a.S = c->S;
-    a.acc_slot = c->n_acc > 0 ? c->acc_slot_dev : nullptr;
     a.acc_cnt = c->acc_cnt;
     a.acc_g = c->acc_g;
     const int eras8 = (a.S + 7) / 8 * 8;  // segments, a multiple of the 8 XCDs

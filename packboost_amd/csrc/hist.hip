@@ -122,16 +122,17 @@ void hist_era_kernel(HistArgs a) {
         const int k0 = tile * FT;
         const int nf = min(FT, a.K - k0);
         if (seg >= a.S || nf <= 0 || Un <= 0) continue;  // uniform over the workgroup
-        const int era = a.seg_era[seg];
-        const int slot = a.acc_slot ? a.acc_slot[era] : -1;  // >= 0: add into the era's sums
+        const int4 si = a.seg_info[seg];  // one load: rows, era and slot of the segment
+        const int era = si.z;
+        const int slot = si.w;  // >= 0: add into the era's sums
 
         const int ng = (nf + P - 1) / P;
         const int words = ng * words_group;
         __syncthreads();  // the previous item's flush is done with the LDS
         for (int x = threadIdx.x; x < words; x += BS) lds[x] = 0ull;
 
-        const int r0 = a.seg_off[seg];
-        const int r1 = a.seg_off[seg + 1];
+        const int r0 = si.x;
+        const int r1 = si.y;
         const int a0 = r0 & ~(RL - 1);
 
         const uint8_t* col[FT];
@@ -143,7 +144,8 @@ void hist_era_kernel(HistArgs a) {
         __syncthreads();
 
         char* lds_bytes = reinterpret_cast<char*>(lds);
-        const uint32_t cells_c = (uint32_t)(cells_node * C);
+        const uint32_t cells_c8 = (uint32_t)(cells_node * C) * 8u;  // bytes per node
+        const uint32_t copy8 = copy * 8u;
         // Software pipeline: the next pass's loads are in flight while this pass does its
         // atomics. Columns past the tile's last feature alias that feature (always in bounds);
         // their groups add into LDS that the flush never reads. A lane with no rows in the era
@@ -191,28 +193,40 @@ void hist_era_kernel(HistArgs a) {
             float4 ggn[RL / 4];
     #pragma unroll
             for (int h = 0; h < RL / 4; ++h) ggn[h] = *reinterpret_cast<const float4*>(a.grad + on + 4 * h);
+            // only a lane of the first or last pass holds rows outside the segment
+            const bool full = (c >= r0) && (c + RL <= r1);
     #pragma unroll
           for (int h = 0; h < RL / 4; ++h) {  // quads of rows c + 4h .. c + 4h + 3
             const uint32_t nq0 = h ? nn.z : nn.x;
             const uint32_t nq1 = h ? nn.w : nn.y;
             const uint32_t n4[4] = {nq0 & 0xffffu, nq0 >> 16, nq1 & 0xffffu, nq1 >> 16};
             const float g4[4] = {gg[h].x, gg[h].y, gg[h].z, gg[h].w};
+            bool ok[4];  // row c+4h+j is counted: in the segment and in one of the item's nodes
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) ok[j] = n4[j] - (uint32_t)u0 < (uint32_t)Un;
+            if (!full) {
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = c + 4 * h + j;
+                    ok[j] = ok[j] && r >= r0 && r < r1;
+                }
+            }
             uint32_t base[4];  // byte offset of (node, cell 0, this lane's copy) in a group's block
             unsigned long long qv[4];
             uint32_t keep = 0u;  // uint8 bins: 0xff in byte j iff row c+4h+j is counted
-            bool any = false;    // some row of the quad is counted
     #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int r = c + 4 * h + j;
-                const uint32_t nl = n4[j] - (uint32_t)u0;  // node within the item's tile
-                const bool ok = (r >= r0) && (r < r1) && (nl < (uint32_t)Un);
-                const uint32_t nj = ok ? nl : 0u;
-                base[j] = (__umul24(nj, cells_c) + copy) * 8u;  // nj < 2^16, cells_c < 2^24
-                const long long q = (long long)__float2int_rn(g4[j] * scale);
-                qv[j] = ok ? (((unsigned long long)q << kCountBits) + 1ull) : 0ull;
-                if (!NIB) keep |= ok ? (0xffu << (8 * j)) : 0u;
-                any = any || ok;
+                const uint32_t nj = ok[j] ? n4[j] - (uint32_t)u0 : 0u;  // node within the tile
+                base[j] = __umul24(nj, cells_c8) + copy8;  // nj < 2^16, cells_c8 < 2^24
+                // (q << 16) + 1 as two 32-bit halves: the count 1 in the low 16 bits, the
+                // fixed-point grad above it (sign-extended into the high word); 0 if not counted
+                const int32_t q = __float2int_rn(g4[j] * scale);
+                const uint32_t lo = ((uint32_t)q << kCountBits) | 1u;
+                const uint32_t hi = (uint32_t)(q >> (32 - kCountBits));
+                qv[j] = ((unsigned long long)(ok[j] ? hi : 0u) << 32) | (ok[j] ? lo : 0u);
+                if (!NIB) keep |= ok[j] ? (0xffu << (8 * j)) : 0u;
             }
+            const bool any = ok[0] || ok[1] || ok[2] || ok[3];  // some row of the quad is counted
             // this quad's byte-per-row bin dwords. uint8 columns: bytes of uncounted rows are
             // masked to bin 0 (the caller's padding rows may hold anything). Nibble columns: every
             // row holds a valid bin (rows past N are zero, pb_pack_bins4), and uncounted rows add
@@ -226,21 +240,18 @@ void hist_era_kernel(HistArgs a) {
                 for (int gi = 0; gi < G; ++gi) {
                     const int kk = gi * P;
                     char* hk = lds_bytes + (uint32_t)(gi * words_group) * 8u;
+                    // Joint index per byte, below 256 so no byte carries into the next row's:
+                    // (b1 * nb + b2) * nb + b3 <= nb^3 - 1 <= 215 for nb <= 6, b1 * nb + b2 <= 255
+                    // for nb <= 16. A group's partners past the tile's last feature read that
+                    // feature's column (valid bins); the flush sums the partners out of the
+                    // marginals of the real features.
                     uint32_t wk;
-                    if (P == 3) {
-                        // (b1 * nb + b2) * nb + b3 <= nb^3 - 1 <= 215 for nb <= 6: every partial
-                        // result stays below 256, so no byte carries into the next row's byte
-                        const uint32_t w2 = (kk + 1 < nf) ? wq(kk + 1) : 0u;
-                        const uint32_t w3 = (kk + 2 < nf) ? wq(kk + 2) : 0u;
-                        wk = mad_bytes(mad_bytes(wq(kk), (uint32_t)nb, w2), (uint32_t)nb, w3);
-                    } else if (P == 2) {
-                        // joint index per byte: b1 * nb + b2 <= 255 (no carry between bytes);
-                        // a lone last feature pairs with bin 0
-                        const uint32_t w2 = (kk + 1 < nf) ? wq(kk + 1) : 0u;
-                        wk = mad_bytes(wq(kk), (uint32_t)nb, w2);
-                    } else {
+                    if (P == 3)
+                        wk = mad_bytes(mad_bytes(wq(kk), (uint32_t)nb, wq(kk + 1)), (uint32_t)nb, wq(kk + 2));
+                    else if (P == 2)
+                        wk = mad_bytes(wq(kk), (uint32_t)nb, wq(kk + 1));
+                    else
                         wk = wq(kk);
-                    }
     #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const uint32_t boff = ((wk >> (8 * j)) & 0xffu) << bin_shift;

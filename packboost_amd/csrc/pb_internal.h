@@ -73,14 +73,12 @@ struct HistArgs {
     int32_t* out_tot_cnt;
     float* out_g;
     float* out_tot_g;
-    // Work segments: rows [seg_off[s], seg_off[s+1]) of era seg_era[s], at most 65535 rows. An
-    // era of several segments (acc_slot[era] >= 0) is summed exactly over its segments in
-    // acc_cnt / acc_g ([slot][U][K][nb], raw per-bin counts and fixed-point grads) and
-    // turned into planes by finalize_kernel; other eras write their planes directly.
-    const int32_t* seg_off;
-    const int32_t* seg_era;
+    // Work segments: seg_info[s] = (first row, end row, era, slot), at most 65535 rows. An era
+    // of several segments (slot >= 0) is summed exactly over its segments in acc_cnt / acc_g
+    // ([slot][U][K][nb], raw per-bin counts and fixed-point grads) and turned into planes by
+    // finalize_kernel; other eras (slot -1) write their planes directly.
+    const int4* seg_info;
     int32_t S;
-    const int32_t* acc_slot;
     uint32_t* acc_cnt;
     unsigned long long* acc_g;
 };
