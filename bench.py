@@ -275,7 +275,8 @@ def main() -> int:
         return copy_probe(args.copy_probe)
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the path would shard).", file=sys.stderr)
+              "(the path would shard by feature, one slice of the bin columns per GPU).",
+              file=sys.stderr)
         return 2
 
     import torch
