@@ -59,11 +59,11 @@ struct DivU16 {
 };
 
 // v moved across lanes by the DPP control CTRL (both 32-bit halves); lanes with no source in
-// range read 0 (bound_ctrl).
-template <int CTRL>
+// range, and the rows outside ROW_MASK, read 0 (bound_ctrl, old value 0).
+template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xf, 0xf, true);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, true);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf, true);
     return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
@@ -309,15 +309,46 @@ void hist_era_kernel(HistArgs a) {
             return Digits{(int)u, (int)(q - u * (uint32_t)nf), (int)((uint32_t)it - q * (uint32_t)nb)};
         };
         if (P == 1 && slot < 0) {
-            // single features own their cells: prefix them in place, one thread per (node, feature)
-            for (int p = threadIdx.x; p < nf * Un; p += BS) {
-                const int u = (int)div_nf.div((uint32_t)p);
-                const int kk = p - u * nf;
-                unsigned long long* hc = lds + ((int64_t)kk * words_group + (int64_t)u * cells_node * C);
-                unsigned long long run = 0ull;
-                for (int bb = 0; bb < nb; ++bb) {
-                    run += hc[bb * C];
-                    hc[bb * C] = run;
+            // single features own their cells: prefix each (node, feature) row of nb cells in
+            // place (the count and the fixed-point grad share one integer word, so one integer
+            // scan does both)
+            if (nb >= 32) {
+                // many bins: one wavefront per row, 64 cells per step (a DPP scan inside each
+                // 16-lane row, then the row totals broadcast across), the running total carried
+                // from step to step; a thread walking a row alone would chain nb dependent LDS
+                // round trips
+                const int lane = (int)(threadIdx.x & (kWave - 1));
+                for (int p = (int)(threadIdx.x / kWave); p < nf * Un; p += BS / kWave) {
+                    const int u = (int)div_nf.div((uint32_t)p);
+                    const int kk = p - u * nf;
+                    unsigned long long* hc = lds + ((int64_t)kk * words_group + (int64_t)u * cells_node * C);
+                    unsigned long long carry = 0ull;
+                    for (int b0 = 0; b0 < nb; b0 += kWave) {
+                        const int b = b0 + lane;
+                        unsigned long long v = b < nb ? hc[b * C] : 0ull;
+                        v += dpp_u64<0x111>(v);        // row_shr:1
+                        v += dpp_u64<0x112>(v);        // row_shr:2
+                        v += dpp_u64<0x114>(v);        // row_shr:4
+                        v += dpp_u64<0x118>(v);        // row_shr:8: inclusive scan per 16-lane row
+                        v += dpp_u64<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+                        v += dpp_u64<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+                        v += carry;
+                        if (b < nb) hc[b * C] = v;
+                        carry = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), kWave - 1) << 32) |
+                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, kWave - 1);
+                    }
+                }
+            } else {
+                // few bins: one thread per (node, feature) row
+                for (int p = threadIdx.x; p < nf * Un; p += BS) {
+                    const int u = (int)div_nf.div((uint32_t)p);
+                    const int kk = p - u * nf;
+                    unsigned long long* hc = lds + ((int64_t)kk * words_group + (int64_t)u * cells_node * C);
+                    unsigned long long run = 0ull;
+                    for (int bb = 0; bb < nb; ++bb) {
+                        run += hc[bb * C];
+                        hc[bb * C] = run;
+                    }
                 }
             }
             __syncthreads();
