@@ -165,7 +165,8 @@ int pb_des_score(pb_ctx* ctx, const int32_t* hist_cnt_dev, const float* hist_gra
  * -G/(H+lambda); no split -> leaf value -G/(H+lambda)), assigns the next frontier
  * (children with >= 2*msl rows, booster.py:516, 794-796) and writes the depth's
  * decisions to decisions_dev + (2^depth - 1) (pb_decision [2^D - 1] per round).
- * values_dev: float32 [2^(D+1)] leaf value per TreeBuilder node id. */
+ * values_dev: float32 [2^(D+1)] leaf value per TreeBuilder node id. max_nodes: the node bound
+ * passed to pb_des_score (at least pb_max_nodes(ctx, depth)). */
 int pb_decide(pb_ctx* ctx, int32_t depth, int32_t max_nodes, const pb_split_params* params,
               pb_decision* decisions_dev, float* values_dev, void* stream);
 

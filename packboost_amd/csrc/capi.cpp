@@ -537,8 +537,9 @@ int pb_decide(pb_ctx* c, int32_t depth, int32_t max_nodes, const pb_split_params
     if (!c || !p || !dec || !values) return fail(PB_ERR_INVALID, "pb_decide: null argument");
     if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_decide: depth out of range");
     if (c->last_w <= 0) return fail(PB_ERR_INVALID, "pb_decide: call pb_des_score first");
-    (void)max_nodes;
-    PB_HIP(pb::launch_decide(c->cand_w, c->last_w, c->ntot, c->st, depth, p->min_samples_leaf,
+    if (max_nodes < max_nodes_at(c, depth))
+        return fail(PB_ERR_INVALID, "pb_decide: max_nodes below the frontier bound of this depth");
+    PB_HIP(pb::launch_decide(c->cand_w, c->last_w, max_nodes, c->ntot, c->st, depth, p->min_samples_leaf,
                              p->lambda_l2, c->ids[depth & 1], c->ids[(depth + 1) & 1], c->rules,
                              dec, values, c->node_best, (hipStream_t)stream),
            "decide launch");

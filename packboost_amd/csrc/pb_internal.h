@@ -165,7 +165,7 @@ hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_
                         int32_t nb,
                         int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                         int32_t* thr_tab, hipStream_t s);
-hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal* ntot,
+hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, int32_t max_nodes, const NodeTotal* ntot,
                          Frontier* st, int32_t depth, int32_t msl, double lambda_l2,
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,

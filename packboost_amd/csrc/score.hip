@@ -712,6 +712,38 @@ __device__ int block_exclusive_scan(int v, int* out_excl, int* s_wave) {
 //  3. exclusive scans over the frontier order give the children's TreeBuilder ids
 //     (tree_size + 2 * splits before) and their slots in the next frontier (children with
 //     >= 2 * min_samples_leaf rows, left before right).
+// Phase 1 of the decision step when the candidate set is wide (many wavefront winners per node,
+// e.g. 254 thresholds x 500 features): one workgroup per node slot reduces that node's W winners
+// under the same strict order (`better`) as decide_kernel's own phase 1, so the winner is the
+// same whatever the reduction order.
+__global__ __launch_bounds__(kBlock) void node_best_kernel(const pb_candidate* cand_w, int32_t W,
+                                                        const Frontier* st, int32_t depth,
+                                                        pb_candidate* node_best) {
+    __shared__ Cand s_best[kBlock / kWave];
+    const int u = blockIdx.x;
+    if (u >= st->u_active[depth]) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    Cand best;
+    best.valid = 0; best.score = 0.0f; best.lt = 0; best.lg = 0.0f; best.f = -1; best.thr = -1;
+    for (int w = threadIdx.x; w < W; w += kBlock) {
+        const Cand c = load_cand(cand_w + (int64_t)u * W + w);
+        take_if(better(c, best), c, best);
+    }
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        const Cand o = shfl_xor_cand(best, m);
+        take_if(better(o, best), o, best);
+    }
+    if (lane == 0) s_best[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < kBlock / kWave; ++i) take_if(better(s_best[i], best), s_best[i], best);
+        store_cand(node_best + u, best);
+    }
+}
+
+// W == 0: node_best already holds each node's winner (node_best_kernel ran first).
 __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand_w, int32_t W,
                                                     const NodeTotal* ntot, Frontier* st,
                                                     int32_t depth, int32_t msl, double lambda_l2,
@@ -726,7 +758,7 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
     const int wave = threadIdx.x / kWave;
     pb_decision* dd = dec + ((1 << depth) - 1);
 
-    for (int u = wave; u < Ua; u += kBlock / kWave) {
+    for (int u = wave; W > 0 && u < Ua; u += kBlock / kWave) {
         Cand best;
         best.valid = 0; best.score = 0.0f; best.lt = 0; best.lg = 0.0f; best.f = -1; best.thr = -1;
         for (int w = lane; w < W; w += kWave) {
@@ -892,12 +924,20 @@ hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_
     return hipGetLastError();
 }
 
-hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, const NodeTotal* ntot,
+hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, int32_t max_nodes, const NodeTotal* ntot,
                          Frontier* st, int32_t depth, int32_t msl, double lambda_l2,
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
                          hipStream_t s) {
-    hipLaunchKernelGGL(decide_kernel, dim3(1), dim3(kBlock), 0, s, cand_w, W, ntot, st, depth,
+    // wide candidate sets: the per-node reductions in parallel, one workgroup per node slot
+    // (one workgroup walking max_nodes x W winners took ~0.1 ms per depth at 128 x 2000)
+    int32_t w_decide = W;
+    if ((int64_t)max_nodes * W >= (int64_t)32 * 1024) {
+        hipLaunchKernelGGL(node_best_kernel, dim3(max_nodes), dim3(kBlock), 0, s, cand_w, W, st, depth,
+                           node_best);
+        w_decide = 0;
+    }
+    hipLaunchKernelGGL(decide_kernel, dim3(1), dim3(kBlock), 0, s, cand_w, w_decide, ntot, st, depth,
                        msl, lambda_l2, cur_ids, next_ids, rules, dec, values, node_best);
     return hipGetLastError();
 }

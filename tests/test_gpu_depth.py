@@ -30,6 +30,9 @@ CASES = [
     # 100 nodes x 255 bins: one feature's histogram exceeds the LDS -> node tiles
     (7, 30000, 12, 6, 255, 100, 6, 5, 1e-6, 0.5, 0.0, 0.0),
     (8, 12000, 9, 4, 200, 70, 9, 3, 1.0, 0.2, 0.1, 1.0),
+    # 210 nodes x 40 features x 254 thresholds: max_nodes x wavefront winners >= 32768, so the
+    # per-node winners are reduced by one workgroup per node before the decision step
+    (9, 40000, 48, 4, 255, 210, 40, 2, 1e-6, 0.5, 0.0, 0.0),
 ]
 
 
