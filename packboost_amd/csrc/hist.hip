@@ -39,6 +39,7 @@
 //  * blockIdx -> (era, tile) is XCD-aware: the 8 XCDs receive blocks round-robin, so all
 //    feature tiles of one era run on the same XCD and share the era's row state in its L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "pb_internal.h"
 
@@ -364,18 +365,41 @@ void hist_era_kernel(HistArgs a) {
             const int bb = d.bb;
             const int b_lo = prefix ? 0 : bb;
             unsigned long long tot = 0ull;
+            // Sums over one partner's nb bins are read as one batch of W loads (clamped to the
+            // last bin, the extra values dropped), so their LDS round trips overlap: the LDS is
+            // busy with the other workgroups' atomics, and a dependent read per cell made the
+            // flush a chain of nb^(P-1) round trips.
+            auto run = [&](const unsigned long long* base, int step, auto width) -> unsigned long long {
+                constexpr int W = decltype(width)::value;
+                unsigned long long v[W];
+    #pragma unroll
+                for (int o = 0; o < W; ++o) v[o] = base[min(o, nb - 1) * step];
+                unsigned long long r = 0ull;
+    #pragma unroll
+                for (int o = 0; o < W; ++o) r += (o < nb) ? v[o] : 0ull;
+                return r;
+            };
             if (P == 3) {
                 const int nb2 = nb * nb;
                 const int stride = side == 0 ? nb2 : (side == 1 ? nb : 1);
                 const int s1 = side == 0 ? nb : nb2;   // stride of the first other feature
                 const int s2 = side == 2 ? nb : 1;     // stride of the second other feature
                 for (int b = b_lo; b <= bb; ++b)
-                    for (int o1 = 0; o1 < nb; ++o1)
-                        for (int o2 = 0; o2 < nb; ++o2) tot += hc[(b * stride + o1 * s1 + o2 * s2) * C];
+                    for (int o1 = 0; o1 < nb; ++o1) {
+                        const unsigned long long* base = hc + (b * stride + o1 * s1) * C;
+                        tot += (nb <= 4) ? run(base, s2 * C, std::integral_constant<int, 4>{})
+                                         : (nb == 5) ? run(base, s2 * C, std::integral_constant<int, 5>{})
+                                                     : run(base, s2 * C, std::integral_constant<int, 6>{});
+                    }
             } else if (P == 2) {
-                for (int b = b_lo; b <= bb; ++b)
-                    for (int o = 0; o < nb; ++o)
-                        tot += hc[(side == 0 ? (b * nb + o) : (o * nb + b)) * C];
+                const int step = (side == 0 ? 1 : nb) * C;  // the partner's bins
+                for (int b = b_lo; b <= bb; ++b) {
+                    const unsigned long long* base = hc + (side == 0 ? b * nb : b) * C;
+                    tot += (nb <= 4)   ? run(base, step, std::integral_constant<int, 4>{})
+                           : (nb == 5) ? run(base, step, std::integral_constant<int, 5>{})
+                           : (nb <= 8) ? run(base, step, std::integral_constant<int, 8>{})
+                                       : run(base, step, std::integral_constant<int, 16>{});
+                }
             } else {
                 tot = hc[bb * C];
             }
@@ -418,7 +442,7 @@ void hist_era_kernel(HistArgs a) {
                 a.out_tot_g[o] = gs;
             }
         };
-        constexpr int kMaxItems = 16;  // marginals a thread holds in registers
+        constexpr int kMaxItems = 8;  // marginals a thread holds in registers
         if (P == 1) {
             for (int it = threadIdx.x; it < items; it += BS) {
                 const Digits d = split(it);
