@@ -279,15 +279,27 @@ void hist_era_kernel(HistArgs a) {
         if (C > 1) {
             const int total_words = cells_total * C;
             const int lane = (int)(threadIdx.x & (kWave - 1));
-            for (int wb = (int)(threadIdx.x / kWave) * kWave; wb < total_words; wb += BS) {
-                const int wi = wb + lane;
-                unsigned long long v = wi < total_words ? lds[wi] : 0ull;
-                v += dpp_u64<0x111>(v);                 // row_shr:1
-                if (C > 2) v += dpp_u64<0x112>(v);      // row_shr:2
-                if (C > 4) v += dpp_u64<0x114>(v);      // row_shr:4
-                if (C > 8) v += dpp_u64<0x118>(v);      // row_shr:8
-                if (C > 16) v += dpp_u64<0x142>(v);     // row_bcast:15 (row r's lane 15 -> row r+1)
-                if ((lane & (C - 1)) == C - 1 && wi < total_words) lds[wi - (C - 1)] = v;
+            // four 64-word windows per wave at a time, their reads issued together (each window
+            // is written only inside itself, so the reads of the next windows cannot see a write)
+            constexpr int kFoldBatch = 4;
+            for (int wb0 = (int)(threadIdx.x / kWave) * kWave; wb0 < total_words; wb0 += kFoldBatch * BS) {
+                unsigned long long vb[kFoldBatch];
+    #pragma unroll
+                for (int k = 0; k < kFoldBatch; ++k) {
+                    const int wi = wb0 + k * BS + lane;
+                    vb[k] = lds[min(wi, total_words - 1)];
+                }
+    #pragma unroll
+                for (int k = 0; k < kFoldBatch; ++k) {
+                    const int wi = wb0 + k * BS + lane;
+                    unsigned long long v = wi < total_words ? vb[k] : 0ull;
+                    v += dpp_u64<0x111>(v);                 // row_shr:1
+                    if (C > 2) v += dpp_u64<0x112>(v);      // row_shr:2
+                    if (C > 4) v += dpp_u64<0x114>(v);      // row_shr:4
+                    if (C > 8) v += dpp_u64<0x118>(v);      // row_shr:8
+                    if (C > 16) v += dpp_u64<0x142>(v);     // row_bcast:15 (row r's lane 15 -> row r+1)
+                    if ((lane & (C - 1)) == C - 1 && wi < total_words) lds[wi - (C - 1)] = v;
+                }
             }
             __syncthreads();
         }
@@ -464,10 +476,24 @@ void hist_era_kernel(HistArgs a) {
                 if (it < items) lds[it] = m[i];
             }
             __syncthreads();
+            // prefix over bins 0..bb of the compacted marginals, its loads as one batch
+            auto prefix = [&](int it, int bb, auto width) -> unsigned long long {
+                constexpr int W = decltype(width)::value;
+                unsigned long long v[W];
+    #pragma unroll
+                for (int o = 0; o < W; ++o) v[o] = lds[it - bb + min(o, bb)];
+                unsigned long long r = 0ull;
+    #pragma unroll
+                for (int o = 0; o < W; ++o) r += (o <= bb) ? v[o] : 0ull;
+                return r;
+            };
             for (int it = threadIdx.x; it < items; it += BS) {
                 const Digits d = split(it);
-                unsigned long long tot = 0ull;
-                for (int b = it - d.bb; b <= it; ++b) tot += lds[b];
+                const unsigned long long tot =
+                    (nb <= 4)   ? prefix(it, d.bb, std::integral_constant<int, 4>{})
+                    : (nb == 5) ? prefix(it, d.bb, std::integral_constant<int, 5>{})
+                    : (nb <= 8) ? prefix(it, d.bb, std::integral_constant<int, 8>{})
+                                : prefix(it, d.bb, std::integral_constant<int, 16>{});
                 emit(d, tot);
             }
         } else {
