@@ -89,7 +89,9 @@ constexpr int hist_waves_per_eu() {
 
 template <int FT, int P, bool NIB, int BS>
 __global__ __launch_bounds__(BS) __attribute__((amdgpu_waves_per_eu(hist_waves_per_eu<FT, P>())))
-void hist_era_kernel(HistArgs a) {
+void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_t* __restrict__ feats) {
+    // seg_info / feats are separate restrict arguments (the same pointers as in `a`): nothing the
+    // kernel writes can alias them, so their workgroup-uniform loads go through the scalar cache
     static_assert(FT % P == 0, "feature tile must hold whole groups");
     constexpr int RL = NIB ? 8 : 4;  // rows per lane per pass (rows per bin dword)
     constexpr int G = FT / P;  // atomic groups (single features or feature pairs) per tile
@@ -123,7 +125,7 @@ void hist_era_kernel(HistArgs a) {
         const int k0 = tile * FT;
         const int nf = min(FT, a.K - k0);
         if (seg >= a.S || nf <= 0 || Un <= 0) continue;  // uniform over the workgroup
-        const int4 si = a.seg_info[seg];  // one load: rows, era and slot of the segment
+        const int4 si = seg_info[seg];  // one load: rows, era and slot of the segment
         const int era = si.z;
         const int slot = si.w;  // >= 0: add into the era's sums
 
@@ -140,7 +142,7 @@ void hist_era_kernel(HistArgs a) {
     #pragma unroll
         for (int kk = 0; kk < FT; ++kk) {
             const int kq = k0 + (kk < nf ? kk : nf - 1);
-            col[kk] = a.bins + (int64_t)a.feats[kq] * a.ld;
+            col[kk] = a.bins + (int64_t)feats[kq] * a.ld;
         }
         __syncthreads();
 
@@ -521,7 +523,8 @@ hipError_t launch_bs(const HistArgs& a, int grid, size_t lds_bytes, hipStream_t 
         const int64_t want = (int64_t)std::max(1, per_cu) * a.resident_cus * std::max(1, a.rounds);
         grid = (int)std::max<int64_t>(8, std::min<int64_t>(grid, want) / 8 * 8);
     }
-    hipLaunchKernelGGL((hist_era_kernel<FT, P, NIB, BS>), dim3(grid), dim3(BS), lds_bytes, s, a);
+    hipLaunchKernelGGL((hist_era_kernel<FT, P, NIB, BS>), dim3(grid), dim3(BS), lds_bytes, s, a, a.seg_info,
+                       a.feats);
     return hipGetLastError();
 }
 
