@@ -234,32 +234,58 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
         if (ch + 1 < nchunks) prefetch(ch + 1);  // loads in flight across phase B
         __syncthreads();
         if (owner) {
-            for (int el = 0; el < ne; ++el) {
-                const int L = sL[el * cstride + tid];
-                const float GLv = sGL[el * cstride + tid];
-                const float wd = sWD[el * cstride + tid];
-                const float gain = sG[el * cstride + tid];
-                const int ct = sCt[el];
-                const float gt = sGt[el];
-                const bool has = L >= 0;
-                lt += has ? L : 0;
-                lg = has ? lg + GLv : lg;
-                tc += ct;
-                tg = (ct != 0) ? tg + gt : tg;
-                const float w = fabsf(wd);
-                const bool act = w > 0.0f;  // implies has; wsum + w > 0 then holds
-                const float wn = wsum + w;
-                const int wi = (int)wn;
-                const float fac = (unit_w && wi < RT) ? recip[act ? wi : 0] : w / (act ? wn : 1.0f);
-                const float delta = gain - mean;
-                const float mean_n = mean + fac * delta;
-                const float M2_n = M2 + (w * delta) * (gain - mean_n);
-                mean = act ? mean_n : mean;
-                M2 = act ? M2_n : M2;
-                wsum = act ? wn : wsum;
-                if (use_dir) {
-                    agn = act ? agn + w * ((wd > 0.0f) ? 1.0f : -1.0f) : agn;
-                    agd = act ? agd + w : agd;
+            // eras in batches of kRecBatch: the batch's records first (their LDS reads in flight
+            // together), then the weight-sum chain with its table lookups, then the era-ordered
+            // sums and the mean/M2 chain; every float operation and its order per candidate are
+            // those of the one-era-at-a-time recurrence
+            constexpr int kRecBatch = 4;
+            for (int b0 = 0; b0 < ne; b0 += kRecBatch) {
+                int Lb[kRecBatch], ctb[kRecBatch];
+                float GLb[kRecBatch], wdb[kRecBatch], gb[kRecBatch], gtb[kRecBatch];
+#pragma unroll
+                for (int j = 0; j < kRecBatch; ++j) {
+                    const int el = min(b0 + j, ne - 1);  // past the chunk: read but not used
+                    Lb[j] = sL[el * cstride + tid];
+                    GLb[j] = sGL[el * cstride + tid];
+                    wdb[j] = sWD[el * cstride + tid];
+                    gb[j] = sG[el * cstride + tid];
+                    ctb[j] = sCt[el];
+                    gtb[j] = sGt[el];
+                }
+                float facb[kRecBatch], wb[kRecBatch];
+                bool actb[kRecBatch];
+#pragma unroll
+                for (int j = 0; j < kRecBatch; ++j) {
+                    const float w = (b0 + j < ne) ? fabsf(wdb[j]) : 0.0f;
+                    const bool act = w > 0.0f;  // implies has; wsum + w > 0 then holds
+                    const float wn = wsum + w;
+                    const int wi = (int)wn;
+                    facb[j] = (unit_w && wi < RT) ? recip[act ? wi : 0] : w / (act ? wn : 1.0f);
+                    wsum = act ? wn : wsum;
+                    wb[j] = w;
+                    actb[j] = act;
+                }
+#pragma unroll
+                for (int j = 0; j < kRecBatch; ++j) {
+                    if (b0 + j >= ne) break;  // uniform
+                    const int L = Lb[j];
+                    const bool has = L >= 0;
+                    lt += has ? L : 0;
+                    lg = has ? lg + GLb[j] : lg;
+                    tc += ctb[j];
+                    tg = (ctb[j] != 0) ? tg + gtb[j] : tg;
+                    const float w = wb[j];
+                    const bool act = actb[j];
+                    const float gain = gb[j];
+                    const float delta = gain - mean;
+                    const float mean_n = mean + facb[j] * delta;
+                    const float M2_n = M2 + (w * delta) * (gain - mean_n);
+                    mean = act ? mean_n : mean;
+                    M2 = act ? M2_n : M2;
+                    if (use_dir) {
+                        agn = act ? agn + w * ((wdb[j] > 0.0f) ? 1.0f : -1.0f) : agn;
+                        agd = act ? agd + w : agd;
+                    }
                 }
             }
         }
