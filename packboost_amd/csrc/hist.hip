@@ -337,21 +337,36 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                     const int u = (int)div_nf.div((uint32_t)p);
                     const int kk = p - u * nf;
                     unsigned long long* hc = lds + ((int64_t)kk * words_group + (int64_t)u * cells_node * C);
-                    unsigned long long carry = 0ull;
-                    for (int b0 = 0; b0 < nb; b0 += kWave) {
-                        const int b = b0 + lane;
-                        unsigned long long v = b < nb ? hc[b * C] : 0ull;
-                        v += dpp_u64<0x111>(v);        // row_shr:1
-                        v += dpp_u64<0x112>(v);        // row_shr:2
-                        v += dpp_u64<0x114>(v);        // row_shr:4
-                        v += dpp_u64<0x118>(v);        // row_shr:8: inclusive scan per 16-lane row
-                        v += dpp_u64<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
-                        v += dpp_u64<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
-                        v += carry;
-                        if (b < nb) hc[b * C] = v;
-                        carry = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), kWave - 1) << 32) |
-                                (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, kWave - 1);
-                    }
+                    // the row's 64-cell steps (NS of them, nb <= 64 * NS) read together; each step
+                    // writes only its own cells
+                    auto scan_row = [&](auto nsteps) {
+                        constexpr int NS = decltype(nsteps)::value;
+                        unsigned long long seg[NS];
+    #pragma unroll
+                        for (int q = 0; q < NS; ++q) seg[q] = hc[min(q * kWave + lane, nb - 1) * C];
+                        unsigned long long carry = 0ull;
+    #pragma unroll
+                        for (int q = 0; q < NS; ++q) {
+                            const int b = q * kWave + lane;
+                            unsigned long long v = b < nb ? seg[q] : 0ull;
+                            v += dpp_u64<0x111>(v);        // row_shr:1
+                            v += dpp_u64<0x112>(v);        // row_shr:2
+                            v += dpp_u64<0x114>(v);        // row_shr:4
+                            v += dpp_u64<0x118>(v);        // row_shr:8: inclusive scan per 16-lane row
+                            v += dpp_u64<0x142, 0xa>(v);   // row_bcast:15 into rows 1 and 3
+                            v += dpp_u64<0x143, 0xc>(v);   // row_bcast:31 into rows 2 and 3
+                            v += carry;
+                            if (b < nb) hc[b * C] = v;
+                            carry = ((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), kWave - 1) << 32) |
+                                    (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, kWave - 1);
+                        }
+                    };
+                    if (nb <= kWave)
+                        scan_row(std::integral_constant<int, 1>{});
+                    else if (nb <= 2 * kWave)
+                        scan_row(std::integral_constant<int, 2>{});
+                    else
+                        scan_row(std::integral_constant<int, 4>{});
                 }
             } else {
                 // few bins: one thread per (node, feature) row
@@ -458,9 +473,19 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         };
         constexpr int kMaxItems = 8;  // marginals a thread holds in registers
         if (P == 1) {
-            for (int it = threadIdx.x; it < items; it += BS) {
-                const Digits d = split(it);
-                emit(d, marginal(d, false));
+            // kEmitBatch elements per thread at a time: their LDS reads first, then the stores
+            constexpr int kEmitBatch = 4;
+            for (int it0 = threadIdx.x; it0 < items; it0 += kEmitBatch * BS) {
+                Digits dd[kEmitBatch];
+                unsigned long long v[kEmitBatch];
+    #pragma unroll
+                for (int q = 0; q < kEmitBatch; ++q) {
+                    dd[q] = split(min(it0 + q * BS, items - 1));
+                    v[q] = marginal(dd[q], false);
+                }
+    #pragma unroll
+                for (int q = 0; q < kEmitBatch; ++q)
+                    if (it0 + q * BS < items) emit(dd[q], v[q]);
             }
         } else if (items <= kMaxItems * BS) {
             // marginals into registers, then compact them over the (no longer needed) joint cells
