@@ -383,8 +383,6 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     a.block = (c->hist_block == 128 || c->hist_block == 256) ? c->hist_block : 256;
     a.grad = grad;
     a.nid = nid;
-    a.era_off = c->era_off_dev;
-    a.E = c->d.num_eras;
     a.feats = feats;
     a.K = K;
     a.ntiles = (K + ftile - 1) / ftile;
@@ -505,7 +503,6 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
         a.g = hist_grad;
         a.tot_g = hist_grad + to;
     }
-    a.E = c->d.num_eras;
     a.U = max_nodes;
     a.K = K;
     a.nb = nb;

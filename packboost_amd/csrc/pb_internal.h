@@ -55,8 +55,6 @@ struct HistArgs {
     int32_t block;         // threads per workgroup: 128 or 256
     const float* grad;
     const uint16_t* nid;
-    const int32_t* era_off;
-    int32_t E;
     const int32_t* feats;
     int32_t K;
     int32_t ntiles;
