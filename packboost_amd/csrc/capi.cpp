@@ -371,7 +371,7 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
         return fail(PB_ERR_UNSUPPORTED,
                     "pb_hist_build: one feature's node x bin histogram exceeds the 160 KiB LDS");
 
-    pb::HistArgs a;
+    pb::HistArgs a{};
     a.resident_cus = c->hist_resident ? c->num_cus : 0;
     a.rounds = c->hist_rounds;
     a.bins = bins;
@@ -494,7 +494,7 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     // the scorer addresses one chunk of eras' plane cells with 31-bit offsets
     if ((int64_t)(pb::kScoreChunkEras + 1) * max_nodes * K * std::max(1, nb - 1) >= (int64_t(1) << 31))
         return fail(PB_ERR_UNSUPPORTED, "pb_des_score: max_nodes x K x bins too large for one era chunk");
-    pb::ScoreArgs a;
+    pb::ScoreArgs a{};
     {
         const int64_t to = pb::plane_tot_off(c->d.num_eras, max_nodes, K, nb);
         a.cnt = reinterpret_cast<const uint16_t*>(hist_cnt);
@@ -503,6 +503,7 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
         a.g = hist_grad;
         a.tot_g = hist_grad + to;
     }
+    a.E = c->d.num_eras;
     a.U = max_nodes;
     a.K = K;
     a.nb = nb;
