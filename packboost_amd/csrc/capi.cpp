@@ -46,6 +46,7 @@ struct pb_ctx {
     int32_t force_pairs;
     int32_t hist_block;  // 0: by LDS size, else 128 or 256 threads
     int32_t score_wgs;  // workgroups the producer/consumer scorer aims for
+    int32_t score_staged;  // T >= 64 thresholds: LDS-staged scorer instead of the wide one
     int32_t num_cus;        // compute units of the device
     int32_t hist_resident;  // histogram: loop work items over a resident grid
     int32_t hist_rounds;
@@ -181,6 +182,7 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     for (int dd = 0; dd < d.max_depth; ++dd) c->umax = std::max(c->umax, max_nodes_at(c, dd));
     const int tmax = std::max(1, d.max_bins - 1);
     c->score_wgs = (int32_t)env_int("PB_SCORE_WGS", 768);
+    c->score_staged = env_int("PB_SCORE_STAGED", 0) != 0 ? 1 : 0;
     c->hist_resident = (int32_t)env_int("PB_HIST_RESIDENT", 0);
     c->hist_rounds = (int32_t)env_int("PB_HIST_ROUNDS", 1);
     c->num_cus = 0;
@@ -525,6 +527,7 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     a.ec = sh.ec;
     a.wpt = sh.wpt;
     a.rt = sh.rt;
+    a.staged = c->score_staged;
     c->last_w = sh.ntiles * sh.wpt;
     PB_HIP(pb::launch_score(a, (int)grid, sh.lds_bytes, (hipStream_t)stream), "score launch");
     return PB_OK;

@@ -145,6 +145,7 @@ struct ScoreArgs {
     int32_t ec;              // eras staged in LDS per chunk
     int32_t wpt;             // wavefront winners per tile (ceil(fts * T / 64))
     int32_t rt;              // size of the 1/n table (equal era weights)
+    int32_t staged;          // T >= 64: 1 = LDS-staged two-phase kernel, 0 = wide kernel
 };
 
 // Launch shape of the scorer for K features and T thresholds (shared by the context's

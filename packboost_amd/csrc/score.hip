@@ -333,6 +333,167 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     }
 }
 
+// Wide scorer for T >= 64 thresholds per feature (the default for that case). One workgroup
+// owns one (node, feature); thread t owns threshold t and walks the eras itself: the era's
+// record (gain, weight, direction) and the Welford step are computed by the same thread, in
+// the same float operations and order as des_score_kernel's two phases. The plane values of
+// kWidePf eras are loaded per batch into registers, two batches in flight (one being
+// consumed while the next one loads), so a workgroup waits on memory once per kWidePf eras
+// and needs no LDS staging or barriers (LDS holds only the 1/n table).
+constexpr int kWidePf = 8;
+
+// one batch of kWidePf eras: this thread's plane values, and the (era, node) totals with
+// lane j of every wavefront holding era e0 + j (read back with readlane, so the totals of
+// two batches stay in two vector registers instead of 2 * kWidePf scalar ones)
+struct EraBatch {
+    int L[kWidePf];
+    float GL[kWidePf];
+    int ct;
+    float Gt;
+};
+
+template <bool C32>
+__global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
+    extern __shared__ unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int u = blockIdx.x / a.ntiles;
+    const int k = blockIdx.x - u * a.ntiles;  // one feature per workgroup
+    const int Ua = a.st->u_active[a.depth];
+    if (u >= Ua) return;
+    const int T = a.T;
+    const int RT = a.rt;
+    float* recip = reinterpret_cast<float*>(smem);
+    for (int i = tid; i < RT; i += kBlock) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
+    __syncthreads();
+
+    const bool owner = tid < T;
+    const int t = owner ? tid : T - 1;  // idle lanes mirror the last threshold (never owners)
+    const int thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
+    const float lam = a.lambda_l2;
+    const float alpha = a.era_alpha;
+    const bool use_dir = a.dir_w != 0.0f;
+    const bool unit_w = !(alpha > 0.0f);
+    const int pt = a.nb - 1;
+    const int64_t estride = (int64_t)a.U * a.K * pt;
+    const int64_t cell0 = ((int64_t)u * a.K + k) * pt + thr;
+    const int E = a.E;
+
+    auto load = [&](int e0, EraBatch& b) {
+        b.ct = 0;
+        b.Gt = 0.0f;
+        if (lane < kWidePf && e0 + lane < E) {
+            const int64_t to = (int64_t)(e0 + lane) * a.U + u;
+            b.ct = a.tot_cnt[to];
+            b.Gt = a.tot_g[to];
+        }
+#pragma unroll
+        for (int j = 0; j < kWidePf; ++j) {
+            b.L[j] = 0;
+            b.GL[j] = 0.0f;
+            if (e0 + j < E) {
+                const int64_t off = (int64_t)(e0 + j) * estride + cell0;
+                b.L[j] = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
+                b.GL[j] = a.g[off];
+            }
+        }
+    };
+
+    float wsum = 0.0f, mean = 0.0f, M2 = 0.0f, agn = 0.0f, agd = 0.0f, lg = 0.0f, tg = 0.0f;
+    int lt = 0, tc = 0;
+    auto step = [&](const EraBatch& b, int j) {
+        const int ctot = __builtin_amdgcn_readlane(b.ct, j);
+        if (ctot == 0) return;  // the node has no rows in this era (or past E): skipped
+        const float Gt = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.Gt), j));
+        const int L = b.L[j];
+        const float GL = b.GL[j];
+        const int R = ctot - L;
+        const float GR = Gt - GL;
+        const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
+        const float w = (L > 0 && R > 0) ? wera : 0.0f;
+        float gain = 0.0f;
+        bool pos = true;
+        if (w > 0.0f) {
+            const float dL = (float)L + lam;
+            const float dR = (float)R + lam;
+            const float pden = (float)ctot + lam;
+            const float parent = (pden > 0.0f) ? (0.5f * (Gt * Gt)) / pden : 0.0f;
+            gain = 0.5f * ((GL * GL) / dL + (GR * GR) / dR) - parent;
+            if (use_dir) {
+                const float lv = -GL / dL;
+                const float rv = -GR / dR;
+                pos = lv > rv;
+            }
+        }
+        lt += L;
+        lg = lg + GL;
+        tc += ctot;
+        tg = tg + Gt;
+        const bool act = w > 0.0f;
+        const float wn = wsum + w;
+        const int wi = (int)wn;
+        const float fac = (unit_w && wi < RT) ? recip[act ? wi : 0] : w / (act ? wn : 1.0f);
+        wsum = act ? wn : wsum;
+        const float delta = gain - mean;
+        const float mean_n = mean + fac * delta;
+        const float M2_n = M2 + (w * delta) * (gain - mean_n);
+        mean = act ? mean_n : mean;
+        M2 = act ? M2_n : M2;
+        if (use_dir) {
+            agn = act ? agn + w * (pos ? 1.0f : -1.0f) : agn;
+            agd = act ? agd + w : agd;
+        }
+    };
+
+    EraBatch ba, bb;
+    load(0, ba);
+    for (int e0 = 0; e0 < E; e0 += 2 * kWidePf) {
+        load(e0 + kWidePf, bb);
+#pragma unroll
+        for (int j = 0; j < kWidePf; ++j) step(ba, j);
+        load(e0 + 2 * kWidePf, ba);
+#pragma unroll
+        for (int j = 0; j < kWidePf; ++j) step(bb, j);
+    }
+
+    Cand c;
+    c.lt = lt;
+    c.lg = lg;
+    c.valid = 0;
+    c.score = 0.0f;
+    c.f = -1;
+    c.thr = -1;
+    if (owner) {
+        c.f = a.feats[k];
+        c.thr = thr;
+        const int rt = tc - lt;
+        const float ws = (wsum < 1e-12f) ? 1e-12f : wsum;
+        const float var = M2 / ws;
+        const float sd = sqrtf((0.0f < var) ? var : 0.0f);
+        float score = mean - a.lambda_dro * sd;
+        if (use_dir && agd > 0.0f) score = score + a.dir_w * (agn / agd);
+        c.score = score;
+        c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
+        if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
+        if (k == 0 && tid == 0) {
+            a.ntot[u].count = tc;
+            a.ntot[u].grad = tg;
+        }
+    }
+    const int wave = tid / kWave;
+    if (wave < a.wpt) {
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const Cand o = shfl_xor_cand(c, m);
+            take_if(better(o, c), o, c);
+        }
+        if ((tid & (kWave - 1)) == 0) {
+            const int W = a.ntiles * a.wpt;
+            store_cand(a.cand_w + (int64_t)u * W + k * a.wpt + wave, c);
+        }
+    }
+}
+
 // Producer/consumer scorer for T <= 63 thresholds per feature. A workgroup owns up to 63
 // candidates (63 / T features of one node):
 //   wave 0 (consumer): one lane per candidate runs the Welford recurrence over the eras;
@@ -922,8 +1083,11 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
 
 template <bool C32>
 hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+    const bool wide = a.T >= kWave && !a.staged;
+    if (wide) lds_bytes = (size_t)a.rt * 4;
     const void* fn = (a.T < kWave) ? reinterpret_cast<const void*>(&des_score_pc_kernel<C32>)
-                                    : reinterpret_cast<const void*>(&des_score_kernel<C32>);
+                     : wide        ? reinterpret_cast<const void*>(&des_score_wide_kernel<C32>)
+                                   : reinterpret_cast<const void*>(&des_score_kernel<C32>);
     if (lds_bytes > 64 * 1024) {
         hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
                                            (int)lds_bytes);
@@ -931,6 +1095,8 @@ hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStr
     }
     if (a.T < kWave)
         hipLaunchKernelGGL(des_score_pc_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
+    else if (wide)
+        hipLaunchKernelGGL(des_score_wide_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
     else
         hipLaunchKernelGGL(des_score_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
     return hipGetLastError();

@@ -204,3 +204,36 @@ def test_hist_copies(hip, oracle_mod, monkeypatch, pairs, copies, block):
         assert np.all(err <= 1e-5 * np.maximum(mass, 1.0))
     finally:
         g.close()
+
+
+WIDE_CASES = [c for c in CASES if c[4] - 1 >= 64]
+
+
+@pytest.mark.parametrize("k_cuts", [0, 70])
+@pytest.mark.parametrize("case", WIDE_CASES, ids=[f"case{c[0]}" for c in WIDE_CASES])
+def test_wide_scorer_matches_staged(hip, oracle_mod, monkeypatch, case, k_cuts):
+    """Features with 64+ thresholds: the wide scorer (one thread per threshold, eras batched in
+    registers) and the LDS-staged two-phase scorer give bit-identical candidates (score, left
+    count, left grad, validity) and the same decisions, with the full sweep and with K-cuts."""
+    seed, N, F, E, nb, U, K, msl, lam, dro, dw, alpha = case
+    T = nb - 1 if (k_cuts == 0 or k_cuts >= nb - 1) else k_cuts
+    print(f"[wide scorer] seed={seed} nb={nb} U={U} K={K} k_cuts={k_cuts}", flush=True)
+    p = make_problem(seed, N, F, E, nb, U, empty_era=(seed % 2 == 0))
+    feats = np.random.default_rng(seed + 100).permutation(F)[:K].astype(np.int32)
+    params = split_params(hip, lambda_l2=lam, lambda_dro=dro, direction_weight=dw,
+                          era_alpha=alpha, msl=msl, k_cuts=k_cuts, cut_selection="mass")
+    out = {}
+    for staged in (1, 0):
+        monkeypatch.setenv("PB_SCORE_STAGED", str(staged))
+        g = GpuDepth(hip, p, K, msl=msl, layout="u8")
+        try:
+            g.hist(feats)
+            out[staged] = (g.score(feats, params, T), g.decide(params))
+        finally:
+            g.close()
+    (c1, d1), (c0, d0) = out[1], out[0]
+    for field in ("valid", "left_total", "feature", "threshold"):
+        np.testing.assert_array_equal(c0[field], c1[field])
+    for field in ("score", "left_grad"):
+        np.testing.assert_array_equal(c0[field].view(np.uint32), c1[field].view(np.uint32))
+    assert d0.tobytes() == d1.tobytes()
