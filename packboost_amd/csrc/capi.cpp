@@ -340,11 +340,15 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     const int64_t budget = c->lds_budget > 0 ? c->lds_budget : (max_nodes >= 16 ? 26 * 1024 : 20000);
     int64_t cap = std::max<int64_t>(budget, 4 * 1024);
     // node tiles when one feature's node x bin histogram does not fit: single features, up
-    // to 64 KiB of LDS, as many nodes per tile as fit
+    // to 32 KiB of LDS, as many nodes per tile as fit (swept at 1M rows x 500 features x 255
+    // bins, depths 4-7: 32 KiB beat 12-24 KiB (more tiles re-read the rows) and 48-160 KiB
+    // (fewer resident workgroups), also where two features per item would fit in 64 KiB)
     int node_tile = max_nodes;
     if ((int64_t)max_nodes * cells_node * 8 > cap) {
         P = 1;
-        cap = std::max<int64_t>(cap, 64 * 1024);
+        cap = c->lds_budget > 0 ? std::min<int64_t>(std::max<int64_t>(c->lds_budget, (int64_t)nb * 8),
+                                                   160 * 1024)
+                                : std::max<int64_t>(cap, 32 * 1024);
         node_tile = (int)std::max<int64_t>(1, std::min<int64_t>(max_nodes, cap / ((int64_t)nb * 8)));
     }
     const int node_tiles = (max_nodes + node_tile - 1) / node_tile;
