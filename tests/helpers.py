@@ -73,7 +73,7 @@ class GpuDepth:
     """Runs hist -> score -> decide -> partition for one teacher-forced depth."""
 
     def __init__(self, hip, p: dict, K: int, *, msl: int, depth: int | None = None,
-                 max_depth: int | None = None, layout: str = "u8"):
+                 max_depth: int | None = None, layout: str = "u8", bins_dev=None):
         import torch
 
         self.torch = torch
@@ -92,9 +92,13 @@ class GpuDepth:
                   "pb_ctx_create")
         self.ctx = ctx
         dev = torch.device("cuda")
-        bfm = np.zeros((F, self.ld), dtype=np.uint8)
-        bfm[:, :N] = p["bins"].T
-        self.bins = torch.from_numpy(bfm).to(dev)
+        if bins_dev is not None:  # column-major [F, ld] uint8 already on the device
+            assert tuple(bins_dev.shape) == (F, self.ld)
+            self.bins = bins_dev
+        else:
+            bfm = np.zeros((F, self.ld), dtype=np.uint8)
+            bfm[:, :N] = p["bins"].T
+            self.bins = torch.from_numpy(bfm).to(dev)
         if layout == "nibble":  # the histogram and partition read the packed copy
             packed = torch.empty((F, self.ld // 2), dtype=torch.uint8, device=dev)
             hip.check(self.lib.pb_pack_bins4(self.bins.data_ptr(), N, self.ld, F, packed.data_ptr(),
