@@ -505,7 +505,8 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
 // reference's float order) runs at full wavefront width while its inputs are made alongside.
 constexpr int kPcEras = kScoreChunkEras;  // eras per chunk
 constexpr int kPcProducers = kBlock - kWave;
-constexpr int kPcPairs = (kPcEras * kWave + kPcProducers - 1) / kPcProducers;
+constexpr int kPcThreadsPerEra = kPcProducers / kPcEras;              // 8
+constexpr int kPcPairs = (kWave + kPcThreadsPerEra - 1) / kPcThreadsPerEra;  // 8 pairs per thread
 
 template <bool C32>
 __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
@@ -540,72 +541,83 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
     const bool consumer = tid < kWave;
     const int ptid = tid - kWave;
 
-    // Producer slot i of this thread always maps to the same (era-in-chunk, candidate); the
-    // plane offsets are precomputed once, so a chunk costs only loads and the gain math.
-    // Only the first `np` slots can hold a record (workgroup-uniform): fewer candidates per
-    // workgroup mean fewer pairs per producer lane.
-    const int np = (kPcEras * ncand + kPcProducers - 1) / kPcProducers;
+    // Producer slot i of this thread always maps to the same (era-in-chunk, candidate): the 8
+    // producer threads of era el = ptid / 8 take candidates ptid % 8 + 8 i, so every pair of a
+    // thread belongs to one era, whose totals are loaded and whose parent term is divided once
+    // per thread. The plane offsets are precomputed once, so a chunk costs only loads and the
+    // gain math. Only the first `np` slots can hold a record (workgroup-uniform): fewer
+    // candidates per workgroup mean fewer pairs per producer lane.
+    static_assert(kPcEras * kPcThreadsPerEra == kPcProducers, "one era per 8 producer threads");
+    const int np = (ncand + kPcThreadsPerEra - 1) / kPcThreadsPerEra;
+    const int my_el = ptid / kPcThreadsPerEra;  // the era (in chunk) of all of this thread's pairs
     int slot_el[kPcPairs], slot_c[kPcPairs];
     // plane element of the slot's (era in chunk, candidate) relative to the chunk's first era,
     // threshold included (the host checks that it fits 31 bits)
     int32_t slot_off[kPcPairs];
 #pragma unroll
     for (int i = 0; i < kPcPairs; ++i) {
-        const int pidx = ptid + i * kPcProducers;
-        const int el = pidx / ncand;
-        const int c = pidx - el * ncand;
-        const int kk = c / T;
-        const int t = c - kk * T;
+        const int c = ptid % kPcThreadsPerEra + kPcThreadsPerEra * i;
+        const int cc = min(c, ncand - 1);
+        const int kk = cc / T;
+        const int t = cc - kk * T;
         const int k = k0 + kk;
-        slot_el[i] = (pidx >= 0 && pidx < kPcEras * ncand) ? el : kPcEras;  // kPcEras: unused
+        slot_el[i] = (ptid >= 0 && c < ncand) ? my_el : kPcEras;  // kPcEras: unused
         slot_c[i] = c;
         const int thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
-        slot_off[i] = (int32_t)((int64_t)el * estride + node_off + (int64_t)k * pt + thr);
+        slot_off[i] = (int32_t)((int64_t)my_el * estride + node_off + (int64_t)k * pt + thr);
     }
 
-    PairIn pin[kPcPairs];
+    // next chunk's inputs: this thread's era totals, and per pair the prefix count and grad
+    int pct = 0;
+    float pGt = 0.0f;
+    int pL[kPcPairs];
+    float pGL[kPcPairs];
     auto prefetch = [&](int chunk) {
         const int e0 = chunk * kPcEras;
         const int ne = min(kPcEras, a.E - e0);
         const int64_t eoff = (int64_t)e0 * estride;
+        const bool live = chunk < nchunks;
+        pct = 0;
+        pGt = 0.0f;
+        if (live && slot_el[0] < ne) {  // slot 0 is valid whenever any slot of the thread is
+            const int64_t to = (int64_t)(e0 + my_el) * a.U + u;  // era total
+            pct = a.tot_cnt[to];
+            pGt = a.tot_g[to];
+        }
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
             if (i >= np) break;
-            pin[i].ctot = 0;
-            pin[i].L = 0;
-            pin[i].Gt = 0.0f;
-            pin[i].GL = 0.0f;
-            if (chunk < nchunks && slot_el[i] < ne) {
+            pL[i] = 0;
+            pGL[i] = 0.0f;
+            if (live && slot_el[i] < ne) {
                 const int64_t off = eoff + slot_off[i];
-                const int64_t to = (int64_t)(e0 + slot_el[i]) * a.U + u;  // era total
-                pin[i].ctot = a.tot_cnt[to];
-                pin[i].Gt = a.tot_g[to];
-                pin[i].L = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
-                pin[i].GL = a.g[off];
+                pL[i] = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
+                pGL[i] = a.g[off];
             }
         }
     };
     // Branch-free per pair (the same float operations as the reference, evaluated for every
-    // pair and selected), so the divide sequences of all pairs interleave.
+    // pair and selected), so the divide sequences of all pairs interleave. The parent term
+    // depends on the era only and is computed once per thread, with the same operations.
     auto produce = [&](int chunk) {
         float4* buf = ring + (chunk & 1) * kPcEras * kWave;
+        const int ctot = pct;
+        const bool has = ctot != 0;
+        const float Gt = pGt;
+        const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
+        const float pden = (float)ctot + lam;
+        const float pq = (0.5f * (Gt * Gt)) / pden;
+        const float parent = (pden > 0.0f) ? pq : 0.0f;
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
             if (i >= np) break;
-            const int ctot = pin[i].ctot;
-            const bool has = ctot != 0;
-            const float Gt = pin[i].Gt;
-            const int Lc = pin[i].L;
-            const float GLc = pin[i].GL;
+            const int Lc = pL[i];
+            const float GLc = pGL[i];
             const int R = ctot - Lc;
             const float GR = Gt - GLc;
-            const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
             const float w = (has && Lc > 0 && R > 0) ? wera : 0.0f;
             const float dL = (float)Lc + lam;
             const float dR = (float)R + lam;
-            const float pden = (float)ctot + lam;
-            const float pq = (0.5f * (Gt * Gt)) / pden;
-            const float parent = (pden > 0.0f) ? pq : 0.0f;
             const float gfull = 0.5f * ((GLc * GLc) / dL + (GR * GR) / dR) - parent;
             bool pos = true;
             if (use_dir) {
@@ -625,7 +637,8 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
             const int el = slot_el[i];
             const int c = slot_c[i];
             // eras past the end of the last chunk get neutral records (no rows, zero
-            // weight: pin is zero there), so the consumer reads whole batches unconditionally
+            // weight: the prefetched values are zero there), so the consumer reads whole
+            // batches unconditionally
             if (el < kPcEras) {
                 buf[el * kWave + c] = make_float4(gain, GL, __int_as_float(L), wd);
                 if (c == 0) {
