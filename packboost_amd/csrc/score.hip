@@ -509,7 +509,8 @@ constexpr int kPcThreadsPerEra = kPcProducers / kPcEras;              // 8
 constexpr int kPcPairs = (kWave + kPcThreadsPerEra - 1) / kPcThreadsPerEra;  // 8 pairs per thread
 
 template <bool C32>
-__global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
+// three workgroups fit a CU's LDS: the register budget is held to the same occupancy
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) void des_score_pc_kernel(ScoreArgs a) {
     extern __shared__ unsigned char smem[];
     const int tid = threadIdx.x;
     const int u = blockIdx.x / a.ntiles;
@@ -667,14 +668,22 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
     auto consume = [&](int chunk, auto table_flag, auto dir_flag) {
         constexpr bool TABLE = decltype(table_flag)::value;
         constexpr bool DIR = decltype(dir_flag)::value;
-        const int e0 = chunk * kPcEras;
-        const int ne = min(kPcEras, a.E - e0);
         const float4* buf = ring + (chunk & 1) * kPcEras * kWave;
         static_assert(kPcEras % 8 == 0, "batches of 8 eras must tile a chunk");
-        for (int b0 = 0; b0 < ne; b0 += 8) {
-            float4 rec[8];
+        // All kPcEras rows of a chunk hold records (eras past the last one are neutral: no rows,
+        // zero weight, which leave every sum bit-unchanged), so the batches are unrolled and
+        // batch bi + 1's records are read while batch bi runs its chains.
+        constexpr int kBatches = kPcEras / 8;
+        float4 rec[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) rec[j] = buf[(b0 + j) * kWave + tid];
+        for (int j = 0; j < 8; ++j) rec[j] = buf[j * kWave + tid];
+#pragma unroll
+        for (int bi = 0; bi < kBatches; ++bi) {
+            float4 nxt[8];
+            if (bi + 1 < kBatches) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) nxt[j] = buf[((bi + 1) * 8 + j) * kWave + tid];
+            }
             float fac[8], wv[8];
             bool actv[8];
 #pragma unroll
@@ -709,6 +718,10 @@ __global__ __launch_bounds__(kBlock) void des_score_pc_kernel(ScoreArgs a) {
                     agn = act ? agn + w * ((rec[j].w > 0.0f) ? 1.0f : -1.0f) : agn;
                     agd = act ? agd + w : agd;
                 }
+            }
+            if (bi + 1 < kBatches) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) rec[j] = nxt[j];
             }
         }
     };
