@@ -8,13 +8,14 @@ boosting round (gradient, 6 depths of histogram -> DES score -> decide -> partit
 aggregation, decision read-back and host tree build), the same span as the reference's
 round_seconds (booster.py:495, 654).
 
-Also reported: the histogram kernel's achieved GB/s (algorithmic bytes / average launch
-time from HIP events on the fit's stream) against the 8 TB/s HBM peak, where the algorithmic
-bytes use the per-unit figures of the reference's formats (one byte per bin code, grad f32 and a
-4-byte node id per row, 4-byte count and grad per histogram cell; hess is never moved); beside it
-the bytes this build's layouts move (nibble bins, 2-byte node ids, compact planes) and the HBM
-traffic rocprofv3 measured; and the CPU oracle (restated reference CPU frontier, C/OpenMP) timed
-on a bounded row sample on the host.
+Also reported: the histogram kernel's achieved GB/s against the 8 TB/s HBM peak, from the
+bytes this build's layouts move per launch (bin codes at half a byte per row in the nibble
+layout, grad f32 and a 2-byte node id per row, the compact planes written) over the average
+launch time from HIP events on the fit's stream; beside it the same time priced in the
+reference's formats (one byte per bin code, 8 bytes of row state, 8 bytes per histogram cell),
+and the HBM traffic rocprofv3 measured. The CPU baseline is the reference's own compiled
+frontier (frontier_cpu.cpp, oracle/_ref) under the oracle's restated fit loop, timed on a
+bounded row sample on the host cores (the C restatement when oracle/_ref is absent).
 """
 
 from __future__ import annotations
@@ -83,8 +84,38 @@ def make_device_data(c: dict, seed: int = 42):
     return bins, y, off
 
 
+def host_cpu() -> dict:
+    """Host CPU facts for the baseline: model, sockets, physical cores, threads per core
+    (lscpu) and the CPUs this process may run on."""
+    import subprocess
+
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    def num(key):
+        try:
+            return int(info.get(key, ""))
+        except ValueError:
+            return None
+    sockets, per_socket, tpc = num("Socket(s)"), num("Core(s) per socket"), num("Thread(s) per core")
+    return {
+        "model": info.get("Model name"),
+        "sockets": sockets,
+        "physical_cores": sockets * per_socket if sockets and per_socket else None,
+        "threads_per_core": tpc,
+        "cpus_allowed": len(os.sched_getaffinity(0)),
+    }
+
+
 def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None) -> dict:
-    """Oracle (restated reference CPU frontier + fit loop) on a bounded row sample."""
+    """The reference CPU path on a bounded row sample: the oracle's restated fit loop with each
+    depth's split finder run by the reference's own compiled frontier (frontier_cpu.cpp, OpenMP
+    over nodes, built into oracle/_ref), or by the C restatement when that is not built."""
     from oracle import oracle as ref
 
     N, F, E, nb = c["rows"], c["features"], c["eras"], c["bins"]
@@ -93,13 +124,15 @@ def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None
     bins = rng.integers(0, nb, size=(n_s, F), dtype=np.uint8)
     y = (rng.integers(0, 5, size=n_s) / 4.0).astype(np.float32)
     codes = np.repeat(np.arange(E), np.diff(era_offsets(n_s, E)))
+    splitter = "reference" if ref.ref_module() is not None else "restated"
     gen = __import__("torch").Generator().manual_seed(42)
     times = []
     t_start = time.perf_counter()
     while len(times) < 6 and (len(times) < 2 or time.perf_counter() - t_start < budget_s):
         r = ref.fit(bins, y, codes, num_rounds=1, pack_size=c["pack_size"], max_depth=c["max_depth"],
                     learning_rate=c["lr"], lambda_l2=c["lambda_l2"], lambda_dro=c["lambda_dro"],
-                    min_samples_leaf=c["msl"], max_bins=nb, layer_feature_fraction=c["frac"], rng=gen)
+                    min_samples_leaf=c["msl"], max_bins=nb, layer_feature_fraction=c["frac"], rng=gen,
+                    splitter=splitter)
         times.append(r.round_seconds[0])
     steady = times[1:] if len(times) > 1 else times
     sec = float(np.mean(steady))
@@ -107,9 +140,12 @@ def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None
         "value": (n_s / N) / sec,
         "unit": "rounds/s",
         "cores": int(ref.lib().oracle_num_threads()),
-        "kind": "port",
+        "kind": "reference" if splitter == "reference" else "port",
         "sample": (f"{n_s} rows x {F} features (row-major int8), {E} eras, full {c['max_depth']}-depth "
-                   f"rounds; mean of {len(steady)} rounds = {sec:.3f} s, scaled by rows {n_s}/{N}"),
+                   f"rounds; {'reference frontier_cpu.cpp' if splitter == 'reference' else 'C restatement'}"
+                   f" under the restated fit loop; mean of {len(steady)} rounds = {sec:.3f} s, "
+                   f"scaled by rows {n_s}/{N}"),
+        "host": host_cpu(),
     }
 
 
@@ -359,7 +395,8 @@ def main() -> int:
             moved_bytes += rows * K * bin_bytes + rows * 6 + u * E * (K * (nb - 1) * 6 + 8)
     hist_ms = float(prof_ms[0].sum())
     n_hist = int(prof_n[0].sum())
-    achieved = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
+    achieved = moved_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
+    ref_format_gbs = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     rounds_per_s = args.steps / elapsed
     metric = METRIC if args.config == 3 else (
         f"boosting rounds/sec (B={c['pack_size']},D={c['max_depth']}, {N}x{c['features']}) on 1 GPU; "
@@ -392,16 +429,20 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "copy_peak_gbs": round(copy_gbs, 1),
-            "frac_of_copy_peak": round(achieved / copy_gbs, 4) if copy_gbs > 0 else None,
             "traffic": profiled_traffic(args.config, N),
             "kernel": "hist_era_kernel",
             "bin_layout": "nibble" if fit.bins4 is not None else "u8",
             "avg_launch_ms": round(hist_ms / max(n_hist, 1), 4),
-            "algorithmic_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
-            "algorithmic_bytes": "rows*K*1 + rows*8 + U*E*K*nb*8 per depth (reference formats, no hess)",
-            "moved_bytes_per_launch": round(moved_bytes / max(n_hist, 1)),
-            "moved_gbs": round(moved_bytes / (hist_ms * 1e-3) / 1e9, 1) if hist_ms > 0 else 0.0,
+            "algorithmic_bytes_per_launch": round(moved_bytes / max(n_hist, 1)),
+            "algorithmic_bytes": ("per depth: rows*K*b (bin codes, b = 1/2 nibble or 1 uint8) + rows*6 "
+                                  "(grad f32, node id u16) + U*E*(K*(nb-1)*6 + 8) (compact planes "
+                                  "written); rows = rows of the depth's active nodes"),
+            "copy_peak_gbs": round(copy_gbs, 1),
+            "frac_of_copy_peak": round(achieved / copy_gbs, 4) if copy_gbs > 0 else None,
+            "reference_format_bytes_per_launch": round(hist_bytes / max(n_hist, 1)),
+            "reference_format_gbs": round(ref_format_gbs, 1),
+            "reference_format_frac": round(ref_format_gbs / HBM_PEAK_GBS, 4),
+            "reference_format_bytes": "rows*K*1 + rows*8 + U*E*K*nb*8 per depth (reference layouts, no hess)",
         },
         "profiled_rounds": {"hist_events": f"every {PROFILE_EVERY}th timed round",
                             "phase_breakdown": f"first {n_phase} rounds replayed untimed"},
@@ -414,7 +455,7 @@ def main() -> int:
     del bins
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline and args.config == 3:
-        print("[bench] timing the CPU oracle on a row sample", file=sys.stderr, flush=True)
+        print("[bench] timing the reference CPU frontier on a row sample", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(c, args.cpu_budget)
     print(json.dumps(out), flush=True)
     return 0

@@ -92,7 +92,9 @@ typedef struct {
     int32_t reserved;
 } pb_decision;
 
-/* Candidate record (one per wavefront winner, or per lane when dumped for tests). */
+/* Candidate record (one per wavefront winner, or per lane when dumped for tests). In a
+ * wavefront winner, reserved[0] counts that wavefront's valid candidates scoring within
+ * 64e-12 of the winner (the decision step's tie-band bound); elsewhere it is 0. */
 typedef struct {
     float score;
     int32_t left_total;
@@ -127,8 +129,8 @@ const int32_t* pb_era_offsets_dev(const pb_ctx* ctx);
 /* ---- round driver ------------------------------------------------------------------ */
 /* grad = preds - y (booster.py:2149-2151, squared loss; hess == 1, booster.py:2153-2154);
  * resets the per-round frontier: every row in root node 0 (active iff N >= 2*msl,
- * booster.py:794-796), tree size 1. Also records max|grad| for the histogram's
- * fixed-point scale. */
+ * booster.py:794-796), tree size 1. Also records the bounds of the histogram's fixed-point
+ * gradient scale (max |grad| and the largest |grad| sum over 1024 consecutive rows). */
 int pb_round_begin(pb_ctx* ctx, const float* preds_dev, const float* y_dev, float* grad_dev,
                    uint16_t* nid_dev, uint16_t* tnode_dev, void* stream);
 
@@ -144,6 +146,8 @@ int pb_round_begin(pb_ctx* ctx, const float* preds_dev, const float* y_dev, floa
  *                 totals [E][max_nodes]
  *   hist_grad_dev float32 [E][max_nodes][K][T]: prefix grad sums; elements O ..: era totals.
  * feats_dev: int32 [K] feature ids; `depth` selects the frontier's active-node count.
+ * grad_dev must hold the gradients the last pb_round_begin on this context wrote: their
+ * per-era |grad| sums set the exact fixed-point scale of each era's sums.
  * Eras of any size: an era above 16384 rows is built in parts whose exact sums are added up
  * before the planes are written, so the planes do not depend on the split. */
 int pb_hist_build(pb_ctx* ctx, const uint8_t* bins_dev, const float* grad_dev,
@@ -160,7 +164,11 @@ int pb_des_score(pb_ctx* ctx, const int32_t* hist_cnt_dev, const float* hist_gra
                  const int32_t* feats_dev, int32_t K, int32_t depth, int32_t max_nodes,
                  const pb_split_params* params, pb_candidate* cand_all_dev, void* stream);
 
-/* Applies the per-node winners of the last pb_des_score: builds the decisions of this
+/* Applies the per-node winners of the last pb_des_score: picks each node's split with the
+ * reference's sequential scan (features in subset order, thresholds ascending; a candidate wins
+ * with a higher score, or within 1e-12 of the best with more left rows, then a larger feature
+ * id, then a larger threshold: frontier_cpu.cpp:415-426), reading the feature ids that call was
+ * given (keep feats_dev valid until this call's work has run), builds the decisions of this
  * depth (booster.py:527-563: split -> children ids (len, len+1), child values
  * -G/(H+lambda); no split -> leaf value -G/(H+lambda)), assigns the next frontier
  * (children with >= 2*msl rows, booster.py:516, 794-796) and writes the depth's

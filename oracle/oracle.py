@@ -208,6 +208,69 @@ def mass_cuts(counts: np.ndarray, max_bins: int, k: int) -> np.ndarray:
     return out[:n].copy()
 
 
+# ------------------------------------------------------------ the compiled reference frontier
+_ref_mod = None
+
+
+def ref_module():
+    """The reference's own find_best_splits_batched_cpu (frontier_cpu.cpp + bindings.cpp,
+    compiled by `make -C oracle ref` into oracle/_ref), or None when it is not built."""
+    global _ref_mod
+    if _ref_mod is None:
+        import glob
+        import importlib.util
+
+        hits = glob.glob(str(REF_DIR / "_backend*.so"))
+        if not hits:
+            return None
+        spec = importlib.util.spec_from_file_location("_backend", hits[0])
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _ref_mod = mod
+    return _ref_mod
+
+
+def ref_split_batch(bins: np.ndarray, grad: np.ndarray, nodes_era_rows: list[list[np.ndarray]],
+                    feats: np.ndarray, max_bins: int, k_cuts: int = 0, cut_selection: str = "mass",
+                    lambda_l2: float = 1e-6, lambda_dro: float = 0.0, direction_weight: float = 0.0,
+                    era_alpha: float = 0.0, min_samples_leaf: int = 20) -> SplitResult:
+    """split_batch through the compiled reference frontier (frontier_cpu.cpp:111-515) instead of
+    the restatement; its decisions and left/right row lists are mapped onto SplitResult."""
+    mod = ref_module()
+    if mod is None:
+        raise RuntimeError("oracle/_ref is not built (`make -C oracle ref`)")
+    M = len(nodes_era_rows)
+    decs, stats = mod.find_best_splits_batched_cpu(
+        np.ascontiguousarray(bins, dtype=np.uint8).view(np.int8), np.ascontiguousarray(grad, np.float32),
+        nodes_era_rows, np.ascontiguousarray(feats, np.int32), int(max_bins), int(k_cuts), cut_selection,
+        float(lambda_l2), float(lambda_dro), float(direction_weight), float(era_alpha),
+        int(min_samples_leaf))
+    n = max(M, 1)
+    out = {k: np.zeros(n, dt) for k, dt in [
+        ("feature", np.int32), ("threshold", np.int32), ("score", np.float32),
+        ("left_grad", np.float32), ("left_hess", np.float32), ("right_grad", np.float32),
+        ("right_hess", np.float32), ("left_count", np.int64), ("right_count", np.int64)]}
+    # go_left per entry of the node-major, era-major row lists: the rows are distinct, so a
+    # mask over all rows marks the reference's left lists
+    left = np.zeros(bins.shape[0], dtype=np.uint8)
+    for m, eras in enumerate(nodes_era_rows):
+        d = decs[m]
+        if d is None:
+            out["feature"][m] = -1
+            continue
+        for key in out:
+            out[key][m] = d[key]
+        lr = [np.asarray(x, dtype=np.int64) for x in d["left_rows"] if len(x)]
+        if lr:
+            left[np.concatenate(lr)] = 1
+    rows = [np.asarray(r, dtype=np.int64) for eras in nodes_era_rows for r in eras]
+    go_left = left[np.concatenate(rows)] if rows else np.zeros(0, np.uint8)
+    tim = np.array([stats.get("hist_ms", 0.0), stats.get("scan_ms", 0.0), stats.get("score_ms", 0.0),
+                    stats.get("partition_ms", 0.0)], dtype=np.float64)
+    return SplitResult(**{k: v[:M] for k, v in out.items()}, go_left=go_left, planes=None,
+                       cands=None, timings=tim)
+
+
 # ----------------------------------------------------------------------------- fit loop
 @dataclass
 class FitResult:
@@ -230,8 +293,12 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
         min_samples_leaf: int = 20, max_bins: int = 63, k_cuts: int = 0,
         cut_selection: str = "mass", layer_feature_fraction: float = 1.0, era_alpha: float = 0.0,
         random_state: int | None = None, rng: torch.Generator | None = None,
-        stop_after_depths: int | None = None, trace: list | None = None) -> FitResult:
-    """PackBoost.fit on the native CPU path, restated (booster.py:375-599)."""
+        stop_after_depths: int | None = None, trace: list | None = None,
+        splitter: str = "restated") -> FitResult:
+    """PackBoost.fit on the native CPU path, restated (booster.py:375-599). splitter
+    "reference" runs each depth's split finder on the compiled reference frontier
+    (ref_split_batch) instead of the C restatement."""
+    split_fn = ref_split_batch if splitter == "reference" else split_batch
     import time
 
     bins = np.ascontiguousarray(bins, dtype=np.uint8)
@@ -273,8 +340,8 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
             if not active:
                 break
             feat_subset = torch.randperm(F, generator=rng)[:k].numpy().astype(np.int32)
-            res = split_batch(bins, grad, [er for _, er in active], feat_subset, max_bins, k_cuts,
-                              cut_selection, lambda_l2, lambda_dro, direction_weight, era_alpha, msl)
+            res = split_fn(bins, grad, [er for _, er in active], feat_subset, max_bins, k_cuts,
+                           cut_selection, lambda_l2, lambda_dro, direction_weight, era_alpha, msl)
             split_ms += float(res.timings.sum())
             if trace is not None:
                 trace.append({"round": len(rounds), "depth": depth, "node_ids": [n for n, _ in active],
@@ -316,7 +383,8 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
                 nxt.append((li, lrows))
                 nxt.append((ri, rrows))
             logs.append({"depth": depth, "nodes_processed": len(active),
-                         "nodes_collapsed": (pack_size - 1) * len(active)})
+                         "nodes_collapsed": (pack_size - 1) * len(active),
+                         "rows_total": int(sum(r.size for _, er in active for r in er))})
             frontier = nxt
         arrs = {key: np.array([n[key] for n in nodes]) for key in
                 ("feature", "threshold", "left", "right", "value", "is_leaf")}

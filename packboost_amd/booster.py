@@ -81,21 +81,26 @@ class Tree:
 
 
 class TreeBuilder:
+    """Grows one tree in breadth-first id order (booster.py:172-190): node 0 is the root and a
+    split appends the two children at the end of the node list, so the ids a depth creates are
+    consecutive and follow the order in which its nodes split."""
+
     def __init__(self) -> None:
         self.nodes: List[TreeNode] = [TreeNode()]
 
     def set_leaf(self, node_id: int, value: float) -> None:
-        n = self.nodes[node_id]
-        n.value = float(value); n.is_leaf = True
-        n.feature = -1; n.threshold = 0; n.left = -1; n.right = -1
+        """Turns node_id into a leaf holding `value` (clearing any split it held)."""
+        self.nodes[node_id] = TreeNode(value=float(value))
 
     def split(self, node_id: int, feature: int, threshold: int) -> Tuple[int, int]:
-        n = self.nodes[node_id]
-        n.feature = int(feature); n.threshold = int(threshold); n.is_leaf = False
-        l = len(self.nodes); r = l + 1
-        n.left = l; n.right = r
-        self.nodes.append(TreeNode()); self.nodes.append(TreeNode())
-        return l, r
+        """Splits node_id on (feature, threshold); returns the ids of its new children."""
+        first_child = len(self.nodes)
+        node = self.nodes[node_id]
+        node.is_leaf = False
+        node.feature, node.threshold = int(feature), int(threshold)
+        node.left, node.right = first_child, first_child + 1
+        self.nodes.extend((TreeNode(), TreeNode()))
+        return node.left, node.right
 
     def build(self) -> Tree:
         return Tree(nodes=self.nodes)
@@ -193,6 +198,12 @@ class PackBoost:
         self._packed_forest: list[dict[str, torch.Tensor]] = []
         self._num_features: int | None = None
         self._use_native_cuda = self._device.type == "cuda" and native_backends.cuda_available()
+        # per-depth phase times in the depth logs (hist_ms, score_ms, partition_ms): off by
+        # default, since timing every phase runs the rounds one at a time
+        self.profile_phases = os.getenv("PACKBOOST_PROFILE_PHASES", "0") not in ("", "0")
+
+    def _phase_times(self) -> bool:
+        return bool(self.profile_phases)
 
     # ---------------------------------------------------------------- public
     @property
@@ -274,7 +285,7 @@ class PackBoost:
         try:
             t0 = perf_counter()
             for round_idx, (log, preds_after, ready) in enumerate(
-                    fitter.rounds(self._rng, num_rounds)):
+                    fitter.rounds(self._rng, num_rounds, phase_times=self._phase_times())):
                 arrs = tree_arrays_from_log(log, cfg, N)
                 self._rounds.append(arrs)
                 self._trees_cache = None
@@ -389,24 +400,38 @@ class PackBoost:
                 "corr_scratch": torch.empty(E + 1, dtype=torch.float64, device=device),
                 "num_eras": E,
                 "preds": torch.zeros(n, dtype=torch.float32, device=device),
+                "rounds_done": 0,
             })
         return states
 
     def _update_eval(self, states: list[dict]) -> None:
-        # Like the reference (booster.py:236-274) the eval predictions are recomputed over
-        # every tree so far, in tree order, so they equal predict() on the same rows.
+        # Like the reference (booster.py:236-274) the eval predictions equal predict() on the
+        # same rows: the sum over every tree so far, in tree order, of float32(weight * value).
+        # That sum is a left fold, so each state extends its own fold by the rounds it has not
+        # seen, one float32 add per tree: the B trees of a round are identical, so the round's
+        # tree is walked once (pb_predict_bins) and its weighted value added B times. The host
+        # work per eval is the new rounds only.
         B = int(self.config.pack_size)
+        w = torch.tensor(np.float32(self._tree_weight), dtype=torch.float32)
         lib = _hip.load()
         for st in states:
-            f = pack_forest(self._rounds, B, st["preds"].device)
-            out = torch.empty_like(st["preds"])
-            _hip.check(lib.pb_predict_forest(
-                st["bins_fm"].data_ptr(), st["n"], st["bins_fm"].shape[1], st["bins_fm"].shape[0],
-                f["feature"].data_ptr(), f["threshold"].data_ptr(), f["left_abs"].data_ptr(),
-                f["right_abs"].data_ptr(), f["value"].data_ptr(), f["is_leaf"].data_ptr(),
-                f["offsets"].data_ptr(), int(f["offsets"].numel() - 1), int(f["value"].numel()),
-                float(self._tree_weight), out.data_ptr(), _hip.stream_ptr()), "pb_predict_forest")
-            st["preds"] = out
+            dev = st["preds"].device
+            wd = w.to(dev)
+            while st["rounds_done"] < len(self._rounds):
+                a = self._rounds[st["rounds_done"]]
+                t = {k: torch.from_numpy(np.ascontiguousarray(np.asarray(a[k]), dtype=dt)).to(dev)
+                     for k, dt in (("feature", np.int32), ("threshold", np.int32), ("left", np.int32),
+                                   ("right", np.int32), ("value", np.float32), ("is_leaf", np.uint8))}
+                v = torch.empty(st["n"], dtype=torch.float32, device=dev)
+                _hip.check(lib.pb_predict_bins(
+                    st["bins_fm"].data_ptr(), st["n"], st["bins_fm"].shape[1], st["bins_fm"].shape[0],
+                    t["feature"].data_ptr(), t["threshold"].data_ptr(), t["left"].data_ptr(),
+                    t["right"].data_ptr(), t["value"].data_ptr(), t["is_leaf"].data_ptr(),
+                    int(t["value"].numel()), v.data_ptr(), _hip.stream_ptr()), "pb_predict_bins")
+                term = wd * v
+                for _ in range(B):
+                    st["preds"] = st["preds"] + term
+                st["rounds_done"] += 1
 
 
 def pack_forest(rounds: Sequence[dict[str, np.ndarray]], pack_size: int,

@@ -34,12 +34,18 @@ struct pb_ctx {
     int32_t S;
     int32_t* seg_info_dev;  // [S][4] per work segment: first row, end row, era, slot of a
                             // split era (-1: the era is one segment)
+    float* win_sum;         // |grad| sum per window of pb::kGradWinRows rows (round_begin)
+    int32_t* sh_era;        // [E] fixed-point gradient scale exponent of each era
     int32_t n_acc;          // eras split into several segments
     int32_t* acc_era_dev;   // [n_acc]
     uint32_t* acc_cnt;      // [n_acc][umax][max_feats][nb]
     unsigned long long* acc_g;
     bool cnt32;             // planes carry 32-bit counts (an era above 65535 rows)
     int32_t last_w;
+    pb::SeqCands seq;              // every candidate of a depth [umax][max_feats][tmax]
+    int32_t last_K, last_T;        // shape, feature ids and threshold table of the last
+    const int32_t* last_feats;     // pb_des_score, read by pb_decide
+    const int32_t* last_thr_tab;
     int64_t lds_budget;
     int32_t force_copies;
     int32_t force_ftile;
@@ -112,10 +118,16 @@ int dev_alloc(T** p, size_t n, const char* what) {
 void free_ctx(pb_ctx* c) {
     if (!c) return;
     (void)hipFree(c->era_off_dev);
+    (void)hipFree(c->win_sum);
+    (void)hipFree(c->sh_era);
     (void)hipFree(c->st);
     (void)hipFree(c->rules);
     (void)hipFree(c->ntot);
     (void)hipFree(c->cand_w);
+    (void)hipFree(c->seq.score);
+    (void)hipFree(c->seq.lt);
+    (void)hipFree(c->seq.lg);
+    (void)hipFree(c->seq.band);
     (void)hipFree(c->node_best);
     (void)hipFree(c->ids[0]);
     (void)hipFree(c->ids[1]);
@@ -249,10 +261,17 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
         }
     }
     if ((rc = dev_alloc(&c->era_off_dev, d.num_eras + 1, "alloc era offsets")) ||
+        (rc = dev_alloc(&c->win_sum, (c->rows_padded + pb::kGradWinRows - 1) / pb::kGradWinRows,
+                        "alloc gradient windows")) ||
+        (rc = dev_alloc(&c->sh_era, d.num_eras, "alloc era scales")) ||
         (rc = dev_alloc(&c->st, 1, "alloc frontier")) ||
         (rc = dev_alloc(&c->rules, c->umax, "alloc split rules")) ||
         (rc = dev_alloc(&c->ntot, c->umax, "alloc node totals")) ||
         (rc = dev_alloc(&c->cand_w, (size_t)c->umax * c->wmax, "alloc candidates")) ||
+        (rc = dev_alloc(&c->seq.score, (size_t)c->umax * d.max_feats * tmax, "alloc candidates")) ||
+        (rc = dev_alloc(&c->seq.lt, (size_t)c->umax * d.max_feats * tmax, "alloc candidates")) ||
+        (rc = dev_alloc(&c->seq.lg, (size_t)c->umax * d.max_feats * tmax, "alloc candidates")) ||
+        (rc = dev_alloc(&c->seq.band, (size_t)c->umax * d.max_feats * tmax, "alloc candidates")) ||
         (rc = dev_alloc(&c->node_best, c->umax, "alloc node winners")) ||
         (rc = dev_alloc(&c->ids[0], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
         (rc = dev_alloc(&c->ids[1], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
@@ -266,7 +285,8 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
         free_ctx(c);
         return hip_fail(e, "copy era offsets");
     }
-    e = hipMemset(c->st, 0, sizeof(pb::Frontier));
+    e = hipMemset(c->sh_era, 0, sizeof(int32_t) * d.num_eras);
+    if (e == hipSuccess) e = hipMemset(c->st, 0, sizeof(pb::Frontier));
     if (e != hipSuccess) {
         free_ctx(c);
         return hip_fail(e, "clear frontier");
@@ -298,7 +318,8 @@ int pb_round_begin(pb_ctx* c, const float* preds, const float* y, float* grad, u
         return fail(PB_ERR_INVALID, "pb_round_begin: null argument");
     const int64_t N = c->d.num_rows;
     const int32_t root_active = (N >= 2 * (int64_t)c->d.min_samples_leaf) ? 1 : 0;
-    PB_HIP(pb::launch_round_begin(preds, y, grad, nid, tnode, N, c->rows_padded, root_active, c->st,
+    PB_HIP(pb::launch_round_begin(preds, y, grad, nid, tnode, N, c->rows_padded, root_active,
+                                  c->era_off_dev, c->d.num_eras, c->win_sum, c->sh_era, c->st,
                                   c->ids[0], (hipStream_t)stream),
            "round_begin launch");
     return PB_OK;
@@ -412,6 +433,9 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     a.S = c->S;
     a.acc_cnt = c->acc_cnt;
     a.acc_g = c->acc_g;
+    a.acc_U = c->umax;  // active nodes < umax whatever max_nodes the caller passes
+    a.acc_K = c->d.max_feats;
+    a.sh_era = c->sh_era;
     const int eras8 = (a.S + 7) / 8 * 8;  // segments, a multiple of the 8 XCDs
     const int64_t grid = (int64_t)eras8 * a.ntiles * node_tiles;
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_hist_build: grid too large");
@@ -425,6 +449,9 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
         f.U = max_nodes;
         f.K = K;
         f.nb = nb;
+        f.acc_U = a.acc_U;
+        f.acc_K = a.acc_K;
+        f.sh_era = c->sh_era;
         f.st = c->st;
         f.depth = depth;
         f.out_cnt = a.out_cnt;
@@ -532,7 +559,12 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     a.wpt = sh.wpt;
     a.rt = sh.rt;
     a.staged = c->score_staged;
+    a.seq = c->seq;
     c->last_w = sh.ntiles * sh.wpt;
+    c->last_K = K;
+    c->last_T = T;
+    c->last_feats = feats;
+    c->last_thr_tab = thr_tab;
     PB_HIP(pb::launch_score(a, (int)grid, sh.lds_bytes, (hipStream_t)stream), "score launch");
     return PB_OK;
 }
@@ -544,9 +576,17 @@ int pb_decide(pb_ctx* c, int32_t depth, int32_t max_nodes, const pb_split_params
     if (c->last_w <= 0) return fail(PB_ERR_INVALID, "pb_decide: call pb_des_score first");
     if (max_nodes < max_nodes_at(c, depth))
         return fail(PB_ERR_INVALID, "pb_decide: max_nodes below the frontier bound of this depth");
-    PB_HIP(pb::launch_decide(c->cand_w, c->last_w, max_nodes, c->ntot, c->st, depth, p->min_samples_leaf,
-                             p->lambda_l2, c->ids[depth & 1], c->ids[(depth + 1) & 1], c->rules,
-                             dec, values, c->node_best, (hipStream_t)stream),
+    pb::DecideCands dc;
+    dc.cand_w = c->cand_w;
+    dc.W = c->last_w;
+    dc.seq = c->seq;
+    dc.K = c->last_K;
+    dc.T = c->last_T;
+    dc.feats = c->last_feats;
+    dc.thr_tab = c->last_thr_tab;
+    PB_HIP(pb::launch_decide(dc, max_nodes, c->ntot, c->st, depth, p->min_samples_leaf, p->lambda_l2,
+                             c->ids[depth & 1], c->ids[(depth + 1) & 1], c->rules, dec, values,
+                             c->node_best, (hipStream_t)stream),
            "decide launch");
     return PB_OK;
 }

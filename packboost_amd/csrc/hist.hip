@@ -16,9 +16,10 @@
 //  * One 64-bit LDS atomic carries (fixed-point grad << 16) + 1, so the count (low 16 bits)
 //    and the grad sum (high 48 bits) accumulate in a single ds_add_u64. Integer addition is
 //    order-independent, so the result is deterministic run to run; grad is quantised as
-//    round(g * 2^s) with max|g| * 2^s < 2^30, far finer than float32 rounding of the
-//    reference's row-order sum. (A per-round 8-byte addend array instead of the 4-byte
-//    gradient measured slower: the row-side loads are re-read by every feature tile.)
+//    round(g * 2^s), with s set per round and era so that the era's sum of |q| stays below
+//    2^45 (era_grad_scale), far finer than float32 rounding of the reference's row-order sum.
+//    (A per-round 8-byte addend array instead of the 4-byte gradient measured slower: the
+//    row-side loads are re-read by every feature tile.)
 //  * Joint bins (P = 2 for nb <= 16, P = 3 for nb <= 6): the P features of a group share one
 //    atomic on the joint cell (b1 * nb + b2, or (b1 * nb + b2) * nb + b3). The joint index is
 //    below 256, so for 4 rows it comes from byte-wise multiply-adds of the packed bin dwords.
@@ -103,8 +104,6 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
     const int C = 1 << a.clog2;
     const int UT = a.node_tile;                      // nodes held in LDS per work item
     const int words_group = UT * cells_node * C;     // LDS words per group
-    const int sh = grad_scale_log2(a.st);  // rows add round(grad * 2^sh)
-    const float scale = ldexpf(1.0f, sh);
     const uint32_t copy = threadIdx.x & (C - 1);
     const uint32_t bin_shift = (uint32_t)a.clog2 + 3u;  // cell -> byte offset of its C copies
 
@@ -128,6 +127,8 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         const int4 si = seg_info[seg];  // one load: rows, era and slot of the segment
         const int era = si.z;
         const int slot = si.w;  // >= 0: add into the era's sums
+        const int sh = a.sh_era[era];  // rows add round(grad * 2^sh)
+        const float scale = ldexpf(1.0f, sh);
 
         const int ng = (nf + P - 1) / P;
         const int words = ng * words_group;
@@ -222,10 +223,14 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 const uint32_t nj = ok[j] ? n4[j] - (uint32_t)u0 : 0u;  // node within the tile
                 base[j] = __umul24(nj, cells_c8) + copy8;  // nj < 2^16, cells_c8 < 2^24
                 // (q << 16) + 1 as two 32-bit halves: the count 1 in the low 16 bits, the
-                // fixed-point grad above it (sign-extended into the high word); 0 if not counted
-                const int32_t q = __float2int_rn(g4[j] * scale);
-                const uint32_t lo = ((uint32_t)q << kCountBits) | 1u;
-                const uint32_t hi = (uint32_t)(q >> (32 - kCountBits));
+                // fixed-point grad q = round(g * 2^sh) above it (|q| < 2^45); 0 if not counted.
+                // In float, exactly: xq = q, xh = floor(q / 2^16) (the high word), xl = q - xh *
+                // 2^16 in [0, 2^16) (the grad's bits in the low word).
+                const float xq = rintf(g4[j] * scale);
+                const float xh = floorf(xq * (1.0f / 65536.0f));
+                const float xl = xq - xh * 65536.0f;
+                const uint32_t lo = ((uint32_t)xl << kCountBits) | 1u;
+                const uint32_t hi = (uint32_t)(int32_t)xh;
                 qv[j] = ((unsigned long long)(ok[j] ? hi : 0u) << 32) | (ok[j] ? lo : 0u);
                 if (!NIB) keep |= ok[j] ? (0xffu << (8 * j)) : 0u;
             }
@@ -440,14 +445,14 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         if (slot >= 0) {
             // part of a split era: add this segment's per-bin cells, exact integers, into the
             // era's sums (integer adds: the order of the segments does not matter)
-            const int64_t srow0 = ((int64_t)slot * a.U + u0) * a.K + k0;
+            const int64_t srow0 = ((int64_t)slot * a.acc_U + u0) * a.acc_K + k0;
             for (int it = threadIdx.x; it < items; it += BS) {
                 const Digits d = split(it);
                 const unsigned long long m = marginal(d, false);
                 const uint32_t cnt = (uint32_t)(m & ((1ull << kCountBits) - 1ull));
                 if (cnt == 0u) continue;
                 const long long Q = ((long long)(m - cnt)) >> kCountBits;
-                const int64_t o = (srow0 + (int64_t)d.u * a.K + d.kk) * nb + d.bb;
+                const int64_t o = (srow0 + (int64_t)d.u * a.acc_K + d.kk) * nb + d.bb;
                 atomicAdd(a.acc_cnt + o, cnt);
                 atomicAdd(a.acc_g + o, (unsigned long long)Q);
             }
@@ -599,7 +604,6 @@ hipError_t launch_layout(const HistArgs& a, int pairs, int grid, size_t lds_byte
 __global__ __launch_bounds__(kBlock) void finalize_kernel(FinalizeArgs f) {
     const int Ua = f.st->u_active[f.depth];
     const int64_t n = (int64_t)f.n_acc * Ua * f.K;
-    const double inv_scale = ldexp(1.0, -grad_scale_log2(f.st));
     const int pt = f.nb - 1;
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t t = (int64_t)blockIdx.x * kBlock + threadIdx.x; t < n; t += stride) {
@@ -608,8 +612,9 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(FinalizeArgs f) {
         const int slot = (int)(sk / Ua);
         const int u = (int)(sk - (int64_t)slot * Ua);
         const int era = f.acc_era[slot];
-        uint32_t* ac = f.acc_cnt + (((int64_t)slot * f.U + u) * f.K + k) * f.nb;
-        unsigned long long* ag = f.acc_g + (((int64_t)slot * f.U + u) * f.K + k) * f.nb;
+        const double inv_scale = ldexp(1.0, -f.sh_era[era]);
+        uint32_t* ac = f.acc_cnt + (((int64_t)slot * f.acc_U + u) * f.acc_K + k) * f.nb;
+        unsigned long long* ag = f.acc_g + (((int64_t)slot * f.acc_U + u) * f.acc_K + k) * f.nb;
         const int64_t o = (((int64_t)era * f.U + u) * f.K + k) * pt;
         uint32_t c = 0u;
         long long q = 0;
@@ -618,7 +623,7 @@ __global__ __launch_bounds__(kBlock) void finalize_kernel(FinalizeArgs f) {
             q += (long long)ag[b];
             ac[b] = 0u;
             ag[b] = 0ull;
-            const float gs = (float)((double)q * inv_scale);
+            const float gs = (float)((double)q * inv_scale);  // exact in double: |q| < 2^45
             if (b < pt) {
                 if (f.out_cnt32)
                     f.out_cnt32[o + b] = c;

@@ -92,43 +92,65 @@ __global__ void reset_kernel(Frontier* st, int32_t root_active, int32_t* cur_ids
         for (int d = 0; d <= PB_MAX_DEPTH; ++d) st->u_active[d] = 0;
         st->u_active[0] = root_active;
         st->tree_size = 1;
-        st->gmax_bits = 0u;
         cur_ids[0] = 0;
     }
 }
 
 // grad = preds - y (booster.py:2149-2151); hess == 1 is implicit (counts). Every row starts in
-// the root; the pad rows [N, rows_padded) are parked with grad 0 and PB_INACTIVE.
+// the root; the pad rows [N, rows_padded) are parked with grad 0 and PB_INACTIVE. Also the sum
+// of |grad| over each window of kGradWinRows consecutive rows (4 per thread, then a fixed
+// reduction tree, so the sums do not depend on scheduling), which bounds the eras' fixed-point
+// scales.
 __global__ __launch_bounds__(kBlock) void round_begin_kernel(const float* __restrict__ preds,
                                                          const float* __restrict__ y,
                                                          float* __restrict__ grad,
                                                          uint16_t* __restrict__ nid,
                                                          uint16_t* __restrict__ tnode, int64_t N,
                                                          int64_t rows_padded, int32_t root_active,
-                                                         Frontier* st) {
-    float amax = 0.0f;
-    const int64_t stride = (int64_t)gridDim.x * kBlock;
-    for (int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x; r < rows_padded; r += stride) {
-        float g = 0.0f;
-        if (r < N) {
-            g = preds[r] - y[r];
-            amax = fmaxf(amax, fabsf(g));
-        }
-        grad[r] = g;
-        nid[r] = (r < N && root_active) ? (uint16_t)0 : (uint16_t)PB_INACTIVE;
-        tnode[r] = 0;
-    }
-    // block max, then one atomic per block (non-negative floats order as their bit patterns)
-    __shared__ float s_max[kBlock / kWave];
+                                                         float* __restrict__ win_sum) {
+    __shared__ float s_sum[kBlock / kWave];
+    const int64_t nwin = (rows_padded + kGradWinRows - 1) / kGradWinRows;
+    for (int64_t w = blockIdx.x; w < nwin; w += gridDim.x) {
+        const int64_t r0 = w * kGradWinRows + (int64_t)threadIdx.x * 4;
+        float s = 0.0f;
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
-    if ((threadIdx.x & (kWave - 1)) == 0) s_max[threadIdx.x / kWave] = amax;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float b = s_max[0];
-        for (int w = 1; w < kBlock / kWave; ++w) b = fmaxf(b, s_max[w]);
-        if (b > 0.0f) atomicMax(&st->gmax_bits, __float_as_uint(b));
+        for (int j = 0; j < 4; ++j) {
+            const int64_t r = r0 + j;
+            if (r >= rows_padded) break;
+            float g = 0.0f;
+            if (r < N) {
+                g = preds[r] - y[r];
+                s = s + fabsf(g);
+            }
+            grad[r] = g;
+            nid[r] = (r < N && root_active) ? (uint16_t)0 : (uint16_t)PB_INACTIVE;
+            tnode[r] = 0;
+        }
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) s = s + __shfl_xor(s, m);
+        __syncthreads();  // the previous window's partial sums have been read
+        if ((threadIdx.x & (kWave - 1)) == 0) s_sum[threadIdx.x / kWave] = s;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float t = s_sum[0];
+            for (int i = 1; i < kBlock / kWave; ++i) t = t + s_sum[i];
+            win_sum[w] = t;
+        }
     }
+}
+
+// One thread per era: the era's |grad| sum is at most the sum over the windows it overlaps;
+// sh_era[e] = era_grad_scale of that bound.
+__global__ __launch_bounds__(kBlock) void era_scale_kernel(const int32_t* __restrict__ era_off, int32_t E,
+                                                       const float* __restrict__ win_sum,
+                                                       int32_t* __restrict__ sh_era) {
+    const int e = blockIdx.x * kBlock + threadIdx.x;
+    if (e >= E) return;
+    const int64_t r0 = era_off[e], r1 = era_off[e + 1];
+    double b = 0.0;
+    if (r1 > r0)
+        for (int64_t w = r0 / kGradWinRows; w <= (r1 - 1) / kGradWinRows; ++w) b += (double)win_sum[w];
+    sh_era[e] = era_grad_scale(b * (1.0 + 1.0 / 1024.0));
 }
 
 // feats[j][k] = window[off + j][k] for j < D, where off is the number of feature subsets the
@@ -193,13 +215,18 @@ hipError_t launch_select_subsets(const pb_round_header* prev, int32_t D, int32_t
 
 hipError_t launch_round_begin(const float* preds, const float* y, float* grad, uint16_t* nid,
                               uint16_t* tnode, int64_t N, int64_t rows_padded, int32_t root_active,
+                              const int32_t* era_off, int32_t E, float* win_sum, int32_t* sh_era,
                               Frontier* st, int32_t* cur_ids, hipStream_t s) {
     hipLaunchKernelGGL(reset_kernel, dim3(1), dim3(64), 0, s, st, root_active, cur_ids);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int grid = grid_for(rows_padded, kBlock, 1024);
+    const int grid = grid_for(rows_padded, kGradWinRows, 1024);
     hipLaunchKernelGGL(round_begin_kernel, dim3(grid), dim3(kBlock), 0, s, preds, y, grad, nid,
-                       tnode, N, rows_padded, root_active, st);
+                       tnode, N, rows_padded, root_active, win_sum);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(era_scale_kernel, dim3((E + kBlock - 1) / kBlock), dim3(kBlock), 0, s, era_off,
+                       E, win_sum, sh_era);
     return hipGetLastError();
 }
 

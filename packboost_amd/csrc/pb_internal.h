@@ -13,24 +13,30 @@ constexpr int kBlock = 256;        // threads per workgroup for the row kernels
 constexpr int kCountBits = 16;     // low bits of a histogram word hold the row count
 constexpr int kMaxEraRowsDirect = (1 << kCountBits) - 1;
 constexpr uint32_t kLeafFeatureBits = 0xFFFFFFu;  // compiled-forest leaf marker
-constexpr int kGradScaleLog2 = 30; // |grad| * scale < 2^30 -> fixed point fits int32 per row
+constexpr int kGradWinRows = kBlock * 4;  // rows per window of the round's |grad| sums
 
 // Frontier state of the round in flight; lives in device memory and is only written
 // by kernels, so a whole round is enqueued without host round trips.
 struct Frontier {
     int32_t u_active[PB_MAX_DEPTH + 1];  // active nodes per depth
     int32_t tree_size;                   // next TreeBuilder id
-    uint32_t gmax_bits;                  // float bits of max |grad| this round
-    int32_t reserved[6];
+    int32_t reserved[7];
 };
 
-// Exponent sh of the round's fixed-point gradient scale 2^sh: max|g| * 2^sh < 2^kGradScaleLog2,
-// capped so that 2^sh stays a finite float.
-__device__ __forceinline__ int grad_scale_log2(const Frontier* st) {
-    const float gmax = __uint_as_float(st->gmax_bits);
+// Fixed-point gradient scale of one era: rows add q = round(g * 2^sh) into the 48-bit grad field
+// of a histogram word. round_begin sums |g| over windows of kGradWinRows consecutive rows, and
+// era_scale_kernel bounds the era's sum of |g| by the sum of the windows that overlap it
+// (times 1 + 2^-10 for the float rounding of those sums), so
+//   sum over the era of |q| <= 2^sh * bound + rows / 2 < 2^45
+// with sh = 44 - ceil(log2(bound)): every cell, prefix, era total and split-era sum fits the
+// field with room to spare, and each row carries about 44 - log2(bound / |g|) bits, far finer
+// than the float32 rounding of the reference's row-order sums unless an era holds rows whose
+// |g| differ by many orders of magnitude. Capped so that 2^sh is a finite float.
+__device__ __forceinline__ int era_grad_scale(double bound) {
+    if (!(bound > 0.0)) return 0;
     int ex = 0;
-    (void)frexpf(gmax, &ex);
-    return (gmax > 0.f) ? min(kGradScaleLog2 - ex, 127) : 0;
+    (void)frexp(bound, &ex);  // bound < 2^ex
+    return min(44 - ex, 126);
 }
 
 // Per active node of the current depth, read by the partition kernel.
@@ -79,6 +85,8 @@ struct HistArgs {
     int32_t S;
     uint32_t* acc_cnt;
     unsigned long long* acc_g;
+    int32_t acc_U, acc_K;  // node and feature strides of acc_cnt / acc_g (their allocation)
+    const int32_t* sh_era;  // [E] fixed-point gradient scale exponent of each era
 };
 
 // Planes of the eras split into several segments (see HistArgs): prefix over bins of the
@@ -88,7 +96,9 @@ struct FinalizeArgs {
     unsigned long long* acc_g;
     const int32_t* acc_era;  // [n_acc] era of each slot
     int32_t n_acc;
-    int32_t U, K, nb;
+    int32_t U, K, nb;        // plane strides and the depth's feature count
+    int32_t acc_U, acc_K;    // node and feature strides of acc_cnt / acc_g
+    const int32_t* sh_era;   // [E] fixed-point gradient scale exponent of each era
     const Frontier* st;
     int32_t depth;
     uint16_t* out_cnt;
@@ -116,6 +126,16 @@ __host__ __device__ inline int64_t plane_elems(int64_t E, int64_t U, int64_t K, 
 }
 
 constexpr int kScoreChunkEras = 24;  // eras whose plane cells a scorer chunk stages at once
+
+// Every candidate of one depth, [U][K][T] in the reference's visiting order (subset feature,
+// then threshold index), for the decision step's sequential pick: score (-inf for a candidate
+// the reference skips), left count, left grad; band is that step's scratch ([U][K * T] indices).
+struct SeqCands {
+    float* score;
+    int32_t* lt;
+    float* lg;
+    int32_t* band;
+};
 
 struct ScoreArgs {
     const uint16_t* cnt;     // prefix counts [E][U][K][nb-1]
@@ -146,6 +166,7 @@ struct ScoreArgs {
     int32_t wpt;             // wavefront winners per tile (ceil(fts * T / 64))
     int32_t rt;              // size of the 1/n table (equal era weights)
     int32_t staged;          // T >= 64: 1 = LDS-staged two-phase kernel, 0 = wide kernel
+    SeqCands seq;            // every candidate, for the sequential pick
 };
 
 // Launch shape of the scorer for K features and T thresholds (shared by the context's
@@ -164,7 +185,18 @@ hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_
                         int32_t nb,
                         int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                         int32_t* thr_tab, hipStream_t s);
-hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, int32_t max_nodes, const NodeTotal* ntot,
+// The candidates of the depth the decision step picks from: the scorer's wavefront winners
+// (cand_w [U][W]) and every candidate in visiting order (seq, K features x T thresholds of the
+// ids feats / thresholds thr_tab, or 0..T-1 when thr_tab is null).
+struct DecideCands {
+    const pb_candidate* cand_w;
+    int32_t W;
+    SeqCands seq;
+    int32_t K, T;
+    const int32_t* feats;
+    const int32_t* thr_tab;
+};
+hipError_t launch_decide(const DecideCands& dc, int32_t max_nodes, const NodeTotal* ntot,
                          Frontier* st, int32_t depth, int32_t msl, double lambda_l2,
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
@@ -174,8 +206,11 @@ hipError_t launch_select_subsets(const pb_round_header* prev, int32_t D, int32_t
 hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s);
+// Also writes win_sum [ceil(rows_padded / kGradWinRows)] (sum of |grad| per window) and
+// sh_era [E] (era_grad_scale of each era, eras at era_off [E+1]).
 hipError_t launch_round_begin(const float* preds, const float* y, float* grad, uint16_t* nid,
                               uint16_t* tnode, int64_t N, int64_t rows_padded, int32_t root_active,
+                              const int32_t* era_off, int32_t E, float* win_sum, int32_t* sh_era,
                               Frontier* st, int32_t* cur_ids, hipStream_t s);
 hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s);
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,

@@ -4,7 +4,8 @@
 // (booster.py:131-169, frontier_cuda.cu:193-233). predict_pack_cuda returns
 // tree_weight * sum of the pack's leaf values (frontier_cuda.cu:925-986); the CPU path of
 // PackBoost.predict accumulates pred += weight * value tree by tree (booster.py:709-712).
-// Malformed child indices end the walk with 0, like the reference's guards.
+// Malformed child indices or split features end the walk with 0 (leaf index -1), like the
+// reference's guards; tree spans are clamped to the node arrays.
 //
 // `sequential` selects the CPU path's order: out = sum_t (weight * value_t), one float32
 // rounding per product and per add, trees in order.
@@ -49,15 +50,18 @@ __global__ __launch_bounds__(kBlock) void predict_pack_kernel(
     const int32_t* __restrict__ feature, const int32_t* __restrict__ threshold,
     const int32_t* __restrict__ left_abs, const int32_t* __restrict__ right_abs,
     const float* __restrict__ value, const uint8_t* __restrict__ is_leaf,
-    const int32_t* __restrict__ offsets, int32_t B, float tree_weight, int32_t sequential,
-    float* __restrict__ out, int32_t* __restrict__ leaf) {
+    const int32_t* __restrict__ offsets, int32_t B, int32_t total_nodes, float tree_weight,
+    int32_t sequential, float* __restrict__ out, int32_t* __restrict__ leaf) {
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x; r < N; r += stride) {
         float s = 0.0f;
         for (int t = 0; t < B; ++t) {
             int32_t lf;
+            // a tree's span, clamped to the node arrays (offsets come from the caller)
+            const int32_t lo = min(max(offsets[t], 0), total_nodes);
+            const int32_t hi = min(max(offsets[t + 1], lo), total_nodes);
             const float v = walk(bins, ld, r, feature, threshold, left_abs, right_abs, value,
-                                 is_leaf, offsets[t], offsets[t + 1], F, &lf);
+                                 is_leaf, lo, hi, F, &lf);
             s = sequential ? (s + tree_weight * v) : (s + v);
             if (leaf) leaf[(int64_t)t * N + r] = lf;
         }
@@ -139,10 +143,9 @@ hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32
                                const int32_t* offsets, int32_t B, int32_t total_nodes,
                                float tree_weight, int32_t sequential, float* out, int32_t* leaf,
                                hipStream_t s) {
-    (void)total_nodes;
     hipLaunchKernelGGL(predict_pack_kernel, dim3(grid_rows(N)), dim3(kBlock), 0, s, bins, N, ld,
                        F, feature, threshold, left_abs, right_abs, value, is_leaf, offsets, B,
-                       tree_weight, sequential, out, leaf);
+                       total_nodes, tree_weight, sequential, out, leaf);
     return hipGetLastError();
 }
 

@@ -16,9 +16,11 @@
 //
 // One lane owns one (node, feature, threshold) candidate and walks the eras; the lanes of a
 // wavefront all belong to one node (the candidate space of a node is padded to 64), so
-// a 6-step xor-shuffle argmax yields the wavefront's winner. Ties on the exact score are
-// broken like the reference: larger left count, then larger feature id, then larger
-// threshold (frontier_cpu.cpp:415-426).
+// a 6-step xor-shuffle argmax yields the wavefront's winner under a strict order (higher
+// score; on an exactly equal score the larger left count, then larger feature id, then larger
+// threshold). Every candidate is also kept in visiting order, and the decision step replays
+// the reference's sequential pick with its 1e-12 tie window (frontier_cpu.cpp:415-426) over the
+// candidates near the top score (sequential_pick).
 #include <algorithm>
 
 #include <type_traits>
@@ -91,6 +93,34 @@ __device__ __forceinline__ Cand load_cand(const pb_candidate* src) {
     c.thr = src->threshold;
     c.valid = src->valid;
     return c;
+}
+
+// Width of the first tie band of the sequential pick (64 x 1e-12, widened past the float
+// rounding of |s - best| <= 1e-12f).
+constexpr double kTieBand0 = 64.0e-12 * (1.0 + 1.0e-6);
+
+// After the wavefront argmax (`win`, held by every lane): how many of the wavefront's valid
+// candidates (own score `mine`, -inf if invalid) score within kTieBand0 of its winner. Stored
+// with the winner, it bounds the node's tie band in the decision step: when the node's band
+// can hold only its best candidate, the sequential pick is the strict argmax.
+__device__ __forceinline__ int wave_band_count(const Cand& win, float mine) {
+    const bool near = win.valid && (double)mine >= (double)win.score - kTieBand0;
+    return __popcll(__ballot(near));
+}
+
+__device__ __forceinline__ void store_winner(pb_candidate* dst, const Cand& c, int band) {
+    store_cand(dst, c);
+    dst->reserved[0] = band;
+}
+
+// Every candidate of the depth in the reference's visiting order (per node: subset feature k,
+// then threshold index t), for the sequential pick of the decision step: its score (-inf when
+// the reference would skip it: below min_samples_leaf, no rows, or NaN), left count and left
+// grad.
+__device__ __forceinline__ void store_seq(const ScoreArgs& a, int64_t i, const Cand& c) {
+    a.seq.score[i] = c.valid ? c.score : -INFINITY;
+    a.seq.lt[i] = c.lt;
+    a.seq.lg[i] = c.lg;
 }
 
 // Scorer. One workgroup owns one (node, tile of `fts` features) = fts * T candidates and walks
@@ -314,6 +344,7 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
         // a node without rows never splits (the reference skips it, frontier_cpu.cpp:191-193)
         c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
         if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
+        store_seq(a, ((int64_t)u * a.K + k) * T + t, c);
         if (tile == 0 && tid == 0) {
             a.ntot[u].count = tc;
             a.ntot[u].grad = tg;
@@ -321,14 +352,16 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     }
     const int wave = tid / kWave;
     if (wave < a.wpt) {
+        const float mine = c.valid ? c.score : -INFINITY;
 #pragma unroll
         for (int m = 1; m < kWave; m <<= 1) {
             const Cand o = shfl_xor_cand(c, m);
             take_if(better(o, c), o, c);
         }
+        const int band = wave_band_count(c, mine);
         if ((tid & (kWave - 1)) == 0) {
             const int W = a.ntiles * a.wpt;
-            store_cand(a.cand_w + (int64_t)u * W + tile * a.wpt + wave, c);
+            store_winner(a.cand_w + (int64_t)u * W + tile * a.wpt + wave, c, band);
         }
     }
 }
@@ -475,6 +508,7 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
         c.score = score;
         c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
         if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
+        store_seq(a, ((int64_t)u * a.K + k) * T + t, c);
         if (k == 0 && tid == 0) {
             a.ntot[u].count = tc;
             a.ntot[u].grad = tg;
@@ -482,14 +516,16 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
     }
     const int wave = tid / kWave;
     if (wave < a.wpt) {
+        const float mine = c.valid ? c.score : -INFINITY;
 #pragma unroll
         for (int m = 1; m < kWave; m <<= 1) {
             const Cand o = shfl_xor_cand(c, m);
             take_if(better(o, c), o, c);
         }
+        const int band = wave_band_count(c, mine);
         if ((tid & (kWave - 1)) == 0) {
             const int W = a.ntiles * a.wpt;
-            store_cand(a.cand_w + (int64_t)u * W + k * a.wpt + wave, c);
+            store_winner(a.cand_w + (int64_t)u * W + k * a.wpt + wave, c, band);
         }
     }
 }
@@ -782,17 +818,20 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
             // a node without rows never splits (the reference skips it, frontier_cpu.cpp:191-193)
             c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
             if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
+        store_seq(a, ((int64_t)u * a.K + k) * T + t, c);
             if (tile == 0 && tid == 0) {
                 a.ntot[u].count = tc;
                 a.ntot[u].grad = tg;
             }
         }
+        const float mine = c.valid ? c.score : -INFINITY;
 #pragma unroll
         for (int m = 1; m < kWave; m <<= 1) {
             const Cand o = shfl_xor_cand(c, m);
             take_if(better(o, c), o, c);
         }
-        if (tid == 0) store_cand(a.cand_w + (int64_t)u * a.ntiles + tile, c);
+        const int band = wave_band_count(c, mine);
+        if (tid == 0) store_winner(a.cand_w + (int64_t)u * a.ntiles + tile, c, band);
     }
 }
 
@@ -925,22 +964,104 @@ __device__ int block_exclusive_scan(int v, int* out_excl, int* s_wave) {
 //  3. exclusive scans over the frontier order give the children's TreeBuilder ids
 //     (tree_size + 2 * splits before) and their slots in the next frontier (children with
 //     >= 2 * min_samples_leaf rows, left before right).
+// The reference scans a node's candidates in order (subset feature, then threshold) and
+// replaces its best when a candidate scores higher, or scores within 1e-12 (a float difference)
+// and has more left rows, then a larger feature id, then a larger threshold
+// (frontier_cpu.cpp:415-426). That relation is not transitive, so the scan order matters when
+// scores lie within 1e-12 of each other. One wavefront replays it exactly from `best`, the
+// node's candidate of the highest score M under the strict order of `better`:
+//  * the first candidate i* of score M is always taken (every earlier score is below M), so
+//    the scan's result is the scan from i* with best = c(i*);
+//  * each later replacement lowers the best score by at most 1e-12, so a scan whose band
+//    [M - w, M] holds fewer than w / 1e-12 candidates never takes one outside the band.
+// The band doubles from w = 64e-12 until that holds, its indices are compacted in order into
+// `band`, and lane 0 scans them. Scores above about 1e-5 in magnitude have float spacing beyond
+// 1e-12, so there the band holds only exact ties and the pick is the strict order's.
+__device__ void sequential_pick(const DecideCands& dc, int u, Cand& best) {
+    const int lane = (int)(threadIdx.x & (kWave - 1));
+    if (!best.valid) return;  // wave-uniform
+    const int64_t n = (int64_t)dc.K * dc.T;
+    const float* sc = dc.seq.score + (int64_t)u * n;
+    const double M = (double)best.score;
+    double w = 0.0;
+    int64_t count = 0;
+    for (int k = 6;; ++k) {
+        w = ldexp(kTieBand0, k - 6);  // 2^k * 1e-12, widened as kTieBand0
+        int64_t c = 0;
+        for (int64_t i = lane; i < n; i += kWave) c += ((double)sc[i] >= M - w) ? 1 : 0;
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) c += __shfl_xor(c, m);
+        count = c;
+        if (count < (int64_t(1) << k) || (int64_t(1) << k) > n) break;
+    }
+    int32_t* band = dc.seq.band + (int64_t)u * n;
+    int64_t pos = 0;
+    for (int64_t b0 = 0; b0 < n; b0 += kWave) {
+        const int64_t i = b0 + lane;
+        const bool in = i < n && (double)sc[i] >= M - w;
+        const unsigned long long m = __ballot(in);
+        if (in) band[pos + __popcll(m & ((1ull << lane) - 1ull))] = (int32_t)i;
+        pos += __popcll(m);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) {
+        Cand cur = best;
+        bool started = false;
+        for (int64_t j = 0; j < pos; ++j) {
+            const int32_t i = band[j];
+            const float sv = sc[i];
+            const int kk = i / dc.T;
+            const int t = i - kk * dc.T;
+            Cand c;
+            c.score = sv;
+            c.lt = dc.seq.lt[(int64_t)u * n + i];
+            c.lg = dc.seq.lg[(int64_t)u * n + i];
+            c.f = dc.feats[kk];
+            c.thr = dc.thr_tab ? dc.thr_tab[kk * dc.T + t] : t;
+            c.valid = 1;
+            const bool first = !started && ((double)sv == M);
+            const bool s_gt = sv > cur.score;
+            const bool near = fabsf(sv - cur.score) <= 1e-12f;
+            const bool tie_win = (c.lt > cur.lt) | ((c.lt == cur.lt) & ((c.f > cur.f) | ((c.f == cur.f) & (c.thr > cur.thr))));
+            const bool take = first | (started & (s_gt | (near & tie_win)));
+            take_if(take, c, cur);
+            started = started | first;
+        }
+        best = cur;
+    }
+}
+
+// Upper bound on the node's candidates within kTieBand0 of its best score M: the wavefront
+// band counts of the winners whose own score is that close (a candidate in the node's band is
+// in its wavefront's band, since that wavefront's winner scores between it and M). Summed by
+// the calling threads over winners w0, w0 + step, ...
+__device__ __forceinline__ int band_bound_part(const DecideCands& dc, int u, int W, int w0, int step,
+                                               const Cand& best) {
+    int n = 0;
+    if (!best.valid) return 0;
+    for (int w = w0; w < W; w += step) {
+        const pb_candidate* r = dc.cand_w + (int64_t)u * W + w;
+        if (r->valid && (double)r->score >= (double)best.score - kTieBand0) n += r->reserved[0];
+    }
+    return n;
+}
+
 // Phase 1 of the decision step when the candidate set is wide (many wavefront winners per node,
 // e.g. 254 thresholds x 500 features): one workgroup per node slot reduces that node's W winners
-// under the same strict order (`better`) as decide_kernel's own phase 1, so the winner is the
-// same whatever the reduction order.
-__global__ __launch_bounds__(kBlock) void node_best_kernel(const pb_candidate* cand_w, int32_t W,
-                                                        const Frontier* st, int32_t depth,
-                                                        pb_candidate* node_best) {
+// under the strict order of `better` (so the winner is the same whatever the reduction order),
+// then its first wavefront replays the reference's sequential pick.
+__global__ __launch_bounds__(kBlock) void node_best_kernel(DecideCands dc, const Frontier* st,
+                                                        int32_t depth, pb_candidate* node_best) {
     __shared__ Cand s_best[kBlock / kWave];
     const int u = blockIdx.x;
     if (u >= st->u_active[depth]) return;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
+    const int W = dc.W;
     Cand best;
     best.valid = 0; best.score = 0.0f; best.lt = 0; best.lg = 0.0f; best.f = -1; best.thr = -1;
     for (int w = threadIdx.x; w < W; w += kBlock) {
-        const Cand c = load_cand(cand_w + (int64_t)u * W + w);
+        const Cand c = load_cand(dc.cand_w + (int64_t)u * W + w);
         take_if(better(c, best), c, best);
     }
 #pragma unroll
@@ -948,16 +1069,26 @@ __global__ __launch_bounds__(kBlock) void node_best_kernel(const pb_candidate* c
         const Cand o = shfl_xor_cand(best, m);
         take_if(better(o, best), o, best);
     }
+    __shared__ int s_band[kBlock / kWave];
     if (lane == 0) s_best[wave] = best;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int i = 1; i < kBlock / kWave; ++i) take_if(better(s_best[i], best), s_best[i], best);
-        store_cand(node_best + u, best);
+    best = s_best[0];
+    for (int i = 1; i < kBlock / kWave; ++i) take_if(better(s_best[i], best), s_best[i], best);
+    int band = band_bound_part(dc, u, W, threadIdx.x, kBlock, best);
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) band += __shfl_xor(band, m);
+    if (lane == 0) s_band[wave] = band;
+    __syncthreads();
+    if (wave == 0) {
+        int nb = 0;
+        for (int i = 0; i < kBlock / kWave; ++i) nb += s_band[i];
+        if (nb > 1) sequential_pick(dc, u, best);
+        if (lane == 0) store_cand(node_best + u, best);
     }
 }
 
 // W == 0: node_best already holds each node's winner (node_best_kernel ran first).
-__global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand_w, int32_t W,
+__global__ __launch_bounds__(kBlock) void decide_kernel(DecideCands dc, int32_t W,
                                                     const NodeTotal* ntot, Frontier* st,
                                                     int32_t depth, int32_t msl, double lambda_l2,
                                                     const int32_t* cur_ids, int32_t* next_ids,
@@ -975,7 +1106,7 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
         Cand best;
         best.valid = 0; best.score = 0.0f; best.lt = 0; best.lg = 0.0f; best.f = -1; best.thr = -1;
         for (int w = lane; w < W; w += kWave) {
-            const Cand c = load_cand(cand_w + (int64_t)u * W + w);
+            const Cand c = load_cand(dc.cand_w + (int64_t)u * W + w);
             take_if(better(c, best), c, best);
         }
 #pragma unroll
@@ -983,6 +1114,10 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(const pb_candidate* cand
             const Cand o = shfl_xor_cand(best, m);
             take_if(better(o, best), o, best);
         }
+        int band = band_bound_part(dc, u, W, lane, kWave, best);
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) band += __shfl_xor(band, m);
+        if (band > 1) sequential_pick(dc, u, best);
         if (lane == 0) store_cand(node_best + u, best);
     }
     if (threadIdx.x == 0) {
@@ -1142,20 +1277,20 @@ hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_
     return hipGetLastError();
 }
 
-hipError_t launch_decide(const pb_candidate* cand_w, int32_t W, int32_t max_nodes, const NodeTotal* ntot,
+hipError_t launch_decide(const DecideCands& dc, int32_t max_nodes, const NodeTotal* ntot,
                          Frontier* st, int32_t depth, int32_t msl, double lambda_l2,
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
                          hipStream_t s) {
     // wide candidate sets: the per-node reductions in parallel, one workgroup per node slot
     // (one workgroup walking max_nodes x W winners took ~0.1 ms per depth at 128 x 2000)
-    int32_t w_decide = W;
-    if ((int64_t)max_nodes * W >= (int64_t)32 * 1024) {
-        hipLaunchKernelGGL(node_best_kernel, dim3(max_nodes), dim3(kBlock), 0, s, cand_w, W, st, depth,
+    int32_t w_decide = dc.W;
+    if ((int64_t)max_nodes * dc.W >= (int64_t)32 * 1024) {
+        hipLaunchKernelGGL(node_best_kernel, dim3(max_nodes), dim3(kBlock), 0, s, dc, st, depth,
                            node_best);
         w_decide = 0;
     }
-    hipLaunchKernelGGL(decide_kernel, dim3(1), dim3(kBlock), 0, s, cand_w, w_decide, ntot, st, depth,
+    hipLaunchKernelGGL(decide_kernel, dim3(1), dim3(kBlock), 0, s, dc, w_decide, ntot, st, depth,
                        msl, lambda_l2, cur_ids, next_ids, rules, dec, values, node_best);
     return hipGetLastError();
 }

@@ -66,6 +66,8 @@ class RoundLog:
     decisions: np.ndarray     # DECISION_DTYPE [2^D - 1], depth d at offset 2^d - 1
     root_grad: float          # float32 sum of grad over all rows (root value numerator)
     depths_drawn: int         # feature subsets the reference would have drawn
+    phase_ms: np.ndarray | None = None  # float64 [4][D] GPU ms of hist / score / decide /
+                                        # partition per depth (rounds(phase_times=True) only)
 
 
 class _DrawStream:
@@ -335,13 +337,25 @@ class DeviceFit:
         return RoundLog(u_active=u[: self.D + 1].copy(), tree_size=int(hdr["tree_size"]),
                         decisions=dec, root_grad=float(dec[0]["node_grad"]), depths_drawn=drawn)
 
+    def read_phase_ms(self) -> tuple[np.ndarray, np.ndarray]:
+        """GPU ms and launch counts [4][D] (hist, score, decide, partition per depth) of the
+        rounds timed since the last read (pb_profile_read; waits for them)."""
+        ms = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.float64)
+        n = np.zeros(4 * _hip.PB_MAX_DEPTH, dtype=np.int64)
+        _hip.check(self.lib.pb_profile_read(self.ctx, ms.ctypes.data, n.ctypes.data), "pb_profile_read")
+        return ms.reshape(4, -1)[:, : self.D], n.reshape(4, -1)[:, : self.D]
+
     def rounds(self, rng: torch.Generator, num_rounds: int, *, profile_every: int = 0,
-               profile_mode: int = 2):
+               profile_mode: int = 2, phase_times: bool = False):
         """Runs `num_rounds` rounds with the host one round ahead of the GPU.
 
         profile_every > 0 turns the library's phase timing (pb_profile_enable, mode
         `profile_mode`) on for every profile_every-th round only, so that the events' queue
         barriers touch few rounds.
+
+        phase_times: every round timed phase by phase, each read back with its log
+        (RoundLog.phase_ms); rounds then run one at a time (no round is enqueued ahead), so
+        the times are the round's own.
 
         Yields (RoundLog, preds_after, ready) per round in order. `preds_after` holds the
         predictions after that round until the consumer resumes the generator (the GPU may
@@ -372,11 +386,15 @@ class DeviceFit:
         draws = _DrawStream(rng, self.F, self.K)
         D = self.D
         p = 0
+        if phase_times:
+            profile_every, profile_mode = 1, 1
         set_profile(0)
         self.enqueue_grow_window(draws.window(0, 2 * D), 0, None)
         for r in range(num_rounds):
             slot = r & 1
-            ahead = r + 1 < num_rounds
+            if phase_times and r > 0:  # this round's subsets start where the last round's ended
+                self.enqueue_grow_window(draws.window(p, 2 * D), slot, None)
+            ahead = r + 1 < num_rounds and not phase_times
             if ahead:
                 with torch.cuda.stream(self.stream):
                     self.preds_snap.copy_(self.preds)
@@ -384,13 +402,15 @@ class DeviceFit:
                 set_profile(r + 1)
                 self.enqueue_grow_window(draws.window(p, 2 * D), slot ^ 1, slot)
             log = self.read_slot(slot)
+            if phase_times:
+                log.phase_ms = self.read_phase_ms()[0]
             p += log.depths_drawn
             draws.release(p)
             if ahead:
                 yield log, self.preds_snap, ready
             else:
                 draws.rewind_to(p)
-                if profile_every > 0:
+                if profile_every > 0 and r + 1 == num_rounds:
                     _hip.check(self.lib.pb_profile_enable(self.ctx, 0), "pb_profile_enable")
                 yield log, self.preds, now()
 
@@ -481,16 +501,28 @@ def tree_arrays_from_log(log: RoundLog, cfg: PackBoostConfig, num_rows: int) -> 
 
 def depth_log_from_round(log: RoundLog, d: int, cfg: PackBoostConfig, k: int,
                          histogram_mode: str) -> dict:
-    """Per-depth instrumentation in the reference's key set (booster.py:220-270, 565-579)."""
+    """Per-depth instrumentation in the reference's key set (booster.py:220-270, 565-579).
+
+    The *_ms fields are GPU times from the library's phase events when the round was timed
+    (log.phase_ms): hist_ms the histogram kernel, which also forms the prefix scan (so scan_ms
+    stays 0.0), score_ms the DES scorer plus the decision step, partition_ms the partition.
+    Untimed rounds report 0.0, as timing costs the pipelined loop its overlap.
+    One frontier serves the pack's B identical trees: the reference's shard dedup collapses
+    B - 1 of every B shards (nodes_collapsed) and processes the rest."""
     ua = int(log.u_active[d])
     recs = log.decisions[(1 << d) - 1: (1 << d) - 1 + ua]
     rows = int(recs["node_count"].astype(np.int64).sum()) if ua else 0
     B = int(cfg.pack_size)
     rebuild = histogram_mode == "rebuild"
+    ph_hist = ph_score = ph_part = 0.0
+    if log.phase_ms is not None and ua:
+        ph_hist = float(log.phase_ms[0, d])
+        ph_score = float(log.phase_ms[1, d] + log.phase_ms[2, d])
+        ph_part = float(log.phase_ms[3, d])
     out = {
         "nodes_processed": ua, "nodes_skipped": 0, "rows_total": rows,
         "feature_blocks": 1 if ua else 0, "bincount_calls": 2 if ua else 0,
-        "hist_ms": 0.0, "scan_ms": 0.0, "score_ms": 0.0, "partition_ms": 0.0,
+        "hist_ms": ph_hist, "scan_ms": 0.0, "score_ms": ph_score, "partition_ms": ph_part,
         "nodes_subtract_ok": 0 if rebuild else ua, "nodes_rebuild": ua if rebuild else 0,
         "nodes_subtract_fallback": 0, "nodes_collapsed": (B - 1) * ua,
         "feature_block_size": k, "depth": d, "feature_subset_size": k, "pack_size": B,

@@ -234,3 +234,88 @@ def split_params(hip, *, lambda_l2=1e-6, lambda_dro=0.0, direction_weight=0.0, e
     p.min_samples_leaf, p.k_cuts = int(msl), int(k_cuts)
     p.cut_selection = 1 if cut_selection == "mass" else 0
     return p
+
+
+def node_sum_bounds(arrs: dict, bins: np.ndarray, grad: np.ndarray, lambda_l2: float,
+                    leaf_index) -> np.ndarray:
+    """Per node of one tree: the |grad| mass of the rows its value is formed from (its parent's
+    rows: a child's value is -G/(n + lambda) with G a left sum or a parent total minus a left
+    sum, booster.py:545-546; the root's own rows) over (rows + lambda_l2). Grad sums within 1e-5
+    of their mass move the value by at most 1e-5 times this."""
+    n = len(arrs["feature"])
+    leaf = leaf_index(arrs, bins)
+    m = np.bincount(leaf, weights=np.abs(grad.astype(np.float64)), minlength=n)
+    c = np.bincount(leaf, minlength=n).astype(np.float64)
+    parent = np.full(n, -1, np.int64)
+    for node in range(n - 1, -1, -1):
+        if not arrs["is_leaf"][node]:
+            for ch in (arrs["left"][node], arrs["right"][node]):
+                m[node] += m[ch]
+                c[node] += c[ch]
+                parent[ch] = node
+    pm = np.where(parent >= 0, m[np.maximum(parent, 0)], m)
+    return pm / (c + lambda_l2)
+
+
+def compare_fit_rounds(oracle_mod, got_rounds, ref, trace, bins, kw) -> int:
+    """Whole-fit parity of the device trees against the oracle's, round by round:
+      * structure (feature, threshold, children, leaf flags) identical; at the first node that
+        differs the device's split must be a near-tie (the oracle's score of it on the same
+        rows within 1e-6, relative, of the oracle's best) and the comparison stops there, as the
+        trajectories part;
+      * node values within 1e-5 (relative) of the oracle's, plus twice 1e-5 of the |grad| mass
+        the value is formed from over its rows (node_sum_bounds): the values are
+        -G/(n + lambda) of grad sums that agree within 1e-5 of their mass, and a right child's
+        G is a float32 difference of two such sums (booster.py:545-546).
+    Returns the number of rounds compared whole."""
+    lam = float(kw.get("lambda_l2", 1e-6))
+    matched = 0
+    for r, (a, b) in enumerate(zip(got_rounds, ref.rounds)):
+        same = all(np.array_equal(np.asarray(a[k]), np.asarray(b[k]))
+                   for k in ("feature", "threshold", "left", "right", "is_leaf"))
+        depth_traces = [t for t in trace if t["round"] == r]
+        if not same:
+            assert_near_tie(oracle_mod, bins, a, b, depth_traces, kw)
+            break
+        va, vb = np.asarray(a["value"], np.float64), np.asarray(b["value"], np.float64)
+        if depth_traces:
+            bound = node_sum_bounds(b, bins, depth_traces[0]["grad"], lam, oracle_mod.leaf_index)
+            err = np.abs(va - vb)
+            bar = 1e-5 * (np.abs(vb) + 2.0 * bound) + 1e-7
+            worst = int(np.argmax(err / bar))
+            print(f"[fit parity] round {r}: worst value error {err[worst]:.3g} at node {worst} "
+                  f"(bar {bar[worst]:.3g}, |value| {abs(vb[worst]):.3g}, mass bound {bound[worst]:.3g})",
+                  flush=True)
+            assert np.all(err <= bar), (f"round {r}: node {worst} value {va[worst]!r} vs {vb[worst]!r} "
+                                        f"(bar {bar[worst]:.3g})")
+        else:
+            np.testing.assert_allclose(va, vb, rtol=1e-5, atol=1e-5, err_msg=f"round {r} value")
+        matched += 1
+    return matched
+
+
+def assert_near_tie(oracle_mod, bins, got, want, depth_traces, kw):
+    """The first node (depth by depth, in frontier order) where the device tree differs from
+    the oracle's: the device's split must score, by the oracle on that node's rows, within 1e-6
+    (relative) of the oracle's best."""
+    for t in depth_traces:
+        res = t["result"]
+        for m, nid in enumerate(t["node_ids"]):
+            fw, tw = int(want["feature"][nid]), int(want["threshold"][nid])
+            fg, tg = int(got["feature"][nid]), int(got["threshold"][nid])
+            if (fw, tw) == (fg, tg):
+                continue
+            assert fg >= 0 and fw >= 0, f"node {nid}: split vs no split"
+            opts = {k: kw[k] for k in ("k_cuts", "cut_selection", "lambda_l2", "lambda_dro",
+                                       "direction_weight", "era_alpha") if k in kw}
+            cands = oracle_mod.split_batch(bins, t["grad"], [t["nodes_era_rows"][m]], t["feats"],
+                                           kw["max_bins"], want_cands=True,
+                                           min_samples_leaf=kw.get("min_samples_leaf", 20), **opts).cands
+            k = int(np.nonzero(t["feats"] == fg)[0][0])
+            s_dev = float(cands[0][0, k, tg])
+            best = float(res.score[m])
+            assert abs(s_dev - best) <= 1e-6 * max(1.0, abs(best)), \
+                f"node {nid}: device split ({fg}, {tg}) scores {s_dev} vs best {best}"
+            print(f"[fit parity] near-tie at node {nid}: {s_dev} vs {best}", flush=True)
+            return
+    raise AssertionError("trees differ outside the traced depths")

@@ -237,3 +237,83 @@ def test_wide_scorer_matches_staged(hip, oracle_mod, monkeypatch, case, k_cuts):
     for field in ("score", "left_grad"):
         np.testing.assert_array_equal(c0[field].view(np.uint32), c1[field].view(np.uint32))
     assert d0.tobytes() == d1.tobytes()
+
+
+def _exact_prefix(p, feats, U):
+    """float64 prefix grad sums and prefix |grad| masses [E][U][K][nb] (bin nb-1: the era total)."""
+    nid = p["nid"].astype(np.int64)
+    act = nid < U
+    E, nb, K = p["E"], p["nb"], len(feats)
+    g = p["grad"].astype(np.float64)[act]
+    e, u = p["era"][act], nid[act]
+    s = np.zeros((E, U, K, nb))
+    m = np.zeros((E, U, K, nb))
+    for k, f in enumerate(feats):
+        b = p["bins"][act, f].astype(np.int64)
+        np.add.at(s, (e, u, k, b), g)
+        np.add.at(m, (e, u, k, b), np.abs(g))
+    return np.cumsum(s, axis=3), np.cumsum(m, axis=3)
+
+
+HEAVY = [
+    # seed, N, F, E, nb, U, K: a few rows with |grad| 1e4..1e6 among N(0, 1) gradients
+    (31, 20000, 16, 8, 5, 4, 16),
+    (32, 30000, 12, 6, 128, 8, 12),
+    (33, 24000, 10, 4, 16, 2, 10),
+    (34, 70000, 8, 2, 16, 3, 8),  # eras of 35000 rows: summed over segments
+]
+HEAVY_LAYOUT = [(c, "u8") for c in HEAVY] + [(c, "nibble") for c in HEAVY if c[4] <= 16]
+
+
+@pytest.mark.parametrize("case,layout", HEAVY_LAYOUT, ids=[f"seed{c[0]}-{lay}" for c, lay in HEAVY_LAYOUT])
+def test_hist_heavy_tailed_grads(hip, oracle_mod, case, layout):
+    """Grad planes when a few rows' |grad| exceed the rest by up to 10^6: every cell within
+    1e-5 of its own |grad| mass (no floor), against exact float64 sums; counts bit-exact
+    against the oracle. The fixed-point scale is set per era, so only the eras that hold an
+    outlier get a coarser step."""
+    seed, N, F, E, nb, U, K = case
+    print(f"[heavy tails] seed={seed} N={N} E={E} nb={nb} U={U} {layout}", flush=True)
+    p = make_problem(seed, N, F, E, nb, U)
+    rng = np.random.default_rng(seed + 7)
+    idx = rng.choice(N, 6, replace=False)
+    p["grad"][idx] = (rng.choice([-1.0, 1.0], 6) * np.array([1e4, 3e4, 1e5, 3e5, 1e6, 1e6])).astype(np.float32)
+    feats = rng.permutation(F)[:K].astype(np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, want_planes=True,
+                                 min_samples_leaf=1)
+    exact, mass = _exact_prefix(p, feats, U)
+    g = GpuDepth(hip, p, K, msl=1, layout=layout)
+    try:
+        g.hist(feats)
+        cnt, gp = g.planes()
+        np.testing.assert_array_equal(cnt, ref.planes[0])
+        err = np.abs(gp.astype(np.float64) - exact)
+        worst = np.max(np.where(mass > 0, err / np.where(mass > 0, mass, 1.0), 0.0))
+        assert np.all(err <= 1e-5 * mass), f"worst relative error {worst:.3g}"
+        # the reference's float32 row-order sums meet the same bar on these inputs
+        assert np.all(np.abs(ref.planes[1].astype(np.float64) - exact) <= 1e-5 * mass)
+    finally:
+        g.close()
+
+
+def test_hist_max_nodes_above_frontier_bound(hip, oracle_mod):
+    """pb_hist_build with max_nodes above pb_max_nodes (the header allows any bound at least
+    that large) on eras split into segments gives the same planes as the pb_max_nodes call:
+    the segment sums are strided by the context's own allocation, not by max_nodes."""
+    import torch
+
+    p = make_problem(51, 70000, 6, 2, 7, 3, inactive_frac=0.05)
+    feats = np.arange(6, dtype=np.int32)
+    g = GpuDepth(hip, p, 6, msl=1)
+    try:
+        g.hist(feats)
+        cnt0, gp0 = g.planes()
+        g.max_nodes += 8
+        plane = int(g.lib.pb_hist_plane_elems(g.ctx, g.max_nodes))
+        g.cnt = torch.zeros(plane, dtype=torch.int32, device="cuda")
+        g.g = torch.zeros(plane, dtype=torch.float32, device="cuda")
+        g.hist(feats)
+        cnt1, gp1 = g.planes()
+        np.testing.assert_array_equal(cnt1, cnt0)
+        np.testing.assert_array_equal(gp1.view(np.uint32), gp0.view(np.uint32))
+    finally:
+        g.close()
