@@ -237,7 +237,7 @@ def split_params(hip, *, lambda_l2=1e-6, lambda_dro=0.0, direction_weight=0.0, e
 
 
 def node_sum_bounds(arrs: dict, bins: np.ndarray, grad: np.ndarray, lambda_l2: float,
-                    leaf_index) -> np.ndarray:
+                    leaf_index, return_leaf: bool = False):
     """Per node of one tree: the |grad| mass of the rows its value is formed from (its parent's
     rows: a child's value is -G/(n + lambda) with G a left sum or a parent total minus a left
     sum, booster.py:545-546; the root's own rows) over (rows + lambda_l2). Grad sums within 1e-5
@@ -254,7 +254,8 @@ def node_sum_bounds(arrs: dict, bins: np.ndarray, grad: np.ndarray, lambda_l2: f
                 c[node] += c[ch]
                 parent[ch] = node
     pm = np.where(parent >= 0, m[np.maximum(parent, 0)], m)
-    return pm / (c + lambda_l2)
+    bound = pm / (c + lambda_l2)
+    return (bound, leaf) if return_leaf else bound
 
 
 def compare_fit_rounds(oracle_mod, got_rounds, ref, trace, bins, kw) -> int:
@@ -267,8 +268,13 @@ def compare_fit_rounds(oracle_mod, got_rounds, ref, trace, bins, kw) -> int:
         the value is formed from over its rows (node_sum_bounds): the values are
         -G/(n + lambda) of grad sums that agree within 1e-5 of their mass, and a right child's
         G is a float32 difference of two such sums (booster.py:545-546).
-    Returns the number of rounds compared whole."""
+    Returns the number of rounds compared whole and, per row, the bound those rounds' value
+    bars put on the predictions: lr * B * the bar of the row's leaf, summed over the rounds
+    (pack aggregation, booster.py:581-599); callers add the float32 rounding of the adds."""
     lam = float(kw.get("lambda_l2", 1e-6))
+    lr = float(kw.get("learning_rate", 0.1))
+    B = int(kw.get("pack_size", 8))
+    pred_bar = np.zeros(bins.shape[0])
     matched = 0
     for r, (a, b) in enumerate(zip(got_rounds, ref.rounds)):
         same = all(np.array_equal(np.asarray(a[k]), np.asarray(b[k]))
@@ -279,9 +285,11 @@ def compare_fit_rounds(oracle_mod, got_rounds, ref, trace, bins, kw) -> int:
             break
         va, vb = np.asarray(a["value"], np.float64), np.asarray(b["value"], np.float64)
         if depth_traces:
-            bound = node_sum_bounds(b, bins, depth_traces[0]["grad"], lam, oracle_mod.leaf_index)
+            bound, leaf = node_sum_bounds(b, bins, depth_traces[0]["grad"], lam, oracle_mod.leaf_index,
+                                          return_leaf=True)
             err = np.abs(va - vb)
             bar = 1e-5 * (np.abs(vb) + 2.0 * bound) + 1e-7
+            pred_bar += lr * B * bar[leaf]
             worst = int(np.argmax(err / bar))
             print(f"[fit parity] round {r}: worst value error {err[worst]:.3g} at node {worst} "
                   f"(bar {bar[worst]:.3g}, |value| {abs(vb[worst]):.3g}, mass bound {bound[worst]:.3g})",
@@ -290,8 +298,9 @@ def compare_fit_rounds(oracle_mod, got_rounds, ref, trace, bins, kw) -> int:
                                         f"(bar {bar[worst]:.3g})")
         else:
             np.testing.assert_allclose(va, vb, rtol=1e-5, atol=1e-5, err_msg=f"round {r} value")
+            pred_bar += lr * B * 1e-5 * np.maximum(1.0, np.abs(vb[oracle_mod.leaf_index(b, bins)]))
         matched += 1
-    return matched
+    return matched, pred_bar
 
 
 def assert_near_tie(oracle_mod, bins, got, want, depth_traces, kw):

@@ -46,13 +46,20 @@ def test_config2_fit(hip, oracle_mod):
     print("[config2] oracle fit", flush=True)
     trace = []
     ref = oracle_mod.fit(bins, y, era.astype(np.int64), num_rounds=rounds, trace=trace, **kw)
-    matched = compare_fit_rounds(oracle_mod, model._rounds, ref, trace, bins, kw)
+    matched, pred_bar = compare_fit_rounds(oracle_mod, model._rounds, ref, trace, bins, kw)
     print(f"[config2] {matched} of {rounds} rounds identical", flush=True)
     assert matched >= 3
-    if matched == rounds:  # predictions: lr times values within the bars above
-        np.testing.assert_allclose(model._train_preds.cpu().numpy(), ref.preds, atol=1e-5, rtol=0)
+    if matched == rounds:
+        # predictions within 1e-5, or within what the node value bars allow (lr * B * bar of
+        # the row's leaf per round) plus one float32 rounding per add (B + 1 per round)
+        bar = np.maximum(1e-5, pred_bar + rounds * 9 * 6e-8 * np.abs(ref.preds))
+        d = np.abs(model._train_preds.cpu().numpy().astype(np.float64) - ref.preds)
+        print(f"[config2] training predictions: {int(np.sum(d > 1e-5))} rows beyond 1e-5, "
+              f"max {d.max():.3g}", flush=True)
+        assert np.all(d <= bar)
         pred = model.predict(X)
-        np.testing.assert_allclose(pred, oracle_mod.predict(ref.rounds, 8, 0.1, bins), atol=1e-5, rtol=0)
+        d = np.abs(pred.astype(np.float64) - oracle_mod.predict(ref.rounds, 8, 0.1, bins))
+        assert np.all(d <= bar)
 
 
 # ----------------------------------------------------------------------------- config 4
