@@ -381,6 +381,23 @@ int pb_rowlist_partition(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t
                          int32_t* right_index_dev, int64_t capacity, int32_t* left_splits_dev,
                          int32_t* right_splits_dev, int32_t* work_dev, void* stream);
 
+/* No counterpart in the reference: pb_rowlist_partition for callers that cannot allocate
+ * device memory (HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same inputs, outputs and results; the workspace is a fixed device array the library holds per
+ * device (16 MiB, kept until the process ends) instead of work_dev, and the four status words
+ * come back in status_dev (int32 [4], written by the call's own kernels). No allocation, no
+ * hipMemset. At most pb_rowlist_noalloc_max_segments() (node, era) segments, S * E, per call:
+ * larger calls return PB_ERR_UNSUPPORTED before any device work. Calls that overlap on one
+ * device share that array and race: serialise them (one stream, or events). */
+int64_t pb_rowlist_noalloc_max_segments(void);
+int pb_rowlist_partition_noalloc(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
+                                 const int32_t* rows_dev, int64_t R, const int32_t* node_row_splits_dev,
+                                 const int32_t* node_era_splits_dev, int32_t S, int32_t E,
+                                 const int32_t* feat_dev, const int32_t* thr_dev,
+                                 int32_t* left_index_dev, int32_t* right_index_dev, int64_t capacity,
+                                 int32_t* left_splits_dev, int32_t* right_splits_dev,
+                                 int32_t* status_dev, void* stream);
+
 /* The row-gathering half of find_best_splits_batched_cuda (frontier_cuda.cu:576-716, which
  * reads bins[f][rows_index[i]] and grad[i] per list position): the listed rows of nodes
  * [node_begin, node_end) in era-major order (era, then node, then list order), the layout

@@ -995,6 +995,38 @@ int pb_rowlist_partition(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, 
     return PB_OK;
 }
 
+int64_t pb_rowlist_noalloc_max_segments(void) { return pb::rowlist_noalloc_max_segments(); }
+
+int pb_rowlist_partition_noalloc(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                                 const int32_t* rows, int64_t R, const int32_t* node_row_splits,
+                                 const int32_t* node_era_splits, int32_t S, int32_t E,
+                                 const int32_t* feat, const int32_t* thr, int32_t* left_index,
+                                 int32_t* right_index, int64_t capacity, int32_t* left_splits,
+                                 int32_t* right_splits, int32_t* status, void* stream) {
+    if (S < 0 || E < 0 || N < 0 || R < 0 || F < 0 || capacity < 0)
+        return fail(PB_ERR_INVALID, "pb_rowlist_partition_noalloc: negative size");
+    if (N > ld) return fail(PB_ERR_INVALID, "pb_rowlist_partition_noalloc: N must be <= ld");
+    if (R > INT32_MAX || capacity > INT32_MAX)
+        return fail(PB_ERR_RANGE, "pb_rowlist_partition_noalloc: row lists above 2^31 - 1 entries");
+    const int64_t segments = (int64_t)S * E;
+    const int64_t max_segments = pb::rowlist_noalloc_max_segments();
+    if (segments > max_segments)
+        return fail(PB_ERR_UNSUPPORTED,
+                    "pb_rowlist_partition_noalloc: " + std::to_string(segments) +
+                        " (node, era) segments exceed the static workspace (at most " +
+                        std::to_string(max_segments) + "); use pb_rowlist_partition with a workspace");
+    if (S == 0) return PB_OK;
+    if (!bins || (!rows && R > 0) || !node_row_splits || !node_era_splits || !feat || !thr ||
+        (!left_index && capacity > 0) || (!right_index && capacity > 0) || !left_splits ||
+        !right_splits || !status)
+        return fail(PB_ERR_INVALID, "pb_rowlist_partition_noalloc: null argument");
+    PB_HIP(pb::launch_rowlist_partition_noalloc(bins, N, ld, F, rows, R, node_row_splits, node_era_splits,
+                                                S, E, feat, thr, left_index, right_index, capacity,
+                                                left_splits, right_splits, status, (hipStream_t)stream),
+           "rowlist partition (no-alloc) launch");
+    return PB_OK;
+}
+
 int pb_rowlist_gather(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const int32_t* feats,
                       int32_t K, const float* values, const int32_t* rows, int64_t R,
                       const int32_t* node_row_splits, const int32_t* node_era_splits,

@@ -220,6 +220,18 @@ hipError_t launch_pack_bins4(const uint8_t* bins, int64_t n, int64_t ld, int32_t
 // Row-list kernels (rowlist.hip). Workspace: rowlist_work_elems(segments) int32, whose first
 // four entries are status flags (segment, row id, feature, capacity) left set after the call.
 int64_t rowlist_work_elems(int64_t segments);
+// pb_rowlist_partition_noalloc: the same stages with the workspace in a fixed device array of
+// kNoAllocScratchInts int32 per device (no allocation); status [4] is the caller's.
+constexpr int64_t kNoAllocScratchInts = int64_t(1) << 22;  // 16 MiB
+constexpr int kNoAllocMaxDevices = 64;
+int64_t rowlist_noalloc_max_segments();
+hipError_t noalloc_scratch(int32_t** out);
+hipError_t launch_rowlist_partition_noalloc(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                                            const int32_t* rows, int64_t R, const int32_t* nrs,
+                                            const int32_t* nes, int32_t S, int32_t E,
+                                            const int32_t* feat, const int32_t* thr, int32_t* left_out,
+                                            int32_t* right_out, int64_t cap, int32_t* left_splits,
+                                            int32_t* right_splits, int32_t* status, hipStream_t s);
 hipError_t launch_rowlist_partition(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
                                     const int32_t* rows, int64_t R, const int32_t* nrs,
                                     const int32_t* nes, int32_t S, int32_t E, const int32_t* feat,

@@ -18,9 +18,40 @@
 // first entries of the workspace) instead of touching memory out of range.
 #include <algorithm>
 
+#include <mutex>
+
 #include "pb_internal.h"
 
+// Workspace of pb_rowlist_partition_noalloc: a fixed device array instead of caller or
+// library allocations (for callers that cannot allocate device memory, e.g. under HIP graph
+// capture). Every device the library runs on holds one copy until the process ends. Host code
+// never passes `scratch` itself to a kernel (on the host it names a shadow variable, not
+// device memory): pb::noalloc_scratch looks up each device's address once, with that device
+// current, and launches take that address.
+static __device__ __align__(256) int32_t scratch[pb::kNoAllocScratchInts];
+
 namespace pb {
+
+// Device address of `scratch` on the current device, looked up on the first call per device
+// (hipGetSymbolAddress with that device current) and kept.
+hipError_t noalloc_scratch(int32_t** out) {
+    static std::mutex mu;
+    static int32_t* addr[kNoAllocMaxDevices] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kNoAllocMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = static_cast<int32_t*>(p);
+    }
+    *out = addr[dev];
+    return hipSuccess;
+}
+
 namespace {
 
 constexpr int kRlBlock = 256;
@@ -370,17 +401,17 @@ int64_t rowlist_work_elems(int64_t segments) {
     return kRlStatus + 2 * segments + (2 * segments + 2) + (2 * tiles_of(segments) + 2);
 }
 
-hipError_t launch_rowlist_partition(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
-                                    const int32_t* rows, int64_t R, const int32_t* nrs,
-                                    const int32_t* nes, int32_t S, int32_t E, const int32_t* feat,
-                                    const int32_t* thr, int32_t* left_out, int32_t* right_out,
-                                    int64_t cap, int32_t* left_splits, int32_t* right_splits,
-                                    int32_t* work, hipStream_t s) {
+namespace {
+
+void rowlist_partition_stages(const uint8_t* bins, int64_t N, int64_t ld, int32_t F, const int32_t* rows,
+                              int64_t R, const int32_t* nrs, const int32_t* nes, int32_t S, int32_t E,
+                              const int32_t* feat, const int32_t* thr, int32_t* left_out,
+                              int32_t* right_out, int64_t cap, int32_t* left_splits,
+                              int32_t* right_splits, int32_t* status, int32_t* rest, hipStream_t s) {
     const int64_t n = (int64_t)S * E;
-    int32_t* status = work;
-    int32_t* vals = status + kRlStatus;  // [2n]
-    int32_t* scan = vals + 2 * n;        // [2n + 2]
-    int32_t* tiles = scan + 2 * n + 2;   // [2 nt + 2]
+    int32_t* vals = rest;               // [2n]
+    int32_t* scan = vals + 2 * n;       // [2n + 2]
+    int32_t* tiles = scan + 2 * n + 2;  // [2 nt + 2]
     const int g = grid_of(n, kRlWaves, 1 << 16);
     hipLaunchKernelGGL(rl_clear_kernel, dim3(1), dim3(kWave), 0, s, status);
     hipLaunchKernelGGL(rl_count_kernel, dim3(g), dim3(kRlBlock), 0, s, bins, N, ld, F, rows, R, nrs, nes,
@@ -390,6 +421,42 @@ hipError_t launch_rowlist_partition(const uint8_t* bins, int64_t N, int64_t ld, 
                        scan, S, E, left_splits, right_splits);
     hipLaunchKernelGGL(rl_scatter_kernel, dim3(g), dim3(kRlBlock), 0, s, bins, N, ld, F, rows, R, nrs, nes,
                        S, E, feat, thr, scan, left_out, right_out, cap, status);
+}
+
+}  // namespace
+
+hipError_t launch_rowlist_partition(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                                    const int32_t* rows, int64_t R, const int32_t* nrs,
+                                    const int32_t* nes, int32_t S, int32_t E, const int32_t* feat,
+                                    const int32_t* thr, int32_t* left_out, int32_t* right_out,
+                                    int64_t cap, int32_t* left_splits, int32_t* right_splits,
+                                    int32_t* work, hipStream_t s) {
+    rowlist_partition_stages(bins, N, ld, F, rows, R, nrs, nes, S, E, feat, thr, left_out, right_out,
+                             cap, left_splits, right_splits, work, work + kRlStatus, s);
+    return hipGetLastError();
+}
+
+int64_t rowlist_noalloc_max_segments() {
+    // largest n with rowlist_work_elems(n) - kRlStatus <= kNoAllocScratchInts
+    int64_t lo = 0, hi = kNoAllocScratchInts;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) / 2;
+        if (rowlist_work_elems(mid) - kRlStatus <= kNoAllocScratchInts) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+hipError_t launch_rowlist_partition_noalloc(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
+                                            const int32_t* rows, int64_t R, const int32_t* nrs,
+                                            const int32_t* nes, int32_t S, int32_t E,
+                                            const int32_t* feat, const int32_t* thr, int32_t* left_out,
+                                            int32_t* right_out, int64_t cap, int32_t* left_splits,
+                                            int32_t* right_splits, int32_t* status, hipStream_t s) {
+    int32_t* rest = nullptr;
+    hipError_t e = noalloc_scratch(&rest);
+    if (e != hipSuccess) return e;
+    rowlist_partition_stages(bins, N, ld, F, rows, R, nrs, nes, S, E, feat, thr, left_out, right_out,
+                             cap, left_splits, right_splits, status, rest, s);
     return hipGetLastError();
 }
 
