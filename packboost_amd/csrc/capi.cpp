@@ -843,7 +843,62 @@ struct pb_forest {
     int32_t total_nodes = 0;
     int32_t depth = 0;         // deepest leaf over all trees
     int32_t max_feature = -1;
+    // every tree as a complete heap of `depth` levels (the tiled walk; null when the forest is
+    // deeper than pb::kForestTileMaxDepth or its features do not fit a row tile)
+    pb::ForestTile tile{};         // shape of the tiled walk's LDS tile
+    uint32_t* heap_rec = nullptr;  // [T][2^depth - 1] packed records (pb::forest_tile_record)
+    float* heap_val = nullptr;     // [T][2^depth] leaf values
+    int32_t* heap_id = nullptr;    // [T][2^depth] leaf node indices (absolute)
 };
+
+namespace {
+
+void free_forest(pb_forest* fo) {
+    if (!fo) return;
+    (void)hipFree(fo->rec);
+    (void)hipFree(fo->roots);
+    (void)hipFree(fo->heap_rec);
+    (void)hipFree(fo->heap_val);
+    (void)hipFree(fo->heap_id);
+    delete fo;
+}
+
+// Heap form of one validated tree (root lo): a split at heap index h sends its children to
+// 2h + 1 and 2h + 2; a leaf above the last level becomes always-left splits (threshold 255:
+// every bin goes left) over its heap subtree, whose leaf slots all hold it.
+void heap_tree(const pb::ForestTile& ft, int lo, int D, const std::vector<int32_t>& f, const std::vector<int32_t>& th,
+               const std::vector<int32_t>& l, const std::vector<int32_t>& r, const std::vector<float>& v,
+               const std::vector<uint8_t>& lf, uint32_t* rec, float* val, int32_t* id) {
+    const int NI = (1 << D) - 1;
+    std::vector<std::pair<int, int>> st{{lo, 0}};  // (node, heap index)
+    while (!st.empty()) {
+        const auto [n, h] = st.back();
+        st.pop_back();
+        if (!lf[n]) {
+            rec[h] = pb::forest_tile_record(ft, f[n], th[n]);
+            st.push_back({l[n], 2 * h + 1});
+            st.push_back({r[n], 2 * h + 2});
+            continue;
+        }
+        // the leaf's heap subtree: levels below h down to the leaf slots
+        std::vector<int> lvl{h};
+        while (!lvl.empty() && lvl[0] < NI) {
+            std::vector<int> next;
+            for (int x : lvl) {
+                rec[x] = 255u << 24;  // offset 0 (feature 0 of the row), always left
+                next.push_back(2 * x + 1);
+                next.push_back(2 * x + 2);
+            }
+            lvl.swap(next);
+        }
+        for (int x : lvl) {
+            val[x - NI] = v[n];
+            id[x - NI] = n;
+        }
+    }
+}
+
+}  // namespace
 
 int pb_forest_create(const int32_t* feature, const int32_t* threshold, const int32_t* left_abs,
                      const int32_t* right_abs, const float* value, const uint8_t* is_leaf,
@@ -876,7 +931,7 @@ int pb_forest_create(const int32_t* feature, const int32_t* threshold, const int
     for (int t = 0; t < T; ++t) {
         const int lo = off[t], hi = off[t + 1];
         if (lo < 0 || hi > total_nodes || hi <= lo) {
-            delete fo;
+            free_forest(fo);
             return fail(PB_ERR_INVALID, "pb_forest_create: bad tree offsets");
         }
         roots[t] = lo;
@@ -893,7 +948,7 @@ int pb_forest_create(const int32_t* feature, const int32_t* threshold, const int
             const int fe = f[n], tr = th[n], a = l[n], b = r[n];
             if (fe < 0 || fe >= (1 << 24) - 1 || tr < 0 || tr > 255 || a < lo || a >= hi || b < lo ||
                 b >= hi || depth[a] >= 0 || depth[b] >= 0 || a == b) {
-                delete fo;
+                free_forest(fo);
                 return fail(PB_ERR_INVALID, "pb_forest_create: malformed tree (feature, threshold "
                                             "or child out of range, or a cycle)");
             }
@@ -906,18 +961,44 @@ int pb_forest_create(const int32_t* feature, const int32_t* threshold, const int
     }
     if (hipMalloc(&fo->rec, sizeof(int4) * rec.size()) != hipSuccess ||
         hipMalloc(&fo->roots, sizeof(int32_t) * roots.size()) != hipSuccess) {
-        (void)hipFree(fo->rec);
-        (void)hipFree(fo->roots);
-        delete fo;
+        free_forest(fo);
         return fail(PB_ERR_NOMEM, "pb_forest_create: device allocation failed");
     }
     hipError_t e1 = hipMemcpy(fo->rec, rec.data(), sizeof(int4) * rec.size(), hipMemcpyHostToDevice);
     hipError_t e2 = hipMemcpy(fo->roots, roots.data(), sizeof(int32_t) * roots.size(), hipMemcpyHostToDevice);
     if (e1 != hipSuccess || e2 != hipSuccess) {
-        (void)hipFree(fo->rec);
-        (void)hipFree(fo->roots);
-        delete fo;
+        free_forest(fo);
         return hip_fail(e1 != hipSuccess ? e1 : e2, "forest upload");
+    }
+    // heap form for the tiled walk
+    const int D = fo->depth;
+    int32_t max_thr = 0;
+    for (int t = 0; t < T; ++t)
+        for (int n = off[t]; n < off[t + 1]; ++n)
+            if (!lf[n] && depth[n] >= 0) max_thr = std::max(max_thr, th[n]);
+    if (D <= pb::kForestTileMaxDepth) fo->tile = pb::forest_tile_shape(fo->max_feature + 1, max_thr, D);
+    if (T > 0 && D <= pb::kForestTileMaxDepth &&
+        pb::forest_tile_lds_bytes(fo->tile, D) <= pb::kForestTileMaxLds) {
+        const size_t NI = ((size_t)1 << D) - 1, NL = (size_t)1 << D;
+        std::vector<uint32_t> hr(std::max<size_t>(1, (size_t)T * NI), 255u << 24);
+        std::vector<float> hv((size_t)T * NL, 0.0f);
+        std::vector<int32_t> hi((size_t)T * NL, -1);
+        for (int t = 0; t < T; ++t)
+            heap_tree(fo->tile, off[t], D, f, th, l, r, v, lf, hr.data() + (size_t)t * NI, hv.data() + (size_t)t * NL,
+                      hi.data() + (size_t)t * NL);
+        if (hipMalloc(&fo->heap_rec, sizeof(uint32_t) * hr.size()) != hipSuccess ||
+            hipMalloc(&fo->heap_val, sizeof(float) * hv.size()) != hipSuccess ||
+            hipMalloc(&fo->heap_id, sizeof(int32_t) * hi.size()) != hipSuccess) {
+            free_forest(fo);
+            return fail(PB_ERR_NOMEM, "pb_forest_create: device allocation failed");
+        }
+        hipError_t e3 = hipMemcpy(fo->heap_rec, hr.data(), sizeof(uint32_t) * hr.size(), hipMemcpyHostToDevice);
+        if (e3 == hipSuccess) e3 = hipMemcpy(fo->heap_val, hv.data(), sizeof(float) * hv.size(), hipMemcpyHostToDevice);
+        if (e3 == hipSuccess) e3 = hipMemcpy(fo->heap_id, hi.data(), sizeof(int32_t) * hi.size(), hipMemcpyHostToDevice);
+        if (e3 != hipSuccess) {
+            free_forest(fo);
+            return hip_fail(e3, "forest upload");
+        }
     }
     *out = fo;
     return PB_OK;
@@ -935,6 +1016,13 @@ int pb_forest_predict(const pb_forest* fo, const uint8_t* bins, int64_t N, int64
         PB_HIP(hipMemsetAsync(out, 0, sizeof(float) * (size_t)N, (hipStream_t)stream), "zero predictions");
         return PB_OK;
     }
+    if (fo->heap_rec && env_int("PB_FOREST_TILE", 1) != 0) {
+        const pb::ForestTile& ft = fo->tile;
+        PB_HIP(pb::launch_forest_tile(bins, N, ld, ft, fo->heap_rec, fo->heap_val, fo->heap_id, fo->T,
+                                      fo->depth, tree_weight, out, leaf, (hipStream_t)stream),
+               "forest tile launch");
+        return PB_OK;
+    }
     static const int32_t group = (int32_t)env_int("PB_FOREST_GROUP", 8);
     static const int32_t max_grid = (int32_t)env_int("PB_FOREST_GRID", 0);
     PB_HIP(pb::launch_forest(bins, N, ld, fo->rec, fo->roots, fo->T, fo->depth, tree_weight, out, leaf,
@@ -944,10 +1032,7 @@ int pb_forest_predict(const pb_forest* fo, const uint8_t* bins, int64_t N, int64
 }
 
 int pb_forest_destroy(pb_forest* fo) {
-    if (!fo) return PB_OK;
-    (void)hipFree(fo->rec);
-    (void)hipFree(fo->roots);
-    delete fo;
+    free_forest(fo);
     return PB_OK;
 }
 

@@ -127,6 +127,219 @@ __global__ __launch_bounds__(kBlock) void forest_kernel(
     }
 }
 
+// Tiled forest walk. The compiled forest also holds every tree as a complete heap of the
+// forest's depth D (a leaf above depth D becomes always-left splits down to its leftmost heap
+// leaf): internal node h at rec[t * (2^D - 1) + h] packs the bit position of its feature in its
+// word of a row tile (bits 0-4), the byte offset of that word row in the tile (bits 5-23; a
+// multiple of 4 * rows) and the threshold (bits 24-31); leaf slot k at val/id[t * 2^D + k].
+// A workgroup owns a tile of R rows (32 or 64). It stages the tile's bins in LDS once, packed
+// `bits` per bin (3 or 4 when every threshold of the forest is below 7 or 15: a bin above that
+// is clamped, which changes no comparison; else 8) and row-interleaved: word (j, r) holds the
+// features of word j of row r, so the rows of a word sit in distinct banks and any mix of
+// features reads without bank conflicts. Then blocks of trees (records and leaf values) are
+// staged in LDS in turn, and 256 / R tree streams (a lane per row) walk them, G trees per lane
+// at once: every load of the walk is an LDS load. Per level a lane reads the bin word of its
+// node and both children's records together, and the comparison picks the child (about six
+// VALU instructions). Each stream adds float32(weight * leaf value) of its trees in double;
+// the streams' sums are added in a fixed order and rounded once to float32.
+
+// Trees per LDS block for depth D: records and leaf values within kForestTreeBlockBytes.
+__host__ __device__ constexpr int forest_tree_block(int D) {
+    return (kForestTreeBlockBytes / 4) / ((1 << (D + 1)) - 1) > 0 ? (kForestTreeBlockBytes / 4) / ((1 << (D + 1)) - 1) : 1;
+}
+
+typedef __attribute__((address_space(3))) uint32_t lds_word;
+
+// LDS dword at byte address `a` of the kernel's (only) LDS allocation.
+__device__ __forceinline__ uint32_t lds_at(uint32_t a) { return *reinterpret_cast<const lds_word*>((size_t)a); }
+
+template <int BITS>
+__device__ __forceinline__ void stage_tile(const uint8_t* __restrict__ bins, int64_t ld, const ForestTile& ft,
+                                           int64_t r0, int R, uint32_t* tile) {
+    constexpr int PW = 32 / BITS;
+    constexpr uint32_t kClamp = (1u << BITS) - 1u;
+    const int words = ft.tile_words / R;
+    for (int idx = threadIdx.x; idx < words * (R / 4); idx += kBlock) {
+        const int j = idx / (R / 4);
+        const int q = idx - j * (R / 4);
+        const int64_t rr = r0 + 4 * q;
+        // unconditional loads from clamped (always valid) addresses, so that all of them are
+        // in flight at once; the out-of-range values are zeroed afterwards
+        const bool row_ok = rr < ld;
+        const int64_t rc = row_ok ? rr : 0;
+        uint32_t d[PW];
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int fc = min(j * PW + k, ft.features - 1);
+            d[k] = *reinterpret_cast<const uint32_t*>(bins + (int64_t)fc * ld + rc);
+        }
+#pragma unroll
+        for (int k = 0; k < PW; ++k) d[k] = (row_ok && j * PW + k < ft.features) ? d[k] : 0u;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            uint32_t w = 0u;
+#pragma unroll
+            for (int k = 0; k < PW; ++k) w |= min((d[k] >> (8 * m)) & 0xffu, kClamp) << (BITS * k);
+            tile[j * R + 4 * q + m] = w;
+        }
+    }
+}
+
+// LDS holds the kernel at two workgroups (two waves per SIMD), so the register budget of two
+// waves per SIMD lets every tree of a lane keep its loads in flight.
+template <int D, int R>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void forest_tile_kernel(
+    const uint8_t* __restrict__ bins, int64_t N, int64_t ld, ForestTile ft,
+    const uint32_t* __restrict__ rec, const float* __restrict__ lval, const int32_t* __restrict__ lid,
+    int32_t T, float tree_weight, float* __restrict__ out, int32_t* __restrict__ leaf) {
+    extern __shared__ uint32_t lds[];
+    constexpr int NI = (1 << D) - 1;
+    constexpr int NL = 1 << D;
+    constexpr int S = kBlock / R;                 // tree streams
+    constexpr int TB = forest_tree_block(D);      // trees per LDS block
+    constexpr int G = TB / S >= 8 ? 8 : (TB / S >= 1 ? TB / S : 1);  // trees a lane walks at once
+    const uint32_t bits = (uint32_t)ft.bits;
+    // LDS (byte addresses): the tile, then the block's records [TB][NI] and leaf values
+    // [TB][NL], then the streams' sums [S][R] at an 8-byte boundary
+    const uint32_t lds0 = (uint32_t)(size_t)(lds_word*)lds;
+    const uint32_t rec_b = lds0 + (uint32_t)ft.tile_words * 4u;
+    const uint32_t val_b = rec_b + (uint32_t)(TB * NI) * 4u;
+    uint32_t* trec = lds + ft.tile_words;
+    float* tval = reinterpret_cast<float*>(trec + TB * NI);
+    double* part = reinterpret_cast<double*>(lds + ((ft.tile_words + TB * (NI + NL) + 1) & ~1));
+    const int64_t r0 = (int64_t)blockIdx.x * R;
+
+    if (ft.bits == 3)
+        stage_tile<3>(bins, ld, ft, r0, R, lds);
+    else if (ft.bits == 4)
+        stage_tile<4>(bins, ld, ft, r0, R, lds);
+    else
+        stage_tile<8>(bins, ld, ft, r0, R, lds);
+
+    const int row = threadIdx.x & (R - 1);
+    const int stream = threadIdx.x / R;  // uniform over a wavefront
+    // the kernel declares no static LDS, so the tile starts at LDS address 0 and a row's word j
+    // sits at j*R*4 | row*4 (disjoint bits): a record's masked offset ORs with rowoff
+    const uint32_t rowoff = lds0 + (uint32_t)row * 4u;
+    const int64_t r = r0 + row;
+    double acc = 0.0;
+    // tree blocks: thread i holds elements i, i + 256, ... of the next block's records followed
+    // by its leaf values, loaded while the current block is walked
+    constexpr int PER = (TB * (NI + NL) + kBlock - 1) / kBlock;
+    uint32_t pre[PER];
+    const uint32_t* lval_u = reinterpret_cast<const uint32_t*>(lval);
+    auto fetch = [&](int tb0) {
+        // one unconditional load per element from a valid address (past the block: the first
+        // record), so that all of them are in flight at once
+        const int nb = min(TB, T - tb0);
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = threadIdx.x + k * kBlock;
+            const bool is_rec = i < nb * NI;
+            const bool is_val = !is_rec && i - nb * NI < nb * NL;
+            const uint32_t* src = is_rec ? rec + (int64_t)tb0 * NI + i
+                                 : is_val ? lval_u + (int64_t)tb0 * NL + (i - nb * NI)
+                                          : rec;
+            pre[k] = *src;
+        }
+    };
+    fetch(0);
+    for (int tb0 = 0; tb0 < T; tb0 += TB) {
+        const int nb = min(TB, T - tb0);
+        __syncthreads();  // the tile is staged; the last block's walks are done
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = threadIdx.x + k * kBlock;
+            if (i < nb * NI)
+                trec[i] = pre[k];
+            else if (i - nb * NI < nb * NL)
+                tval[i - nb * NI] = __uint_as_float(pre[k]);
+        }
+        __syncthreads();
+        if (tb0 + TB < T) fetch(tb0 + TB);
+        for (int k0 = stream; k0 < nb; k0 += S * G) {
+            // per tree: n = LDS word index of the current node; the left child of n is
+            // 2n + c with c = 1 - (the tree's first record), its leaf value at n + dv
+            uint32_t n[G], q[G], c[G], dv[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int k = min(k0 + g * S, nb - 1);
+                const uint32_t first = (rec_b >> 2) + (uint32_t)(k * NI);
+                n[g] = first;
+                c[g] = 1u - first;
+                dv[g] = (val_b >> 2) + (uint32_t)(k * NL) - first - (uint32_t)NI;
+                q[g] = D > 0 ? lds_at(first * 4u) : 0u;
+            }
+#pragma unroll
+            for (int lvl = 0; lvl < D; ++lvl) {
+                // all trees' reads are issued before any result is used, so that a lane keeps
+                // 2G reads in flight instead of waiting on each tree in turn
+                uint32_t w[G], left[G], ql[G], qr[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    w[g] = lds_at((q[g] & 0x00FFFFE0u) | rowoff);
+                    left[g] = 2u * n[g] + c[g];
+                }
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    ql[g] = 0u;
+                    qr[g] = 0u;
+                    if (lvl + 1 < D) {
+                        ql[g] = lds_at(left[g] * 4u);
+                        qr[g] = lds_at(left[g] * 4u + 4u);
+                    }
+                }
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const bool right = __builtin_amdgcn_ubfe(w[g], q[g], bits) > (q[g] >> 24);
+                    n[g] = left[g] + (right ? 1u : 0u);
+                    q[g] = right ? qr[g] : ql[g];
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const int k = k0 + g * S;
+                if (k < nb) {
+                    acc += (double)(tree_weight * __uint_as_float(lds_at((n[g] + dv[g]) * 4u)));
+                    if (leaf && r < N) {
+                        const int slot = (int)(n[g] + dv[g]) - (int)(val_b >> 2) - k * NL;
+                        leaf[(int64_t)(tb0 + k) * N + r] = lid[(int64_t)(tb0 + k) * NL + slot];
+                    }
+                }
+            }
+        }
+    }
+    part[stream * R + row] = acc;
+    __syncthreads();
+    if (threadIdx.x < R) {
+        double sum = 0.0;
+#pragma unroll
+        for (int s = 0; s < S; ++s) sum += part[s * R + threadIdx.x];
+        const int64_t rr = r0 + threadIdx.x;
+        if (rr < N) out[rr] = (float)sum;
+    }
+}
+
+template <int D>
+hipError_t launch_tile_d(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft, const uint32_t* rec,
+                         const float* lval, const int32_t* lid, int32_t T, float w, float* out,
+                         int32_t* leaf, hipStream_t s) {
+    const size_t lds = forest_tile_lds_bytes(ft, D);
+    const int64_t tiles = (N + ft.rows - 1) / ft.rows;
+    if (tiles > INT32_MAX) return hipErrorInvalidValue;
+    auto go = [&](auto kern) -> hipError_t {
+        const void* fn = reinterpret_cast<const void*>(kern);
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kBlock), lds, s, bins, N, ld, ft, rec, lval, lid,
+                           T, w, out, leaf);
+        return hipGetLastError();
+    };
+    return ft.rows == 64 ? go(forest_tile_kernel<D, 64>) : go(forest_tile_kernel<D, 32>);
+}
+
 int grid_rows(int64_t N) {
     int64_t g = (N + kBlock - 1) / kBlock;
     if (g < 1) g = 1;
@@ -173,6 +386,53 @@ hipError_t launch_forest(const uint8_t* bins, int64_t N, int64_t ld, const int4*
                                roots, T, depth, tree_weight, out, leaf);
     }
     return hipGetLastError();
+}
+
+ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t depth) {
+    ForestTile ft{};
+    ft.features = std::max(1, features);
+    ft.bits = max_threshold < 7 ? 3 : max_threshold < 15 ? 4 : 8;
+    const int per_word = 32 / ft.bits;
+    const int words = (ft.features + per_word - 1) / per_word;
+    ft.tree_block = forest_tree_block(depth);
+    ft.group = 0;
+    // 64-row tiles while two workgroups still fit a CU, else 32
+    ft.rows = 64;
+    ft.tile_words = words * ft.rows;
+    if (forest_tile_lds_bytes(ft, depth) > kForestTileTargetLds) {
+        ft.rows = 32;
+        ft.tile_words = words * ft.rows;
+    }
+    return ft;
+}
+
+size_t forest_tile_lds_bytes(const ForestTile& ft, int32_t depth) {
+    const size_t words = ((size_t)ft.tile_words + (size_t)ft.tree_block * (((size_t)2 << depth) - 1) + 1) & ~(size_t)1;
+    return words * 4 + (size_t)kBlock * 8;
+}
+
+uint32_t forest_tile_record(const ForestTile& ft, int32_t feature, int32_t threshold) {
+    const int per_word = 32 / ft.bits;
+    const uint32_t j = (uint32_t)(feature / per_word);
+    const uint32_t shift = (uint32_t)((feature % per_word) * ft.bits);  // < 32
+    return (j * (uint32_t)ft.rows * 4u) | shift | ((uint32_t)threshold << 24);
+}
+
+hipError_t launch_forest_tile(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft,
+                              const uint32_t* rec, const float* lval, const int32_t* lid, int32_t T,
+                              int32_t depth, float tree_weight, float* out, int32_t* leaf, hipStream_t s) {
+    switch (depth) {
+        case 0: return launch_tile_d<0>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 1: return launch_tile_d<1>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 2: return launch_tile_d<2>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 3: return launch_tile_d<3>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 4: return launch_tile_d<4>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 5: return launch_tile_d<5>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 6: return launch_tile_d<6>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 7: return launch_tile_d<7>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 8: return launch_tile_d<8>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_predict_bins(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,

@@ -1,8 +1,9 @@
 """Compiled-forest prediction (pb_forest_create / pb_forest_predict) on a config-5 style
 forest (full depth-6 trees, random features and thresholds, leaves N(0, 0.01)) against the
 per-row walk of pb_predict_forest and the CPU oracle (booster.py:131-169, 709-712):
-predictions bit-identical to pb_predict_forest (same summation order), within 1e-5 of the
-oracle's float32 tree-order sum; leaf indices bit-exact. Malformed forests are rejected."""
+predictions within 1e-5 of the oracle's float32 tree-order sum (the per-row walk bit-identical
+to pb_predict_forest, the tiled walk within 1e-5 of it); leaf indices bit-exact. Malformed
+forests are rejected."""
 
 from __future__ import annotations
 
@@ -32,10 +33,15 @@ def _forest(seed, packs, B, D, F, ragged=False):
     return rounds
 
 
+@pytest.mark.parametrize("tile", [1, 0], ids=["tiled", "per-row"])
 @pytest.mark.parametrize("ragged", [False, True])
-def test_compiled_forest(hip, oracle_mod, ragged):
+def test_compiled_forest(hip, oracle_mod, monkeypatch, ragged, tile):
+    """tile 1: the tiled walk (double sums rounded once; the tree-order float32 sum of
+    pb_predict_forest carries up to T float32 roundings, so the two agree to 1e-5); tile 0: the
+    per-row walk, bit-identical to pb_predict_forest."""
     import torch
 
+    monkeypatch.setenv("PB_FOREST_TILE", str(tile))
     from packboost_amd.booster import pack_forest
     from packboost_amd.predictor import CompiledForest
 
@@ -61,7 +67,10 @@ def test_compiled_forest(hip, oracle_mod, ragged):
                                     f["is_leaf"].data_ptr(), f["offsets"].data_ptr(), T,
                                     int(f["value"].numel()), 0.5, ref.data_ptr(), hip.stream_ptr()),
               "pb_predict_forest")
-    np.testing.assert_array_equal(got, ref.cpu().numpy())
+    if tile:
+        np.testing.assert_allclose(got, ref.cpu().numpy(), rtol=0, atol=1e-5)
+    else:
+        np.testing.assert_array_equal(got, ref.cpu().numpy())
     np.testing.assert_allclose(got, oracle_mod.predict(rounds, B, 0.5, bins), rtol=0, atol=1e-5)
     lv = leaves.cpu().numpy() - f["offsets"][:-1].cpu().numpy()[:, None]
     for r, arrs in enumerate(rounds):
