@@ -846,9 +846,9 @@ struct pb_forest {
     // every tree as a complete heap of `depth` levels (the tiled walk; null when the forest is
     // deeper than pb::kForestTileMaxDepth or its features do not fit a row tile)
     pb::ForestTile tile{};         // shape of the tiled walk's LDS tile
-    uint32_t* heap_rec = nullptr;  // [T][2^depth - 1] packed records (pb::forest_tile_record)
-    float* heap_val = nullptr;     // [T][2^depth] leaf values
-    int32_t* heap_id = nullptr;    // [T][2^depth] leaf node indices (absolute)
+    uint32_t* heap_blocks = nullptr;  // tile.blocks x kForestBlockWords: per block of trees, the
+                                      // packed records (pb::forest_tile_record), then leaf values
+    int32_t* heap_id = nullptr;       // [T][2^depth] leaf node indices (absolute)
 };
 
 namespace {
@@ -857,8 +857,7 @@ void free_forest(pb_forest* fo) {
     if (!fo) return;
     (void)hipFree(fo->rec);
     (void)hipFree(fo->roots);
-    (void)hipFree(fo->heap_rec);
-    (void)hipFree(fo->heap_val);
+    (void)hipFree(fo->heap_blocks);
     (void)hipFree(fo->heap_id);
     delete fo;
 }
@@ -976,24 +975,28 @@ int pb_forest_create(const int32_t* feature, const int32_t* threshold, const int
     for (int t = 0; t < T; ++t)
         for (int n = off[t]; n < off[t + 1]; ++n)
             if (!lf[n] && depth[n] >= 0) max_thr = std::max(max_thr, th[n]);
-    if (D <= pb::kForestTileMaxDepth) fo->tile = pb::forest_tile_shape(fo->max_feature + 1, max_thr, D);
-    if (T > 0 && D <= pb::kForestTileMaxDepth &&
-        pb::forest_tile_lds_bytes(fo->tile, D) <= pb::kForestTileMaxLds) {
-        const size_t NI = ((size_t)1 << D) - 1, NL = (size_t)1 << D;
-        std::vector<uint32_t> hr(std::max<size_t>(1, (size_t)T * NI), 255u << 24);
-        std::vector<float> hv((size_t)T * NL, 0.0f);
+    if (D <= pb::kForestTileMaxDepth) fo->tile = pb::forest_tile_shape(fo->max_feature + 1, max_thr, D, T);
+    if (T > 0 && D <= pb::kForestTileMaxDepth && pb::forest_tile_lds_bytes(fo->tile) <= pb::kForestTileMaxLds) {
+        const size_t NL = (size_t)1 << D, TB = (size_t)fo->tile.tree_block;
+        const size_t BW = pb::kForestBlockWords;
+        // tree k of block b at dwords b*BW + k*2NL: node i (from 1) at dword i, leaves from NL;
+        // padding trees: always-left records and zero leaf values
+        std::vector<uint32_t> blk((size_t)fo->tile.blocks * BW, 0u);
+        for (size_t x = 0; x < blk.size(); x += 2 * NL)
+            std::fill(blk.begin() + x + 1, blk.begin() + x + NL, 255u << 24);
+        std::vector<float> val(NL);
         std::vector<int32_t> hi((size_t)T * NL, -1);
-        for (int t = 0; t < T; ++t)
-            heap_tree(fo->tile, off[t], D, f, th, l, r, v, lf, hr.data() + (size_t)t * NI, hv.data() + (size_t)t * NL,
-                      hi.data() + (size_t)t * NL);
-        if (hipMalloc(&fo->heap_rec, sizeof(uint32_t) * hr.size()) != hipSuccess ||
-            hipMalloc(&fo->heap_val, sizeof(float) * hv.size()) != hipSuccess ||
+        for (int t = 0; t < T; ++t) {
+            uint32_t* tree = blk.data() + (size_t)(t / TB) * BW + (size_t)(t % TB) * 2 * NL;
+            heap_tree(fo->tile, off[t], D, f, th, l, r, v, lf, tree + 1, val.data(), hi.data() + (size_t)t * NL);
+            std::memcpy(tree + NL, val.data(), sizeof(float) * NL);
+        }
+        if (hipMalloc(&fo->heap_blocks, sizeof(uint32_t) * blk.size()) != hipSuccess ||
             hipMalloc(&fo->heap_id, sizeof(int32_t) * hi.size()) != hipSuccess) {
             free_forest(fo);
             return fail(PB_ERR_NOMEM, "pb_forest_create: device allocation failed");
         }
-        hipError_t e3 = hipMemcpy(fo->heap_rec, hr.data(), sizeof(uint32_t) * hr.size(), hipMemcpyHostToDevice);
-        if (e3 == hipSuccess) e3 = hipMemcpy(fo->heap_val, hv.data(), sizeof(float) * hv.size(), hipMemcpyHostToDevice);
+        hipError_t e3 = hipMemcpy(fo->heap_blocks, blk.data(), sizeof(uint32_t) * blk.size(), hipMemcpyHostToDevice);
         if (e3 == hipSuccess) e3 = hipMemcpy(fo->heap_id, hi.data(), sizeof(int32_t) * hi.size(), hipMemcpyHostToDevice);
         if (e3 != hipSuccess) {
             free_forest(fo);
@@ -1016,10 +1019,11 @@ int pb_forest_predict(const pb_forest* fo, const uint8_t* bins, int64_t N, int64
         PB_HIP(hipMemsetAsync(out, 0, sizeof(float) * (size_t)N, (hipStream_t)stream), "zero predictions");
         return PB_OK;
     }
-    if (fo->heap_rec && env_int("PB_FOREST_TILE", 1) != 0) {
-        const pb::ForestTile& ft = fo->tile;
-        PB_HIP(pb::launch_forest_tile(bins, N, ld, ft, fo->heap_rec, fo->heap_val, fo->heap_id, fo->T,
-                                      fo->depth, tree_weight, out, leaf, (hipStream_t)stream),
+    // the tiled walk reads a tile's rows four at a time: row stride and columns 4-byte aligned
+    if (fo->heap_blocks && ld % 4 == 0 && reinterpret_cast<uintptr_t>(bins) % 4 == 0 &&
+        env_int("PB_FOREST_TILE", 1) != 0) {
+        PB_HIP(pb::launch_forest_tile(bins, N, ld, fo->tile, fo->heap_blocks, fo->heap_id, fo->T, fo->depth,
+                                      tree_weight, out, leaf, (hipStream_t)stream),
                "forest tile launch");
         return PB_OK;
     }

@@ -264,21 +264,23 @@ hipError_t launch_forest(const uint8_t* bins, int64_t N, int64_t ld, const int4*
 constexpr int kForestTileMaxDepth = 8;
 constexpr size_t kForestTileMaxLds = 144 * 1024;
 constexpr size_t kForestTileTargetLds = 80 * 1024;  // two workgroups per CU
-constexpr int kForestTreeBlockBytes = 16 * 1024;     // trees staged in LDS at a time
+constexpr int kForestBlockWords = 4096;             // dwords of one tree block (16 KB)
+// Trees per block at depth D: each tree takes 2^(D+1) dwords (its complete heap, slot 0 unused).
+constexpr int forest_tree_block(int D) { return kForestBlockWords >> (D + 1); }
 struct ForestTile {
     int32_t features;    // feature columns in the tile (the forest's largest feature + 1)
     int32_t bits;        // bits per bin in the tile (3, 4 or 8)
     int32_t rows;        // rows per tile (32 or 64)
     int32_t tile_words;  // dwords of the packed tile
-    int32_t tree_block;  // trees per LDS block
-    int32_t group;       // reserved
+    int32_t tree_block;  // trees per block (forest_tree_block of the depth)
+    int32_t blocks;      // tree blocks (the last one padded with trees that add 0)
 };
-ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t depth);
-size_t forest_tile_lds_bytes(const ForestTile& ft, int32_t depth);
+ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t depth, int32_t trees);
+size_t forest_tile_lds_bytes(const ForestTile& ft);
 uint32_t forest_tile_record(const ForestTile& ft, int32_t feature, int32_t threshold);
 hipError_t launch_forest_tile(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft,
-                              const uint32_t* rec, const float* lval, const int32_t* lid, int32_t T,
-                              int32_t depth, float tree_weight, float* out, int32_t* leaf, hipStream_t s);
+                              const uint32_t* blocks, const int32_t* lid, int32_t T, int32_t depth,
+                              float tree_weight, float* out, int32_t* leaf, hipStream_t s);
 hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
                                const int32_t* feature, const int32_t* threshold,
                                const int32_t* left_abs, const int32_t* right_abs,

@@ -129,30 +129,40 @@ __global__ __launch_bounds__(kBlock) void forest_kernel(
 
 // Tiled forest walk. The compiled forest also holds every tree as a complete heap of the
 // forest's depth D (a leaf above depth D becomes always-left splits down to its leftmost heap
-// leaf): internal node h at rec[t * (2^D - 1) + h] packs the bit position of its feature in its
-// word of a row tile (bits 0-4), the byte offset of that word row in the tile (bits 5-23; a
-// multiple of 4 * rows) and the threshold (bits 24-31); leaf slot k at val/id[t * 2^D + k].
+// leaf), grouped in blocks of TB = forest_tree_block(D) trees of kForestBlockWords dwords:
+// tree k of a block takes dwords k * 2^(D+1) .. (k + 1) * 2^(D+1) - 1, node i (counted from 1,
+// children 2i and 2i + 1) at dword i: the records of its internal nodes (i < 2^D) and the
+// values of its leaves (i >= 2^D); dword 0 is unused, so that both children of a node sit in
+// one aligned 8-byte pair. A record packs the bit position of its feature in its word of a row
+// tile (bits 0-4), the byte offset of that word row in the tile (bits 5-23; a multiple of
+// 4 * rows) and the threshold (bits 24-31). Trees past the forest's last one pad the last
+// block with always-left records and zero leaf values.
 // A workgroup owns a tile of R rows (32 or 64). It stages the tile's bins in LDS once, packed
 // `bits` per bin (3 or 4 when every threshold of the forest is below 7 or 15: a bin above that
 // is clamped, which changes no comparison; else 8) and row-interleaved: word (j, r) holds the
 // features of word j of row r, so the rows of a word sit in distinct banks and any mix of
-// features reads without bank conflicts. Then blocks of trees (records and leaf values) are
-// staged in LDS in turn, and 256 / R tree streams (a lane per row) walk them, G trees per lane
-// at once: every load of the walk is an LDS load. Per level a lane reads the bin word of its
-// node and both children's records together, and the comparison picks the child (about six
-// VALU instructions). Each stream adds float32(weight * leaf value) of its trees in double;
-// the streams' sums are added in a fixed order and rounded once to float32.
-
-// Trees per LDS block for depth D: records and leaf values within kForestTreeBlockBytes.
-__host__ __device__ constexpr int forest_tree_block(int D) {
-    return (kForestTreeBlockBytes / 4) / ((1 << (D + 1)) - 1) > 0 ? (kForestTreeBlockBytes / 4) / ((1 << (D + 1)) - 1) : 1;
-}
+// features reads without bank conflicts. The tree blocks then pass through LDS in turn (each
+// thread copies four dwords per 1024 of the next block into registers while the current block
+// is walked), and 256 / R tree streams (a lane per row) walk them, G trees per lane at once:
+// every load of the walk is an LDS load. Per level a lane reads the bin word of its node and
+// both children's records (one 8-byte read), and the comparison picks the child. Each stream
+// adds float32(weight * leaf value) of its trees in double; the streams' sums are added in a
+// fixed order and rounded once to float32.
 
 typedef __attribute__((address_space(3))) uint32_t lds_word;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte copies of tree blocks
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) u32x2 lds_pair;
 
 // LDS dword at byte address `a` of the kernel's (only) LDS allocation.
 __device__ __forceinline__ uint32_t lds_at(uint32_t a) { return *reinterpret_cast<const lds_word*>((size_t)a); }
+// LDS dwords a and a + 4 (a a multiple of 8) in one 64-bit read.
+__device__ __forceinline__ u32x2 lds_pair_at(uint32_t a) { return *reinterpret_cast<const lds_pair*>((size_t)a); }
 
+// Bins of rows r0 .. r0 + R - 1 into the packed, row-interleaved tile. The rows are read four
+// at a time as one dword per feature column, which the caller allows by a row stride that is
+// a multiple of 4 (and 4-byte aligned columns): rows past the column's end read as 0.
 template <int BITS>
 __device__ __forceinline__ void stage_tile(const uint8_t* __restrict__ bins, int64_t ld, const ForestTile& ft,
                                            int64_t r0, int R, uint32_t* tile) {
@@ -187,26 +197,25 @@ __device__ __forceinline__ void stage_tile(const uint8_t* __restrict__ bins, int
 
 // LDS holds the kernel at two workgroups (two waves per SIMD), so the register budget of two
 // waves per SIMD lets every tree of a lane keep its loads in flight.
-template <int D, int R>
+template <int D, int R, bool LEAF>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void forest_tile_kernel(
-    const uint8_t* __restrict__ bins, int64_t N, int64_t ld, ForestTile ft,
-    const uint32_t* __restrict__ rec, const float* __restrict__ lval, const int32_t* __restrict__ lid,
-    int32_t T, float tree_weight, float* __restrict__ out, int32_t* __restrict__ leaf) {
+    const uint8_t* __restrict__ bins, int64_t N, int64_t ld, ForestTile ft, const u32x4* __restrict__ blocks,
+    const int32_t* __restrict__ lid, int32_t T, float tree_weight, float* __restrict__ out,
+    int32_t* __restrict__ leaf) {
     extern __shared__ uint32_t lds[];
-    constexpr int NI = (1 << D) - 1;
     constexpr int NL = 1 << D;
     constexpr int S = kBlock / R;                 // tree streams
-    constexpr int TB = forest_tree_block(D);      // trees per LDS block
+    constexpr int TB = forest_tree_block(D);      // trees per block
     constexpr int G = TB / S >= 8 ? 8 : (TB / S >= 1 ? TB / S : 1);  // trees a lane walks at once
+    static_assert(TB % (S * G) == 0 || TB < S, "a block splits evenly over streams and lanes");
+    constexpr int PER = kForestBlockWords / (4 * kBlock);  // 16-byte copies of a block per thread
+    static_assert(PER * 4 * kBlock == kForestBlockWords, "whole 16-byte copies per thread");
     const uint32_t bits = (uint32_t)ft.bits;
-    // LDS (byte addresses): the tile, then the block's records [TB][NI] and leaf values
-    // [TB][NL], then the streams' sums [S][R] at an 8-byte boundary
+    // LDS: the tile, then the current tree block, then the streams' sums [S][R]
     const uint32_t lds0 = (uint32_t)(size_t)(lds_word*)lds;
     const uint32_t rec_b = lds0 + (uint32_t)ft.tile_words * 4u;
-    const uint32_t val_b = rec_b + (uint32_t)(TB * NI) * 4u;
-    uint32_t* trec = lds + ft.tile_words;
-    float* tval = reinterpret_cast<float*>(trec + TB * NI);
-    double* part = reinterpret_cast<double*>(lds + ((ft.tile_words + TB * (NI + NL) + 1) & ~1));
+    u32x4* tblock = reinterpret_cast<u32x4*>(lds + ft.tile_words);
+    double* part = reinterpret_cast<double*>(lds + ft.tile_words + kForestBlockWords);
     const int64_t r0 = (int64_t)blockIdx.x * R;
 
     if (ft.bits == 3)
@@ -217,94 +226,64 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
         stage_tile<8>(bins, ld, ft, r0, R, lds);
 
     const int row = threadIdx.x & (R - 1);
-    const int stream = threadIdx.x / R;  // uniform over a wavefront
+    // a stream is uniform over a wavefront when R = 64
+    const int stream = R == 64 ? __builtin_amdgcn_readfirstlane(threadIdx.x / R) : threadIdx.x / R;
     // the kernel declares no static LDS, so the tile starts at LDS address 0 and a row's word j
     // sits at j*R*4 | row*4 (disjoint bits): a record's masked offset ORs with rowoff
     const uint32_t rowoff = lds0 + (uint32_t)row * 4u;
     const int64_t r = r0 + row;
     double acc = 0.0;
-    // tree blocks: thread i holds elements i, i + 256, ... of the next block's records followed
-    // by its leaf values, loaded while the current block is walked
-    constexpr int PER = (TB * (NI + NL) + kBlock - 1) / kBlock;
-    uint32_t pre[PER];
-    const uint32_t* lval_u = reinterpret_cast<const uint32_t*>(lval);
-    auto fetch = [&](int tb0) {
-        // one unconditional load per element from a valid address (past the block: the first
-        // record), so that all of them are in flight at once
-        const int nb = min(TB, T - tb0);
+    u32x4 pre[PER];
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = threadIdx.x + k * kBlock;
-            const bool is_rec = i < nb * NI;
-            const bool is_val = !is_rec && i - nb * NI < nb * NL;
-            const uint32_t* src = is_rec ? rec + (int64_t)tb0 * NI + i
-                                 : is_val ? lval_u + (int64_t)tb0 * NL + (i - nb * NI)
-                                          : rec;
-            pre[k] = *src;
-        }
-    };
-    fetch(0);
-    for (int tb0 = 0; tb0 < T; tb0 += TB) {
-        const int nb = min(TB, T - tb0);
+    for (int k = 0; k < PER; ++k) pre[k] = blocks[threadIdx.x + k * kBlock];
+    for (int b = 0; b < ft.blocks; ++b) {
         __syncthreads();  // the tile is staged; the last block's walks are done
 #pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = threadIdx.x + k * kBlock;
-            if (i < nb * NI)
-                trec[i] = pre[k];
-            else if (i - nb * NI < nb * NL)
-                tval[i - nb * NI] = __uint_as_float(pre[k]);
-        }
+        for (int k = 0; k < PER; ++k) tblock[threadIdx.x + k * kBlock] = pre[k];
         __syncthreads();
-        if (tb0 + TB < T) fetch(tb0 + TB);
-        for (int k0 = stream; k0 < nb; k0 += S * G) {
-            // per tree: n = LDS word index of the current node; the left child of n is
-            // 2n + c with c = 1 - (the tree's first record), its leaf value at n + dv
-            uint32_t n[G], q[G], c[G], dv[G];
+        {
+            // the next block (the last one again after the last: an unconditional load keeps
+            // the copies in registers)
+            const u32x4* src = blocks + (int64_t)min(b + 1, ft.blocks - 1) * (kForestBlockWords / 4) + threadIdx.x;
+#pragma unroll
+            for (int k = 0; k < PER; ++k) pre[k] = src[k * kBlock];
+        }
+        for (int k0 = stream; k0 < TB; k0 += S * G) {
+            // per tree: i = heap index of the current node counted from 1 (children 2i and
+            // 2i + 1); node i's record (internal) or leaf value (i >= 2^D) at byte base + 4i
+            uint32_t i[G], q[G], base[G];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const int k = min(k0 + g * S, nb - 1);
-                const uint32_t first = (rec_b >> 2) + (uint32_t)(k * NI);
-                n[g] = first;
-                c[g] = 1u - first;
-                dv[g] = (val_b >> 2) + (uint32_t)(k * NL) - first - (uint32_t)NI;
-                q[g] = D > 0 ? lds_at(first * 4u) : 0u;
+                base[g] = rec_b + (uint32_t)(k0 + g * S) * (4u << (D + 1));
+                i[g] = 1u;
+                q[g] = D > 0 ? lds_at(base[g] + 4u) : 0u;
             }
 #pragma unroll
             for (int lvl = 0; lvl < D; ++lvl) {
                 // all trees' reads are issued before any result is used, so that a lane keeps
                 // 2G reads in flight instead of waiting on each tree in turn
-                uint32_t w[G], left[G], ql[G], qr[G];
+                uint32_t w[G];
+                u32x2 ch[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) w[g] = lds_at((q[g] & 0x00FFFFE0u) | rowoff);
+#pragma unroll
+                for (int g = 0; g < G; ++g) ch[g] = lvl + 1 < D ? lds_pair_at(base[g] + 8u * i[g]) : u32x2{0u, 0u};
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    w[g] = lds_at((q[g] & 0x00FFFFE0u) | rowoff);
-                    left[g] = 2u * n[g] + c[g];
-                }
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    ql[g] = 0u;
-                    qr[g] = 0u;
-                    if (lvl + 1 < D) {
-                        ql[g] = lds_at(left[g] * 4u);
-                        qr[g] = lds_at(left[g] * 4u + 4u);
-                    }
-                }
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const bool right = __builtin_amdgcn_ubfe(w[g], q[g], bits) > (q[g] >> 24);
-                    n[g] = left[g] + (right ? 1u : 0u);
-                    q[g] = right ? qr[g] : ql[g];
+                    // right = bin > threshold as a lane mask; then i = i + i + right (one
+                    // add with carry-in) and q = right ? right child : left child
+                    const uint64_t right = __builtin_amdgcn_uicmp(__builtin_amdgcn_ubfe(w[g], q[g], bits), q[g] >> 24, 34);
+                    uint64_t co;
+                    asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(i[g]), "=s"(co) : "v"(i[g]), "s"(right));
+                    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(q[g]) : "v"(ch[g].x), "v"(ch[g].y), "s"(right));
                 }
             }
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const int k = k0 + g * S;
-                if (k < nb) {
-                    acc += (double)(tree_weight * __uint_as_float(lds_at((n[g] + dv[g]) * 4u)));
-                    if (leaf && r < N) {
-                        const int slot = (int)(n[g] + dv[g]) - (int)(val_b >> 2) - k * NL;
-                        leaf[(int64_t)(tb0 + k) * N + r] = lid[(int64_t)(tb0 + k) * NL + slot];
-                    }
+                acc += (double)(tree_weight * __uint_as_float(lds_at(base[g] + 4u * i[g])));
+                if (LEAF) {
+                    const int t = b * TB + k0 + g * S;
+                    if (t < T && r < N) leaf[(int64_t)t * N + r] = lid[(int64_t)t * NL + (int)i[g] - NL];
                 }
             }
         }
@@ -321,23 +300,24 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 }
 
 template <int D>
-hipError_t launch_tile_d(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft, const uint32_t* rec,
-                         const float* lval, const int32_t* lid, int32_t T, float w, float* out,
-                         int32_t* leaf, hipStream_t s) {
-    const size_t lds = forest_tile_lds_bytes(ft, D);
+hipError_t launch_tile_d(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft, const uint32_t* blocks,
+                         const int32_t* lid, int32_t T, float w, float* out, int32_t* leaf, hipStream_t s) {
+    const size_t lds = forest_tile_lds_bytes(ft);
     const int64_t tiles = (N + ft.rows - 1) / ft.rows;
-    if (tiles > INT32_MAX) return hipErrorInvalidValue;
+    if (tiles > INT32_MAX || ft.tree_block != forest_tree_block(D) || (ft.rows != 32 && ft.rows != 64))
+        return hipErrorInvalidValue;
     auto go = [&](auto kern) -> hipError_t {
         const void* fn = reinterpret_cast<const void*>(kern);
         if (lds > 64 * 1024) {
             hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
-        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kBlock), lds, s, bins, N, ld, ft, rec, lval, lid,
-                           T, w, out, leaf);
+        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kBlock), lds, s, bins, N, ld, ft,
+                           reinterpret_cast<const u32x4*>(blocks), lid, T, w, out, leaf);
         return hipGetLastError();
     };
-    return ft.rows == 64 ? go(forest_tile_kernel<D, 64>) : go(forest_tile_kernel<D, 32>);
+    if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, true>) : go(forest_tile_kernel<D, 32, true>);
+    return ft.rows == 64 ? go(forest_tile_kernel<D, 64, false>) : go(forest_tile_kernel<D, 32, false>);
 }
 
 int grid_rows(int64_t N) {
@@ -388,27 +368,26 @@ hipError_t launch_forest(const uint8_t* bins, int64_t N, int64_t ld, const int4*
     return hipGetLastError();
 }
 
-ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t depth) {
+ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t depth, int32_t trees) {
     ForestTile ft{};
     ft.features = std::max(1, features);
     ft.bits = max_threshold < 7 ? 3 : max_threshold < 15 ? 4 : 8;
     const int per_word = 32 / ft.bits;
     const int words = (ft.features + per_word - 1) / per_word;
     ft.tree_block = forest_tree_block(depth);
-    ft.group = 0;
+    ft.blocks = (std::max(0, trees) + ft.tree_block - 1) / ft.tree_block;
     // 64-row tiles while two workgroups still fit a CU, else 32
     ft.rows = 64;
     ft.tile_words = words * ft.rows;
-    if (forest_tile_lds_bytes(ft, depth) > kForestTileTargetLds) {
+    if (forest_tile_lds_bytes(ft) > kForestTileTargetLds) {
         ft.rows = 32;
         ft.tile_words = words * ft.rows;
     }
     return ft;
 }
 
-size_t forest_tile_lds_bytes(const ForestTile& ft, int32_t depth) {
-    const size_t words = ((size_t)ft.tile_words + (size_t)ft.tree_block * (((size_t)2 << depth) - 1) + 1) & ~(size_t)1;
-    return words * 4 + (size_t)kBlock * 8;
+size_t forest_tile_lds_bytes(const ForestTile& ft) {
+    return ((size_t)ft.tile_words + kForestBlockWords) * 4 + (size_t)kBlock * 8;
 }
 
 uint32_t forest_tile_record(const ForestTile& ft, int32_t feature, int32_t threshold) {
@@ -419,18 +398,19 @@ uint32_t forest_tile_record(const ForestTile& ft, int32_t feature, int32_t thres
 }
 
 hipError_t launch_forest_tile(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft,
-                              const uint32_t* rec, const float* lval, const int32_t* lid, int32_t T,
-                              int32_t depth, float tree_weight, float* out, int32_t* leaf, hipStream_t s) {
+                              const uint32_t* blocks, const int32_t* lid, int32_t T, int32_t depth,
+                              float tree_weight, float* out, int32_t* leaf, hipStream_t s) {
+    if (ld % 4 != 0 || reinterpret_cast<uintptr_t>(bins) % 4 != 0 || ft.blocks < 1) return hipErrorInvalidValue;
     switch (depth) {
-        case 0: return launch_tile_d<0>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 1: return launch_tile_d<1>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 2: return launch_tile_d<2>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 3: return launch_tile_d<3>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 4: return launch_tile_d<4>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 5: return launch_tile_d<5>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 6: return launch_tile_d<6>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 7: return launch_tile_d<7>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
-        case 8: return launch_tile_d<8>(bins, N, ld, ft, rec, lval, lid, T, tree_weight, out, leaf, s);
+        case 0: return launch_tile_d<0>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 1: return launch_tile_d<1>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 2: return launch_tile_d<2>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 3: return launch_tile_d<3>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 4: return launch_tile_d<4>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 5: return launch_tile_d<5>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 6: return launch_tile_d<6>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 7: return launch_tile_d<7>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 8: return launch_tile_d<8>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
         default: return hipErrorInvalidValue;
     }
 }

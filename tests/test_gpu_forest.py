@@ -15,7 +15,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
-def _forest(seed, packs, B, D, F, ragged=False):
+def _forest(seed, packs, B, D, F, ragged=False, max_thr=3):
     rng = np.random.default_rng(seed)
     n_nodes = (1 << (D + 1)) - 1
     inner = (1 << D) - 1
@@ -23,10 +23,10 @@ def _forest(seed, packs, B, D, F, ragged=False):
     for p in range(packs):
         idx = np.arange(n_nodes)
         leaf = idx >= inner
-        if ragged and p % 2:  # a shallower tree: depth-2 subtree under the root's right child
+        if ragged and p % 2 and D >= 2:  # a shallower tree: depth-2 subtree under the root's right child
             leaf = leaf | ((idx >= 3) & (idx % 2 == 0))
         r = {"feature": np.where(leaf, -1, rng.integers(0, F, n_nodes)),
-             "threshold": np.where(leaf, 0, rng.integers(0, 4, n_nodes)),
+             "threshold": np.where(leaf, 0, rng.integers(0, max_thr + 1, n_nodes)),
              "left": np.where(leaf, -1, 2 * idx + 1), "right": np.where(leaf, -1, 2 * idx + 2),
              "value": np.where(leaf, rng.normal(0.0, 0.01, n_nodes), 0.0), "is_leaf": leaf}
         rounds.append(r)
@@ -72,6 +72,46 @@ def test_compiled_forest(hip, oracle_mod, monkeypatch, ragged, tile):
     else:
         np.testing.assert_array_equal(got, ref.cpu().numpy())
     np.testing.assert_allclose(got, oracle_mod.predict(rounds, B, 0.5, bins), rtol=0, atol=1e-5)
+    lv = leaves.cpu().numpy() - f["offsets"][:-1].cpu().numpy()[:, None]
+    for r, arrs in enumerate(rounds):
+        want = oracle_mod.leaf_index(arrs, bins)
+        for t in range(B):
+            np.testing.assert_array_equal(lv[r * B + t], want)
+    cf.close()
+
+
+@pytest.mark.parametrize("D,F,max_thr,odd_ld", [
+    (0, 7, 3, False), (1, 40, 3, False), (2, 300, 6, True), (3, 300, 14, False),
+    (4, 1000, 14, False), (5, 700, 200, False), (7, 2376, 255, False), (8, 90, 3, False)])
+def test_forest_shapes(hip, oracle_mod, D, F, max_thr, odd_ld):
+    """The tiled walk at every depth it serves (0-8), all three tile packings (3 bits for
+    thresholds < 7, 4 bits < 15, else 8), 64- and 32-row tiles (2376 features at 8 bits do not
+    fit two 64-row tiles per CU), a tree count that leaves the last tree block part-filled, and
+    an odd row stride (the per-row walk then serves the call): predictions within 1e-5 of the
+    oracle, leaf indices bit-exact."""
+    import torch
+
+    from packboost_amd.booster import pack_forest
+    from packboost_amd.predictor import CompiledForest
+
+    N, B = 3001, 4
+    packs = 13 if D <= 6 else 3
+    print(f"[forest-shape] D={D} F={F} max_thr={max_thr} odd_ld={odd_ld}", flush=True)
+    rounds = _forest(11 + D, packs, B, D, F, ragged=True, max_thr=max_thr)
+    rng = np.random.default_rng(12 + D)
+    bins = rng.integers(0, min(max_thr + 2, 256), size=(N, F)).astype(np.uint8)
+    dev = torch.device("cuda")
+    ld = N if odd_ld else (N + 15) // 16 * 16
+    bfm = torch.zeros((F, ld), dtype=torch.uint8, device=dev)
+    bfm[:, :N] = torch.from_numpy(np.ascontiguousarray(bins.T)).to(dev)
+    f = pack_forest(rounds, B, dev)
+    T = int(f["offsets"].numel() - 1)
+    cf = CompiledForest(f)
+    leaves = torch.empty((T, N), dtype=torch.int32, device=dev)
+    got = cf.predict(bfm, N, 0.25, leaves=leaves).cpu().numpy()
+    np.testing.assert_allclose(got, oracle_mod.predict(rounds, B, 0.25, bins), rtol=0, atol=1e-5)
+    plain = cf.predict(bfm, N, 0.25).cpu().numpy()  # the walk without leaf output
+    np.testing.assert_array_equal(plain, got)
     lv = leaves.cpu().numpy() - f["offsets"][:-1].cpu().numpy()[:, None]
     for r, arrs in enumerate(rounds):
         want = oracle_mod.leaf_index(arrs, bins)
