@@ -274,6 +274,7 @@ struct ForestTile {
     int32_t tile_words;  // dwords of the packed tile
     int32_t tree_block;  // trees per block (forest_tree_block of the depth)
     int32_t blocks;      // tree blocks (the last one padded with trees that add 0)
+    int32_t threads;     // threads per workgroup (256, 512 or 1024)
 };
 ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t depth, int32_t trees);
 size_t forest_tile_lds_bytes(const ForestTile& ft);

@@ -132,8 +132,7 @@ __global__ __launch_bounds__(kBlock) void forest_kernel(
 // leaf), grouped in blocks of TB = forest_tree_block(D) trees of kForestBlockWords dwords:
 // tree k of a block takes dwords k * 2^(D+1) .. (k + 1) * 2^(D+1) - 1, node i (counted from 1,
 // children 2i and 2i + 1) at dword i: the records of its internal nodes (i < 2^D) and the
-// values of its leaves (i >= 2^D); dword 0 is unused, so that both children of a node sit in
-// one aligned 8-byte pair. A record packs the bit position of its feature in its word of a row
+// values of its leaves (i >= 2^D); dword 0 is unused. A record packs the bit position of its feature in its word of a row
 // tile (bits 0-4), the byte offset of that word row in the tile (bits 5-23; a multiple of
 // 4 * rows) and the threshold (bits 24-31). Trees past the forest's last one pad the last
 // block with always-left records and zero leaf values.
@@ -142,34 +141,30 @@ __global__ __launch_bounds__(kBlock) void forest_kernel(
 // is clamped, which changes no comparison; else 8) and row-interleaved: word (j, r) holds the
 // features of word j of row r, so the rows of a word sit in distinct banks and any mix of
 // features reads without bank conflicts. The tree blocks then pass through LDS in turn (each
-// thread copies four dwords per 1024 of the next block into registers while the current block
-// is walked), and 256 / R tree streams (a lane per row) walk them, G trees per lane at once:
-// every load of the walk is an LDS load. Per level a lane reads the bin word of its node and
-// both children's records (one 8-byte read), and the comparison picks the child. Each stream
-// adds float32(weight * leaf value) of its trees in double; the streams' sums are added in a
-// fixed order and rounded once to float32.
+// thread copies its share of the next block into registers while the current block is
+// walked), and NT / R tree streams (a lane per row) walk them, G trees per lane at once: every
+// load of the walk is an LDS load. Per level a lane reads the bin word of its node, compares,
+// and reads the chosen child's record (five VALU instructions per node). Each stream adds
+// float32(weight * leaf value) of its trees in double; the streams' sums are added in a fixed
+// order and rounded once to float32.
 
 typedef __attribute__((address_space(3))) uint32_t lds_word;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte copies of tree blocks
 
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) u32x2 lds_pair;
 
 // LDS dword at byte address `a` of the kernel's (only) LDS allocation.
 __device__ __forceinline__ uint32_t lds_at(uint32_t a) { return *reinterpret_cast<const lds_word*>((size_t)a); }
-// LDS dwords a and a + 4 (a a multiple of 8) in one 64-bit read.
-__device__ __forceinline__ u32x2 lds_pair_at(uint32_t a) { return *reinterpret_cast<const lds_pair*>((size_t)a); }
 
 // Bins of rows r0 .. r0 + R - 1 into the packed, row-interleaved tile. The rows are read four
 // at a time as one dword per feature column, which the caller allows by a row stride that is
 // a multiple of 4 (and 4-byte aligned columns): rows past the column's end read as 0.
-template <int BITS>
+template <int BITS, int NT>
 __device__ __forceinline__ void stage_tile(const uint8_t* __restrict__ bins, int64_t ld, const ForestTile& ft,
                                            int64_t r0, int R, uint32_t* tile) {
     constexpr int PW = 32 / BITS;
     constexpr uint32_t kClamp = (1u << BITS) - 1u;
     const int words = ft.tile_words / R;
-    for (int idx = threadIdx.x; idx < words * (R / 4); idx += kBlock) {
+    for (int idx = threadIdx.x; idx < words * (R / 4); idx += NT) {
         const int j = idx / (R / 4);
         const int q = idx - j * (R / 4);
         const int64_t rr = r0 + 4 * q;
@@ -195,35 +190,42 @@ __device__ __forceinline__ void stage_tile(const uint8_t* __restrict__ bins, int
     }
 }
 
-// LDS holds the kernel at two workgroups (two waves per SIMD), so the register budget of two
-// waves per SIMD lets every tree of a lane keep its loads in flight.
-template <int D, int R, bool LEAF>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) void forest_tile_kernel(
+// LDS holds the kernel at two workgroups per CU (NT / 128 waves per SIMD), which sets the
+// register budget of a lane: all of it goes to the trees a lane walks at once.
+template <int D, int R, int NT, bool LEAF>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT / 128, NT / 128))) void forest_tile_kernel(
     const uint8_t* __restrict__ bins, int64_t N, int64_t ld, ForestTile ft, const u32x4* __restrict__ blocks,
     const int32_t* __restrict__ lid, int32_t T, float tree_weight, float* __restrict__ out,
     int32_t* __restrict__ leaf) {
     extern __shared__ uint32_t lds[];
     constexpr int NL = 1 << D;
-    constexpr int S = kBlock / R;                 // tree streams
+    constexpr int S = NT / R;                     // tree streams
     constexpr int TB = forest_tree_block(D);      // trees per block
     constexpr int G = TB / S >= 8 ? 8 : (TB / S >= 1 ? TB / S : 1);  // trees a lane walks at once
     static_assert(TB % (S * G) == 0 || TB < S, "a block splits evenly over streams and lanes");
-    constexpr int PER = kForestBlockWords / (4 * kBlock);  // 16-byte copies of a block per thread
-    static_assert(PER * 4 * kBlock == kForestBlockWords, "whole 16-byte copies per thread");
+    constexpr int PER = kForestBlockWords / (4 * NT);  // 16-byte copies of a block per thread
+    static_assert(PER * 4 * NT == kForestBlockWords, "whole 16-byte copies per thread");
+    static_assert(NT * 8 <= kForestBlockWords * 4, "the streams' sums fit the block's LDS");
     const uint32_t bits = (uint32_t)ft.bits;
-    // LDS: the tile, then the current tree block, then the streams' sums [S][R]
+    // LDS: the tile, then the current tree block (at the end, the streams' sums [S][R])
     const uint32_t lds0 = (uint32_t)(size_t)(lds_word*)lds;
     const uint32_t rec_b = lds0 + (uint32_t)ft.tile_words * 4u;
     u32x4* tblock = reinterpret_cast<u32x4*>(lds + ft.tile_words);
-    double* part = reinterpret_cast<double*>(lds + ft.tile_words + kForestBlockWords);
-    const int64_t r0 = (int64_t)blockIdx.x * R;
+    double* part = reinterpret_cast<double*>(lds + ft.tile_words);
+    // workgroups are dealt round-robin over the 8 XCDs: ids w and w + 8 (same XCD, dispatched
+    // one after the other) take neighbouring tiles, whose bins share 128-byte lines when R = 64
+    // (64 bytes per feature column), so that one XCD's L2 fetches each line once. The ids of a
+    // last, partial group of 16 keep their own tile.
+    const int w = blockIdx.x;
+    const int tile = w < (int)(gridDim.x & ~15u) ? (w & ~15) | ((w & 7) << 1) | ((w >> 3) & 1) : w;
+    const int64_t r0 = (int64_t)tile * R;
 
     if (ft.bits == 3)
-        stage_tile<3>(bins, ld, ft, r0, R, lds);
+        stage_tile<3, NT>(bins, ld, ft, r0, R, lds);
     else if (ft.bits == 4)
-        stage_tile<4>(bins, ld, ft, r0, R, lds);
+        stage_tile<4, NT>(bins, ld, ft, r0, R, lds);
     else
-        stage_tile<8>(bins, ld, ft, r0, R, lds);
+        stage_tile<8, NT>(bins, ld, ft, r0, R, lds);
 
     const int row = threadIdx.x & (R - 1);
     // a stream is uniform over a wavefront when R = 64
@@ -235,18 +237,18 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     double acc = 0.0;
     u32x4 pre[PER];
 #pragma unroll
-    for (int k = 0; k < PER; ++k) pre[k] = blocks[threadIdx.x + k * kBlock];
+    for (int k = 0; k < PER; ++k) pre[k] = blocks[threadIdx.x + k * NT];
     for (int b = 0; b < ft.blocks; ++b) {
         __syncthreads();  // the tile is staged; the last block's walks are done
 #pragma unroll
-        for (int k = 0; k < PER; ++k) tblock[threadIdx.x + k * kBlock] = pre[k];
+        for (int k = 0; k < PER; ++k) tblock[threadIdx.x + k * NT] = pre[k];
         __syncthreads();
         {
             // the next block (the last one again after the last: an unconditional load keeps
             // the copies in registers)
             const u32x4* src = blocks + (int64_t)min(b + 1, ft.blocks - 1) * (kForestBlockWords / 4) + threadIdx.x;
 #pragma unroll
-            for (int k = 0; k < PER; ++k) pre[k] = src[k * kBlock];
+            for (int k = 0; k < PER; ++k) pre[k] = src[k * NT];
         }
         for (int k0 = stream; k0 < TB; k0 += S * G) {
             // per tree: i = heap index of the current node counted from 1 (children 2i and
@@ -260,22 +262,21 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             }
 #pragma unroll
             for (int lvl = 0; lvl < D; ++lvl) {
-                // all trees' reads are issued before any result is used, so that a lane keeps
-                // 2G reads in flight instead of waiting on each tree in turn
+                // per level: the bin word of each tree's node, the comparison (right = bin >
+                // threshold as a lane mask; i = i + i + right as one add with carry-in), then
+                // the chosen child's record
                 uint32_t w[G];
-                u32x2 ch[G];
 #pragma unroll
                 for (int g = 0; g < G; ++g) w[g] = lds_at((q[g] & 0x00FFFFE0u) | rowoff);
 #pragma unroll
-                for (int g = 0; g < G; ++g) ch[g] = lvl + 1 < D ? lds_pair_at(base[g] + 8u * i[g]) : u32x2{0u, 0u};
-#pragma unroll
                 for (int g = 0; g < G; ++g) {
-                    // right = bin > threshold as a lane mask; then i = i + i + right (one
-                    // add with carry-in) and q = right ? right child : left child
                     const uint64_t right = __builtin_amdgcn_uicmp(__builtin_amdgcn_ubfe(w[g], q[g], bits), q[g] >> 24, 34);
                     uint64_t co;
                     asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(i[g]), "=s"(co) : "v"(i[g]), "s"(right));
-                    asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(q[g]) : "v"(ch[g].x), "v"(ch[g].y), "s"(right));
+                }
+                if (lvl + 1 < D) {
+#pragma unroll
+                    for (int g = 0; g < G; ++g) q[g] = lds_at(base[g] + 4u * i[g]);
                 }
             }
 #pragma unroll
@@ -288,6 +289,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2, 2))) 
             }
         }
     }
+    __syncthreads();  // every walk of the last block is done: its LDS takes the sums
     part[stream * R + row] = acc;
     __syncthreads();
     if (threadIdx.x < R) {
@@ -304,7 +306,8 @@ hipError_t launch_tile_d(const uint8_t* bins, int64_t N, int64_t ld, const Fores
                          const int32_t* lid, int32_t T, float w, float* out, int32_t* leaf, hipStream_t s) {
     const size_t lds = forest_tile_lds_bytes(ft);
     const int64_t tiles = (N + ft.rows - 1) / ft.rows;
-    if (tiles > INT32_MAX || ft.tree_block != forest_tree_block(D) || (ft.rows != 32 && ft.rows != 64))
+    if (tiles > INT32_MAX || ft.tree_block != forest_tree_block(D) || (ft.rows != 32 && ft.rows != 64) ||
+        (ft.threads != 256 && ft.threads != 512 && ft.threads != 1024))
         return hipErrorInvalidValue;
     auto go = [&](auto kern) -> hipError_t {
         const void* fn = reinterpret_cast<const void*>(kern);
@@ -312,12 +315,20 @@ hipError_t launch_tile_d(const uint8_t* bins, int64_t N, int64_t ld, const Fores
             hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
             if (e != hipSuccess) return e;
         }
-        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(kBlock), lds, s, bins, N, ld, ft,
+        hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(ft.threads), lds, s, bins, N, ld, ft,
                            reinterpret_cast<const u32x4*>(blocks), lid, T, w, out, leaf);
         return hipGetLastError();
     };
-    if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, true>) : go(forest_tile_kernel<D, 32, true>);
-    return ft.rows == 64 ? go(forest_tile_kernel<D, 64, false>) : go(forest_tile_kernel<D, 32, false>);
+    if (ft.threads == 1024) {
+        if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 1024, true>) : go(forest_tile_kernel<D, 32, 1024, true>);
+        return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 1024, false>) : go(forest_tile_kernel<D, 32, 1024, false>);
+    }
+    if (ft.threads == 512) {
+        if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 512, true>) : go(forest_tile_kernel<D, 32, 512, true>);
+        return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 512, false>) : go(forest_tile_kernel<D, 32, 512, false>);
+    }
+    if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 256, true>) : go(forest_tile_kernel<D, 32, 256, true>);
+    return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 256, false>) : go(forest_tile_kernel<D, 32, 256, false>);
 }
 
 int grid_rows(int64_t N) {
@@ -383,12 +394,14 @@ ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t de
         ft.rows = 32;
         ft.tile_words = words * ft.rows;
     }
+    // as many tree streams as keep every stream busy with at least one tree of a block, up to
+    // 1024 threads: the walk is bound by instruction issue and LDS latency, which the waves
+    // of two such workgroups per CU (eight per SIMD) hide
+    ft.threads = std::min(1024, std::max(256, ft.rows * ft.tree_block));
     return ft;
 }
 
-size_t forest_tile_lds_bytes(const ForestTile& ft) {
-    return ((size_t)ft.tile_words + kForestBlockWords) * 4 + (size_t)kBlock * 8;
-}
+size_t forest_tile_lds_bytes(const ForestTile& ft) { return ((size_t)ft.tile_words + kForestBlockWords) * 4; }
 
 uint32_t forest_tile_record(const ForestTile& ft, int32_t feature, int32_t threshold) {
     const int per_word = 32 / ft.bits;
