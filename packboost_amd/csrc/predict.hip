@@ -176,7 +176,9 @@ __device__ __forceinline__ void stage_tile(const uint8_t* __restrict__ bins, int
 #pragma unroll
         for (int k = 0; k < PW; ++k) {
             const int fc = min(j * PW + k, ft.features - 1);
-            d[k] = *reinterpret_cast<const uint32_t*>(bins + (int64_t)fc * ld + rc);
+            // streamed once: a non-temporal load keeps the bins from evicting the tree
+            // blocks, which every tile re-reads, from L2
+            d[k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(bins + (int64_t)fc * ld + rc));
         }
 #pragma unroll
         for (int k = 0; k < PW; ++k) d[k] = (row_ok && j * PW + k < ft.features) ? d[k] : 0u;
