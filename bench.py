@@ -149,11 +149,11 @@ def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None
     }
 
 
-def profiled_traffic(config: int, rows: int) -> float | None:
-    """HBM bytes per hist launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary of
-    this workload (profiles/hist_score_config<N>.md, its `traffic_bytes_per_launch` line), or
-    None when the workload differs from the profiled one."""
-    path = ROOT / "profiles" / f"hist_score_config{config}.md"
+def profiled_traffic(config: int, rows: int, summary: str = "hist_score") -> float | None:
+    """HBM bytes per launch of the line's roofline kernel from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary of this workload (profiles/<summary>_config<N>.md, its
+    `traffic_bytes_per_launch` line), or None when the workload differs from the profiled one."""
+    path = ROOT / "profiles" / f"{summary}_config{config}.md"
     if rows != CONFIGS[config]["rows"] or not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -292,7 +292,8 @@ def bench_predict(args, c: dict) -> int:
         "config": {"workload": f"config5: {N} rows x {F} features, {T} trees of depth {D}"},
         "kernel_ms": round(ms, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(5, N, "predict"),
                      "kernel": "forest_tile_kernel",
                      "algorithmic_bytes": "N*F bin bytes read once + N*4 output (compulsory)"},
     }), flush=True)
