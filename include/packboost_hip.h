@@ -422,6 +422,17 @@ int pb_best_thresholds(const pb_candidate* cand_dev, int32_t M, int32_t K, int32
                        float* scores_dev, int32_t* thresholds_dev, float* left_grad_dev,
                        float* left_hess_dev, int64_t* left_count_dev, void* stream);
 
+/* The per-node pick of find_best_splits_batched_cpu (frontier_cpu.cpp:415-426, the scan that
+ * feeds its decisions at 446-499) over candidate records cand_dev [M][K][T] in its visiting
+ * order (subset feature, then threshold: pb_des_score's cand_all_dev): features and thresholds
+ * are scanned in order and a candidate replaces the best when it scores higher, or scores
+ * within 1e-12 (a float32 difference) and has more left rows, then a larger feature id, then a
+ * larger threshold; candidates with valid == 0 or a NaN score are skipped. out_dev [M]: the
+ * winner (valid = 0, feature = threshold = -1 when the node has none). band_dev: int32
+ * [M][K * T] scratch. */
+int pb_pick_sequential(const pb_candidate* cand_dev, int32_t M, int32_t K, int32_t T, int32_t* band_dev,
+                       pb_candidate* out_dev, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,10 +1,12 @@
 """Backend shim with the reference's names (packboost/backends/__init__.py:9-163).
 
 The reference resolves these names on its pybind11 module; here they are served by
-libpackboost_hip.so through ctypes. There is no CPU compute backend: `cpu_available()` is
-False and `find_best_splits_batched` raises, as the reference does when its CPU build is
-missing (backends/__init__.py:79-87). The "cuda" names keep their spelling for drop-in
-callers and run on the HIP device.
+libpackboost_hip.so through ctypes, and every one of them computes on the HIP device.
+`find_best_splits_batched` keeps the host schema of the reference's CPU splitter (numpy
+inputs, per-node per-era row lists, decision dicts with left/right row lists;
+frontier_cpu.cpp:111-515), so `cpu_available()` reports whether that entry point is served,
+i.e. whether a gfx950 device and the library are present. The "cuda" names keep their spelling
+for drop-in callers.
 """
 
 from __future__ import annotations
@@ -27,11 +29,18 @@ __all__ = [
 
 
 def cpu_available() -> bool:
-    return False
+    """True when the host-schema split finder can run: a gfx950 device and the library."""
+    return _hip.device_available()
 
 
 def find_best_splits_batched(*args: Any, **kwargs: Any):
-    raise RuntimeError("CPU backend is unavailable in this build.")
+    """find_best_splits_batched_cpu's schema on the HIP device (frontier_cpu.cpp:111-515; caller
+    booster.py:1080-1093): (decisions, stats)."""
+    if not _hip.device_available():
+        raise RuntimeError("CPU backend is unavailable in this build.")
+    from .rowlist import find_best_splits_batched_host
+
+    return find_best_splits_batched_host(*args, **kwargs)
 
 
 def cuda_available() -> bool:

@@ -117,12 +117,36 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
                            direction_weight=float(direction_weight), era_alpha=alpha,
                            min_samples_leaf=int(min_samples_leaf), k_cuts=int(k_cuts),
                            cut_selection=1 if str(cut_selection) == "mass" else 0, reserved=0)
+    t0 = time.perf_counter()
+
+    def consume(m0, U, mx, cand, cnt, gp):
+        _hip.check(lib.pb_best_thresholds(cand.data_ptr(), U, K, T, out_s[m0].data_ptr(),
+                                          out_t[m0].data_ptr(), out_g[m0].data_ptr(),
+                                          out_h[m0].data_ptr(), out_c[m0].data_ptr(), _hip.stream_ptr()),
+                   "pb_best_thresholds")
+
+    _score_node_chunks(lib, b_fm, F, N, ld_in, fid, fid, K, vals, rows, R, nrs, nes, M, E, nb, T, p,
+                       _NODE_CHUNK, consume, "find_best_splits_batched_cuda")
+    kernel_ms = (time.perf_counter() - t0) * 1e3
+    return {"scores": out_s, "thresholds": out_t, "left_grad": out_g, "left_hess": out_h,
+            "left_count": out_c, "kernel_ms": kernel_ms}
+
+
+def _score_node_chunks(lib, b_fm, F, N, ld_in, fid_gather, fid_score, K, vals, rows, R, nrs, nes, M, E, nb, T,
+                       p, chunk, consume, what, times=None):
+    """For nodes [m0, m0 + chunk) at a time: pb_rowlist_gather of their listed rows (feature
+    columns fid_gather of b_fm), pb_round_begin / pb_hist_build / pb_des_score over them (the
+    candidates' feature ids are fid_score), then consume(m0, U, max_nodes, cand, cnt, gp) with
+    the candidate records [max_nodes][K][T] and the histogram planes, before the chunk's
+    context is released. Chunks whose lists hold no row are skipped. `times` (optional dict)
+    accumulates the milliseconds of gather + histogram ("hist_ms") and of the scorer
+    ("score_ms"), from HIP events."""
+    dev = b_fm.device
     # rows listed per node (the gather places exactly these when the segments are consistent)
     node_rows = (nes[:, E] - nes[:, 0]).to(torch.int64).clamp_min(0).cpu()
     s = _hip.stream_ptr()
-    t0 = time.perf_counter()
-    for m0 in range(0, M, _NODE_CHUNK):
-        m1 = min(M, m0 + _NODE_CHUNK)
+    for m0 in range(0, M, chunk):
+        m1 = min(M, m0 + chunk)
         U = m1 - m0
         cap = int(node_rows[m0:m1].sum())
         if cap == 0:
@@ -133,11 +157,14 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
         nid = torch.full((ld,), -1, dtype=torch.int16, device=dev)  # 0xFFFF: rows in no node
         era_off_dev = torch.empty(E + 1, dtype=torch.int32, device=dev)
         work = torch.empty(int(lib.pb_rowlist_work_elems(U, E)), dtype=torch.int32, device=dev)
-        _hip.check(lib.pb_rowlist_gather(b_fm.data_ptr(), N, ld_in, F, fid.data_ptr(), K, vals.data_ptr(),
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)] if times is not None else None
+        if ev:
+            ev[0].record()
+        _hip.check(lib.pb_rowlist_gather(b_fm.data_ptr(), N, ld_in, F, fid_gather.data_ptr(), K, vals.data_ptr(),
                                          rows.data_ptr(), R, nrs.data_ptr(), nes.data_ptr(), m0, m1, E,
                                          b.data_ptr(), ld, preds.data_ptr(), nid.data_ptr(),
                                          era_off_dev.data_ptr(), work.data_ptr(), s), "pb_rowlist_gather")
-        _check_status(work, "find_best_splits_batched_cuda")
+        _check_status(work, what)
         era_off = np.ascontiguousarray(era_off_dev.cpu().numpy())
         Rc = int(era_off[E])
         if Rc == 0:
@@ -168,18 +195,20 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
                                          local.data_ptr(), K, depth, mx, cnt.data_ptr(), gp.data_ptr(),
                                          s), "pb_hist_build")
             cand = torch.empty(mx * K * T * _hip.CANDIDATE_DTYPE.itemsize, dtype=torch.uint8, device=dev)
-            _hip.check(lib.pb_des_score(ctx, cnt.data_ptr(), gp.data_ptr(), fid.data_ptr(), K, depth,
+            if ev:
+                ev[1].record()
+            _hip.check(lib.pb_des_score(ctx, cnt.data_ptr(), gp.data_ptr(), fid_score.data_ptr(), K, depth,
                                         mx, ctypes.byref(p), cand.data_ptr(), s), "pb_des_score")
-            _hip.check(lib.pb_best_thresholds(cand.data_ptr(), U, K, T, out_s[m0].data_ptr(),
-                                              out_t[m0].data_ptr(), out_g[m0].data_ptr(),
-                                              out_h[m0].data_ptr(), out_c[m0].data_ptr(), s),
-                       "pb_best_thresholds")
+            if ev:
+                ev[2].record()
+            consume(m0, U, mx, cand, cnt, gp)
+            if ev:
+                torch.cuda.synchronize(dev)
+                times["hist_ms"] = times.get("hist_ms", 0.0) + ev[0].elapsed_time(ev[1])
+                times["score_ms"] = times.get("score_ms", 0.0) + ev[1].elapsed_time(ev[2])
         finally:
             torch.cuda.synchronize(dev)
             lib.pb_ctx_destroy(ctx)
-    kernel_ms = (time.perf_counter() - t0) * 1e3
-    return {"scores": out_s, "thresholds": out_t, "left_grad": out_g, "left_hess": out_h,
-            "left_count": out_c, "kernel_ms": kernel_ms}
 
 
 def partition_frontier_rowlist(bins, rows_index, node_row_splits, node_era_splits, feat_per_node,
@@ -214,3 +243,169 @@ def partition_frontier_rowlist(bins, rows_index, node_row_splits, node_era_split
     _check_status(work, "partition_frontier_cuda")
     nl, nr = int(ls[-1, -1]), int(rs[-1, -1])
     return {"left_index": left[:nl], "right_index": right[:nr], "left_splits": ls, "right_splits": rs}
+
+
+_STATS_ZERO = {"nodes_processed": 0, "nodes_skipped": 0, "rows_total": 0, "feature_blocks": 0,
+               "bincount_calls": 0, "hist_ms": 0.0, "scan_ms": 0.0, "score_ms": 0.0, "partition_ms": 0.0,
+               "nodes_subtract_ok": 0, "nodes_subtract_fallback": 0, "nodes_rebuild": 0, "block_size": 0}
+_HOST_CHUNK = 1 << 15  # nodes per HIP context (frontier depth 15): one chunk for any real frontier
+
+
+def find_best_splits_batched_host(bins, grad, nodes_era_rows, feature_subset, max_bins, k_cuts, cut_selection,
+                                  lambda_l2, lambda_dro, direction_weight, era_alpha, min_samples_leaf):
+    """find_best_splits_batched_cpu (frontier_cpu.cpp:111-515) with its host schema, computed on
+    the HIP device: bins int8 [N, F] (rows, features), grad float32 [N], nodes_era_rows a list
+    (per node) of lists (per era) of row-id arrays, feature_subset int32 [K]. Returns
+    (decisions, stats): decisions[i] is None for a node without a valid split (or without rows),
+    else a dict of feature, threshold, score, left/right grad and hess, left/right count and
+    left_rows / right_rows (per era, int64 row ids in list order); stats the reference's keys
+    (booster.py:1094-1110), its timings measured here with HIP events per phase.
+
+    The listed rows of the subset's columns go to the device once per call; gather, histogram,
+    scorer, sequential pick and partition are the HIP kernels (pb_rowlist_gather, pb_hist_build,
+    pb_des_score, pb_pick_sequential, pb_rowlist_partition). Differences from the reference:
+    a node's left/right sums come from exact fixed-point histograms rounded once to float32
+    (the reference adds float32 in row order); every node must list the same number of eras;
+    bins >= max_bins raise ValueError (the reference skips such rows in the histogram); mass
+    K-cuts are taken over the whole call up to 32768 nodes."""
+    lib = _hip.load()
+    bins_np = np.asarray(bins)
+    grad_np = np.asarray(grad, dtype=np.float32)
+    if bins_np.ndim != 2:
+        raise ValueError("bins must be 2D (rows, features)")
+    if grad_np.ndim != 1:
+        raise ValueError("grad must be 1D")
+    N, F = int(bins_np.shape[0]), int(bins_np.shape[1])
+    if grad_np.shape[0] != N:
+        raise ValueError("grad length must match bins rows")
+    nb = max(1, int(max_bins))
+    n_in = len(nodes_era_rows)
+    index_map, node_lists, rows_total = [], [], 0
+    for idx in range(n_in):
+        item = nodes_era_rows[idx]
+        if not isinstance(item, list):
+            raise ValueError("Each node entry must be a list of era row arrays")
+        if len(item) == 0:
+            continue
+        arrs = []
+        for e in item:
+            a = np.asarray(e)
+            if a.ndim != 1:
+                raise ValueError("era row array must be 1D")
+            a = a.astype(np.int64, copy=False)
+            if a.size and (int(a.min()) < 0 or int(a.max()) >= N):
+                raise IndexError("row index out of bounds")
+            arrs.append(a)
+        cnt = sum(int(a.size) for a in arrs)
+        if cnt == 0:
+            continue
+        rows_total += cnt
+        index_map.append(idx)
+        node_lists.append(arrs)
+    stats = dict(_STATS_ZERO)
+    decisions = [None] * n_in
+    stats["rows_total"] = rows_total
+    stats["nodes_skipped"] = n_in - len(index_map)
+    M = len(index_map)
+    if M == 0:
+        return decisions, stats
+    feats = np.asarray(feature_subset)
+    if feats.ndim != 1:
+        raise ValueError("feature_subset must be 1D")
+    feats = feats.astype(np.int32, copy=False)
+    K = int(feats.shape[0])
+    if K and (int(feats.min()) < 0 or int(feats.max()) >= F):
+        raise IndexError("feature index out of range")
+    E = len(node_lists[0])
+    if any(len(a) != E for a in node_lists):
+        raise ValueError("every node must list the same number of eras")
+    stats.update(nodes_processed=M, feature_blocks=1 if K else 0, bincount_calls=2 if K else 0,
+                 nodes_subtract_ok=M, block_size=K)
+    if K == 0:
+        return decisions, stats
+    if not 2 <= nb <= 255:
+        raise ValueError("max_bins must lie in [2, 255]")
+    sub = np.ascontiguousarray(bins_np[:, feats]).astype(np.int8, copy=False).view(np.uint8)  # [N, K]
+    if int(sub.max()) >= nb:
+        raise ValueError("bins >= max_bins are not supported by the HIP backend")
+    dev = torch.device("cuda")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]  # around the partition
+    b_fm = torch.from_numpy(sub).to(dev).t().contiguous()  # [K, N] feature-major
+    flat = [a for arrs in node_lists for a in arrs]
+    sizes = np.array([a.size for a in flat], dtype=np.int64).reshape(M, E)
+    # the CUDA path's list layout: node_row_splits absolute, node_era_splits relative to the node
+    nes_np = np.zeros((M, E + 1), dtype=np.int64)
+    nes_np[:, 1:] = np.cumsum(sizes, axis=1)
+    nrs_np = np.zeros(M + 1, dtype=np.int64)
+    nrs_np[1:] = np.cumsum(sizes.sum(axis=1))
+    R = int(nrs_np[-1])
+    if R >= 2 ** 31:
+        raise ValueError("more than 2^31 - 1 listed rows")
+    rows = torch.from_numpy(np.concatenate(flat).astype(np.int32)).to(dev)
+    nes = torch.from_numpy(nes_np.astype(np.int32)).to(dev)
+    nrs = torch.from_numpy(nrs_np.astype(np.int32)).to(dev)
+    vals = torch.from_numpy(grad_np).to(dev)[rows.long()]  # per list position, as the gather reads
+    fid = torch.from_numpy(feats).to(dev)
+    local = torch.arange(K, dtype=torch.int32, device=dev)
+    T = k_cuts if 0 < int(k_cuts) < nb - 1 else nb - 1
+    p = _hip.PbSplitParams(lambda_l2=float(lambda_l2), lambda_dro=float(lambda_dro),
+                           direction_weight=float(direction_weight), era_alpha=max(0.0, float(era_alpha)),
+                           min_samples_leaf=int(min_samples_leaf), k_cuts=int(k_cuts),
+                           cut_selection=1 if str(cut_selection) == "mass" else 0, reserved=0)
+    win = torch.zeros(M * _hip.CANDIDATE_DTYPE.itemsize, dtype=torch.uint8, device=dev)  # valid = 0
+    tot_g = np.zeros((M, E), dtype=np.float32)
+    sc_ms = [0.0]
+
+    def consume(m0, U, mx, cand, cnt, gp):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        band = torch.empty(U * K * T, dtype=torch.int32, device=dev)
+        _hip.check(lib.pb_pick_sequential(cand.data_ptr(), U, K, T, band.data_ptr(),
+                                          win.data_ptr() + m0 * _hip.CANDIDATE_DTYPE.itemsize,
+                                          _hip.stream_ptr()), "pb_pick_sequential")
+        e1.record()
+        # era totals [E][mx] after the prefix planes (pb_hist_build's layout)
+        off = (E * mx * K * (nb - 1) + 63) // 64 * 64
+        tot_g[m0:m0 + U] = gp[off:off + E * mx].view(E, mx)[:, :U].t().cpu().numpy()
+        sc_ms[0] += e0.elapsed_time(e1)
+
+    times = {}
+    _score_node_chunks(lib, b_fm, K, N, int(b_fm.stride(0)), local, fid, K, vals, rows, R, nrs, nes, M, E, nb, T,
+                       p, _HOST_CHUNK, consume, "find_best_splits_batched", times)
+    w = np.frombuffer(win.cpu().numpy().tobytes(), dtype=_hip.CANDIDATE_DTYPE)
+    split = w["valid"] != 0
+    # partition every node (nodes without a split go all left and are not read)
+    f_loc = np.zeros(M, dtype=np.int32)
+    t_loc = np.full(M, 255, dtype=np.int32)
+    if split.any():
+        where = {int(f): i for i, f in enumerate(feats.tolist())}  # first subset slot of a feature id
+        f_loc[split] = [where[int(f)] for f in w["feature"][split]]
+        t_loc[split] = w["threshold"][split]
+    ev[0].record()
+    part = partition_frontier_rowlist(b_fm, rows, nrs, nes, torch.from_numpy(f_loc), torch.from_numpy(t_loc))
+    ev[1].record()
+    torch.cuda.synchronize(dev)
+    left = part["left_index"].cpu().numpy().astype(np.int64)
+    right = part["right_index"].cpu().numpy().astype(np.int64)
+    ls = part["left_splits"].cpu().numpy().astype(np.int64)
+    rs = part["right_splits"].cpu().numpy().astype(np.int64)
+    for j in range(M):
+        if not split[j]:
+            continue
+        total_count = int(sizes[j].sum())
+        total_grad = np.cumsum(tot_g[j], dtype=np.float32)[-1]  # float32 era-order sum, as the reference
+        lg = np.float32(w["left_grad"][j])
+        lc = int(w["left_total"][j])
+        lh = np.float32(lc)
+        decisions[index_map[j]] = {
+            "feature": int(w["feature"][j]), "threshold": int(w["threshold"][j]), "score": float(w["score"][j]),
+            "left_grad": float(lg), "left_hess": float(lh), "right_grad": float(np.float32(total_grad - lg)),
+            "right_hess": float(np.float32(np.float32(total_count) - lh)), "left_count": lc,
+            "right_count": total_count - lc,
+            "left_rows": [left[ls[j, e]:ls[j, e + 1]] for e in range(E)],
+            "right_rows": [right[rs[j, e]:rs[j, e + 1]] for e in range(E)],
+        }
+    stats["hist_ms"] = times.get("hist_ms", 0.0)
+    stats["score_ms"] = times.get("score_ms", 0.0) + sc_ms[0]
+    stats["partition_ms"] = ev[0].elapsed_time(ev[1])
+    return decisions, stats

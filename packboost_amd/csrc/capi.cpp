@@ -1153,4 +1153,15 @@ int pb_best_thresholds(const pb_candidate* cand, int32_t M, int32_t K, int32_t T
     return PB_OK;
 }
 
+int pb_pick_sequential(const pb_candidate* cand, int32_t M, int32_t K, int32_t T, int32_t* band, pb_candidate* out,
+                       void* stream) {
+    if (M < 0 || K < 0 || T < 0) return fail(PB_ERR_INVALID, "pb_pick_sequential: negative size");
+    if (M == 0) return PB_OK;
+    if (!out || ((int64_t)K * T > 0 && (!cand || !band)))
+        return fail(PB_ERR_INVALID, "pb_pick_sequential: null argument");
+    PB_HIP(pb::launch_pick_sequential(cand, M, (int64_t)K * T, band, out, (hipStream_t)stream),
+           "sequential pick launch");
+    return PB_OK;
+}
+
 }  // extern "C"

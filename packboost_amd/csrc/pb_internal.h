@@ -201,6 +201,10 @@ hipError_t launch_decide(const DecideCands& dc, int32_t max_nodes, const NodeTot
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
                          hipStream_t s);
+// One winner per node of candidate records [M][n] in visiting order, by the reference's
+// sequential scan (band: int32 [M][n] scratch).
+hipError_t launch_pick_sequential(const pb_candidate* cand, int32_t M, int64_t n, int32_t* band,
+                                  pb_candidate* out, hipStream_t s);
 hipError_t launch_select_subsets(const pb_round_header* prev, int32_t D, int32_t K,
                                  const int32_t* window, int32_t* feats, hipStream_t s);
 hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,

@@ -1211,6 +1211,71 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(DecideCands dc, int32_t 
     }
 }
 
+// The sequential pick of sequential_pick for plain candidate records (pb_candidate [M][n] in
+// visiting order: the cand_all output of the scorer): one wavefront per node finds the highest
+// score M among the candidates the reference can take (valid, not NaN, above -inf), then
+// replays the reference's scan (frontier_cpu.cpp:415-426) over the band of candidates near M,
+// compacted in order into `band` ([M][n] scratch). A node without such a candidate gets
+// valid = 0, feature = threshold = -1.
+__global__ __launch_bounds__(kBlock) void pick_sequential_kernel(const pb_candidate* __restrict__ cand, int32_t M,
+                                                                 int64_t n, int32_t* __restrict__ band_all,
+                                                                 pb_candidate* __restrict__ out) {
+    const int lane = (int)(threadIdx.x & (kWave - 1));
+    const int u = (int)blockIdx.x * (kBlock / kWave) + (int)(threadIdx.x / kWave);
+    if (u >= M) return;  // wave-uniform
+    const pb_candidate* c = cand + (int64_t)u * n;
+    float top = -INFINITY;
+    for (int64_t i = lane; i < n; i += kWave) {
+        const float sv = c[i].score;
+        top = (c[i].valid != 0 && sv > top) ? sv : top;  // NaN never compares above
+    }
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) top = fmaxf(top, __shfl_xor(top, m));
+    Cand cur;
+    cur.score = -INFINITY;
+    cur.lt = -1;
+    cur.lg = 0.0f;
+    cur.f = -1;
+    cur.thr = -1;
+    cur.valid = 0;
+    if (top > -INFINITY) {  // wave-uniform
+        const double Mx = (double)top;
+        double w = 0.0;
+        for (int k = 6;; ++k) {
+            w = ldexp(kTieBand0, k - 6);
+            int64_t cnt = 0;
+            for (int64_t i = lane; i < n; i += kWave) cnt += (c[i].valid != 0 && (double)c[i].score >= Mx - w) ? 1 : 0;
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) cnt += __shfl_xor(cnt, m);
+            if (cnt < (int64_t(1) << k) || (int64_t(1) << k) > n) break;
+        }
+        int32_t* band = band_all + (int64_t)u * n;
+        int64_t pos = 0;
+        for (int64_t b0 = 0; b0 < n; b0 += kWave) {
+            const int64_t i = b0 + lane;
+            const bool in = i < n && c[i].valid != 0 && (double)c[i].score >= Mx - w;
+            const unsigned long long msk = __ballot(in);
+            if (in) band[pos + __popcll(msk & ((1ull << lane) - 1ull))] = (int32_t)i;
+            pos += __popcll(msk);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) {
+            bool started = false;
+            for (int64_t j = 0; j < pos; ++j) {
+                const Cand cj = load_cand(c + band[j]);
+                const bool first = !started && ((double)cj.score == Mx);
+                const bool s_gt = cj.score > cur.score;
+                const bool near = fabsf(cj.score - cur.score) <= 1e-12f;
+                const bool tie_win = (cj.lt > cur.lt) | ((cj.lt == cur.lt) & ((cj.f > cur.f) | ((cj.f == cur.f) & (cj.thr > cur.thr))));
+                const bool take = first | (started & (s_gt | (near & tie_win)));
+                take_if(take, cj, cur);
+                started = started | first;
+            }
+        }
+    }
+    if (lane == 0) store_cand(out + u, cur);
+}
+
 }  // namespace
 
 ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t target_wgs) {
@@ -1292,6 +1357,15 @@ hipError_t launch_decide(const DecideCands& dc, int32_t max_nodes, const NodeTot
     }
     hipLaunchKernelGGL(decide_kernel, dim3(1), dim3(kBlock), 0, s, dc, w_decide, ntot, st, depth,
                        msl, lambda_l2, cur_ids, next_ids, rules, dec, values, node_best);
+    return hipGetLastError();
+}
+
+hipError_t launch_pick_sequential(const pb_candidate* cand, int32_t M, int64_t n, int32_t* band,
+                                  pb_candidate* out, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    const int per_block = kBlock / kWave;
+    hipLaunchKernelGGL(pick_sequential_kernel, dim3((M + per_block - 1) / per_block), dim3(kBlock), 0, s, cand, M,
+                       n, band, out);
     return hipGetLastError();
 }
 
