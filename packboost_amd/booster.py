@@ -327,7 +327,10 @@ class PackBoost:
         return self
 
     def predict(self, X) -> np.ndarray:
-        """Sum over all trees in order of float32(tree_weight * leaf value) (booster.py:709-712)."""
+        """Sum over all trees of float32(tree_weight * leaf value) (booster.py:658-712), on the
+        compiled forest's tiled walk: the sums are taken in double and rounded once, so they lie
+        within float32 rounding of any of the reference's summation orders (its CPU path adds
+        tree by tree in float32, its CUDA path pack by pack)."""
         if self._binner is None:
             raise RuntimeError("Model must be fitted before predict()")
         _require_backend(self._device)
