@@ -93,8 +93,9 @@ typedef struct {
 } pb_decision;
 
 /* Candidate record (one per wavefront winner, or per lane when dumped for tests). In a
- * wavefront winner, reserved[0] counts that wavefront's valid candidates scoring within
- * 64e-12 of the winner (the decision step's tie-band bound); elsewhere it is 0. */
+ * wavefront winner, reserved[0] counts that wavefront's valid candidates scoring below the
+ * winner but within 64e-12 of it (the decision step replays the reference's sequential scan
+ * only when such candidates exist near the node's top score); elsewhere it is 0. */
 typedef struct {
     float score;
     int32_t left_total;

@@ -100,11 +100,13 @@ __device__ __forceinline__ Cand load_cand(const pb_candidate* src) {
 constexpr double kTieBand0 = 64.0e-12 * (1.0 + 1.0e-6);
 
 // After the wavefront argmax (`win`, held by every lane): how many of the wavefront's valid
-// candidates (own score `mine`, -inf if invalid) score within kTieBand0 of its winner. Stored
-// with the winner, it bounds the node's tie band in the decision step: when the node's band
-// can hold only its best candidate, the sequential pick is the strict argmax.
+// candidates (own score `mine`, -inf if invalid) score below its winner but within kTieBand0
+// of it. Stored with the winner, it tells the decision step whether the node's tie band holds
+// any score other than the top one: when every candidate within kTieBand0 of the top score M
+// scores exactly M, the sequential scan takes only score-M candidates after the first one, by
+// the order (left count, feature, threshold), and that is the strict argmax.
 __device__ __forceinline__ int wave_band_count(const Cand& win, float mine) {
-    const bool near = win.valid && (double)mine >= (double)win.score - kTieBand0;
+    const bool near = win.valid && mine < win.score && (double)mine >= (double)win.score - kTieBand0;
     return __popcll(__ballot(near));
 }
 
@@ -1031,17 +1033,20 @@ __device__ void sequential_pick(const DecideCands& dc, int u, Cand& best) {
     }
 }
 
-// Upper bound on the node's candidates within kTieBand0 of its best score M: the wavefront
-// band counts of the winners whose own score is that close (a candidate in the node's band is
-// in its wavefront's band, since that wavefront's winner scores between it and M). Summed by
-// the calling threads over winners w0, w0 + step, ...
+// Candidates of the node scoring below its best score M but within kTieBand0 of it, as far
+// as the wavefront winners show them: a winner in [M - kTieBand0, M) is one, and a winner
+// scoring M brings its wavefront's count of such candidates (a candidate in that band belongs
+// to a wavefront whose winner scores between it and M, so none is missed). Zero means the
+// strict argmax is the sequential pick. Summed by the calling threads over winners w0,
+// w0 + step, ...
 __device__ __forceinline__ int band_bound_part(const DecideCands& dc, int u, int W, int w0, int step,
                                                const Cand& best) {
     int n = 0;
     if (!best.valid) return 0;
     for (int w = w0; w < W; w += step) {
         const pb_candidate* r = dc.cand_w + (int64_t)u * W + w;
-        if (r->valid && (double)r->score >= (double)best.score - kTieBand0) n += r->reserved[0];
+        if (r->valid && (double)r->score >= (double)best.score - kTieBand0)
+            n += (r->score < best.score ? 1 : 0) + r->reserved[0];
     }
     return n;
 }
@@ -1082,7 +1087,7 @@ __global__ __launch_bounds__(kBlock) void node_best_kernel(DecideCands dc, const
     if (wave == 0) {
         int nb = 0;
         for (int i = 0; i < kBlock / kWave; ++i) nb += s_band[i];
-        if (nb > 1) sequential_pick(dc, u, best);
+        if (nb > 0) sequential_pick(dc, u, best);
         if (lane == 0) store_cand(node_best + u, best);
     }
 }
@@ -1117,7 +1122,7 @@ __global__ __launch_bounds__(kBlock) void decide_kernel(DecideCands dc, int32_t 
         int band = band_bound_part(dc, u, W, lane, kWave, best);
 #pragma unroll
         for (int m = 1; m < kWave; m <<= 1) band += __shfl_xor(band, m);
-        if (band > 1) sequential_pick(dc, u, best);
+        if (band > 0) sequential_pick(dc, u, best);
         if (lane == 0) store_cand(node_best + u, best);
     }
     if (threadIdx.x == 0) {
