@@ -385,6 +385,7 @@ struct EraBatch {
     float GL[kWidePf];
     int ct;
     float Gt;
+    float parent;  // lane j: 0.5 * Gt^2 / (ct + lambda) of era e0 + j, 0 without rows
 };
 
 template <bool C32>
@@ -422,6 +423,7 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
             b.ct = a.tot_cnt[to];
             b.Gt = a.tot_g[to];
         }
+        b.parent = 0.0f;
 #pragma unroll
         for (int j = 0; j < kWidePf; ++j) {
             b.L[j] = 0;
@@ -432,6 +434,13 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
                 b.GL[j] = a.g[off];
             }
         }
+    };
+
+    // the parent term of era e0 + lane, once per era (lanes 0 .. kWidePf - 1), after the
+    // batch's totals have arrived
+    auto parents = [&](EraBatch& b) {
+        const float pden = (float)b.ct + lam;
+        b.parent = (b.ct != 0 && pden > 0.0f) ? (0.5f * (b.Gt * b.Gt)) / pden : 0.0f;
     };
 
     float wsum = 0.0f, mean = 0.0f, M2 = 0.0f, agn = 0.0f, agd = 0.0f, lg = 0.0f, tg = 0.0f;
@@ -451,8 +460,7 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
         if (w > 0.0f) {
             const float dL = (float)L + lam;
             const float dR = (float)R + lam;
-            const float pden = (float)ctot + lam;
-            const float parent = (pden > 0.0f) ? (0.5f * (Gt * Gt)) / pden : 0.0f;
+            const float parent = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(b.parent), j));
             gain = 0.5f * ((GL * GL) / dL + (GR * GR) / dR) - parent;
             if (use_dir) {
                 const float lv = -GL / dL;
@@ -484,9 +492,11 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
     load(0, ba);
     for (int e0 = 0; e0 < E; e0 += 2 * kWidePf) {
         load(e0 + kWidePf, bb);
+        parents(ba);
 #pragma unroll
         for (int j = 0; j < kWidePf; ++j) step(ba, j);
         load(e0 + 2 * kWidePf, ba);
+        parents(bb);
 #pragma unroll
         for (int j = 0; j < kWidePf; ++j) step(bb, j);
     }
