@@ -387,10 +387,13 @@ def main() -> int:
     phase_ms = {name: float(phase_raw[i].sum()) for i, name in
                 enumerate(("hist", "score", "decide", "partition"))}
     hist_bytes = 0.0
+    # a segment-mode fit builds no planes from its first fused depth on: those depths' fused
+    # histogram + scorer launches are not part of this histogram roofline
+    hist_depths = fit.seg_from if fit.segments else D
     for r, log in enumerate(logs):
         if r % PROFILE_EVERY:
             continue
-        for d in range(D):
+        for d in range(hist_depths):
             u = int(log.u_active[d])
             if u == 0:
                 continue
@@ -398,8 +401,8 @@ def main() -> int:
             rows = int(log.decisions[base: base + u]["node_count"].astype(np.int64).sum())
             hist_bytes += rows * K + rows * 8 + u * E * K * nb * 8
             moved_bytes += rows * K * bin_bytes + rows * 6 + u * E * (K * (nb - 1) * 6 + 8)
-    hist_ms = float(prof_ms[0].sum())
-    n_hist = int(prof_n[0].sum())
+    hist_ms = float(prof_ms[0][:hist_depths].sum())
+    n_hist = int(prof_n[0][:hist_depths].sum())
     achieved = moved_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     ref_format_gbs = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     rounds_per_s = args.steps / elapsed
@@ -426,6 +429,7 @@ def main() -> int:
                          f"{c['bins']} bins, B={c['pack_size']}, D={c['max_depth']}, K={K}/depth"),
             "rows": N, "features": c["features"], "eras": c["eras"], "max_bins": c["bins"],
             "pack_size": c["pack_size"], "max_depth": c["max_depth"], "features_per_depth": K,
+            "fit_mode": (f"segments (fused from depth {fit.seg_from})" if fit.segments else "planes"),
             "parallelism": "single GPU",
         },
         "roofline": {

@@ -35,7 +35,7 @@ EXPORTED_SYMBOLS = (
     "pb_predict_forest", "pb_predict_bins", "pb_era_corr", "pb_quantile_edges", "pb_apply_bins",
     "pb_forest_create", "pb_forest_predict", "pb_forest_destroy", "pb_pack_bins4",
     "pb_set_bin_layout", "pb_select_subsets", "pb_rowlist_work_elems", "pb_rowlist_partition",
-    "pb_rowlist_gather", "pb_best_thresholds", "pb_pick_sequential", "pb_rowlist_noalloc_max_segments",
+    "pb_rowlist_gather", "pb_best_thresholds", "pb_pick_sequential", "pb_set_segment_mode", "pb_rowlist_noalloc_max_segments",
     "pb_rowlist_partition_noalloc",
 )
 
@@ -136,6 +136,7 @@ _SIGNATURES = {
                                          _I32, _I32, _I32, _VP, _I64, _VP, _VP, _VP, _VP, _VP]),
     "pb_best_thresholds": (ctypes.c_int, [_VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP]),
     "pb_pick_sequential": (ctypes.c_int, [_VP, _I32, _I32, _I32, _VP, _VP, _VP]),
+    "pb_set_segment_mode": (ctypes.c_int, [_VP, _I32, _I32]),
     "pb_rowlist_noalloc_max_segments": (ctypes.c_int64, []),
     "pb_rowlist_partition_noalloc": (ctypes.c_int, [_VP, _I64, _I64, _I32, _VP, _I64, _VP, _VP, _I32, _I32,
                                                     _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP, _VP]),

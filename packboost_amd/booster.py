@@ -322,6 +322,7 @@ class PackBoost:
         finally:
             torch.cuda.synchronize(device)
         self._train_preds = fitter.preds[:N].clone()
+        self._fit_mode = "segments" if fitter.segments else "planes"
         fitter.close()
         self._fitter = None
         return self

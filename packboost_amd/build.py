@@ -19,7 +19,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libpackboost_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["hist.hip", "score.hip", "partition.hip", "predict.hip", "metrics.hip", "binning.hip", "rowlist.hip",
+SOURCES = ["hist.hip", "score.hip", "partition.hip", "predict.hip", "metrics.hip", "binning.hip", "rowlist.hip", "segment.hip",
            "capi.cpp"]
 ARCH = "gfx950"
 

@@ -58,6 +58,13 @@ struct pb_ctx {
     int32_t hist_rounds;
     // phase timing of pb_grow_round (pb_profile_enable): per depth, 5 events bracket the
     // hist / score / decide / partition launches on the caller's stream
+    // segment mode (pb_set_segment_mode): rows sorted by (era, slot) in two buffer sets
+    bool seg_mode;
+    int32_t seg_from;           // first depth scored by the fused kernel
+    int32_t seg_cur;            // buffer set holding the current depth's rows
+    pb::SegBuffers sb[2];
+    int32_t* seg[2];            // [E][segw] segment starts of the rows in sb[i]
+    pb::SegState ss;            // partition shape and workspace
     int32_t profile;  // 0 off, 1 every phase, 2 the histogram only
     int32_t bin_layout;  // bins_dev of pb_hist_build / pb_partition: 0 uint8, 1 nibble
     std::vector<hipEvent_t> ev_free;
@@ -132,6 +139,17 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->ids[0]);
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
+    for (int i = 0; i < 2; ++i) {
+        (void)hipFree(c->sb[i].bins);
+        (void)hipFree(c->sb[i].g);
+        (void)hipFree(c->sb[i].row);
+        (void)hipFree(c->sb[i].tnode);
+        (void)hipFree(c->seg[i]);
+    }
+    (void)hipFree(c->ss.cp);
+    (void)hipFree(c->ss.cnt_l);
+    (void)hipFree(c->ss.cnt_r);
+    (void)hipFree(c->ss.base);
     (void)hipFree(c->seg_info_dev);
     (void)hipFree(c->acc_era_dev);
     (void)hipFree(c->acc_cnt);
@@ -208,6 +226,11 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
                                                         c->score_wgs);
             c->wmax = std::max(c->wmax, sh.ntiles * sh.wpt);
         }
+    for (int dd = 0; dd < d.max_depth; ++dd) {  // the segment-mode scorer's winners
+        const int32_t ft = pb::seg_score_fts(max_nodes_at(c, dd), d.max_feats);
+        const int32_t nt = (d.max_feats + ft - 1) / ft;
+        c->wmax = std::max(c->wmax, nt * std::min(4, (ft * std::max(1, d.max_bins - 1) + pb::kWave - 1) / pb::kWave));
+    }
     c->lds_budget = env_int("PB_HIST_LDS_BUDGET", 0);  // 0: by frontier width
     c->hist_block = (int32_t)env_int("PB_HIST_BLOCK", 0);
     c->force_pairs = (int32_t)env_int("PB_HIST_PAIRS", 0);
@@ -608,6 +631,126 @@ int pb_round_end(pb_ctx* c, const uint16_t* tnode, const float* values, int32_t 
     return PB_OK;
 }
 
+namespace {
+
+// The segment-mode scorer of depth `depth` (pb::launch_seg_score) over the context's sorted rows,
+// leaving what pb_decide reads as pb_des_score does.
+int seg_score(pb_ctx* c, const int32_t* feats, int32_t K, int32_t depth, int32_t max_nodes,
+              const pb_split_params* p, void* stream) {
+    const int nb = c->d.max_bins;
+    pb::SegScoreArgs a{};
+    a.bins = c->sb[c->seg_cur].bins;
+    a.ld = c->d.ld;
+    a.g = c->sb[c->seg_cur].g;
+    a.seg = c->seg[c->seg_cur];
+    a.segw = c->ss.segw;
+    a.sh_era = c->sh_era;
+    a.feats = feats;
+    a.K = K;
+    a.E = c->d.num_eras;
+    a.nb = nb;
+    a.T = nb - 1;
+    a.lambda_l2 = (float)p->lambda_l2;
+    a.lambda_dro = (float)p->lambda_dro;
+    a.dir_w = (float)p->direction_weight;
+    a.era_alpha = (float)p->era_alpha;
+    a.msl = p->min_samples_leaf;
+    a.st = c->st;
+    a.depth = depth;
+    a.cand_w = c->cand_w;
+    a.fts = pb::seg_score_fts(max_nodes, K);
+    a.ntiles = (K + a.fts - 1) / a.fts;
+    a.wpt = std::min(4, (a.fts * a.T + pb::kWave - 1) / pb::kWave);
+    a.seq = c->seq;
+    a.ntot = c->ntot;
+    a.rt = std::max(2, std::min<int32_t>(a.E + 1, 4096));
+    if (a.ntiles * a.wpt > c->wmax) return fail(PB_ERR_INVALID, "segment scorer: candidate buffer too small");
+    c->last_w = a.ntiles * a.wpt;
+    c->last_K = K;
+    c->last_T = a.T;
+    c->last_feats = feats;
+    c->last_thr_tab = nullptr;
+    PB_HIP(pb::launch_seg_score(a, max_nodes, (hipStream_t)stream), "segment scorer launch");
+    return PB_OK;
+}
+
+}  // namespace
+
+int pb_set_segment_mode(pb_ctx* c, int32_t enable, int32_t from_depth) {
+    if (!c) return fail(PB_ERR_INVALID, "pb_set_segment_mode: null context");
+    if (enable != 0 && enable != 1) return fail(PB_ERR_INVALID, "pb_set_segment_mode: enable must be 0 or 1");
+    if (!enable) {
+        c->seg_mode = false;
+        return PB_OK;
+    }
+    if (c->max_era_rows > pb::kMaxEraRowsDirect)
+        return fail(PB_ERR_UNSUPPORTED, "pb_set_segment_mode: an era holds more than 65535 rows");
+    if (c->d.num_rows >= INT32_MAX || c->d.max_bins > 255)
+        return fail(PB_ERR_UNSUPPORTED, "pb_set_segment_mode: too many rows or bins");
+    const int64_t N = c->d.num_rows;
+    const int32_t E = c->d.num_eras;
+    const int32_t segw = c->umax + 1;
+    const int64_t chunks = pb::seg_chunk_bound(N, E, segw);
+    if (chunks >= INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_set_segment_mode: too many row chunks");
+    int32_t from = from_depth;
+    if (from < 0) {
+        // the first depth whose planes would pass 4 GiB: the shallower depths' planes cost
+        // less than moving every row's columns between depths
+        const int64_t cells = (int64_t)E * c->d.max_feats * std::max(1, c->d.max_bins - 1) * 6;
+        from = c->d.max_depth;
+        for (int dd = 0; dd < c->d.max_depth; ++dd)
+            if ((int64_t)max_nodes_at(c, dd) * cells >= (int64_t(4) << 30)) {
+                from = dd;
+                break;
+            }
+    }
+    int rc = PB_OK;
+    if (!c->sb[0].row) {
+        for (int i = 0; i < 2 && rc == PB_OK; ++i) {
+            if ((rc = dev_alloc(&c->sb[i].bins, (size_t)c->d.num_features * c->d.ld, "alloc sorted bins")) ||
+                (rc = dev_alloc(&c->sb[i].g, (size_t)std::max<int64_t>(1, N), "alloc sorted rows")) ||
+                (rc = dev_alloc(&c->sb[i].row, (size_t)std::max<int64_t>(1, N), "alloc sorted rows")) ||
+                (rc = dev_alloc(&c->sb[i].tnode, (size_t)std::max<int64_t>(1, N), "alloc sorted rows")) ||
+                (rc = dev_alloc(&c->seg[i], (size_t)E * segw, "alloc segments")))
+                break;
+        }
+        if (rc == PB_OK) {
+            if ((rc = dev_alloc(&c->ss.cp, (size_t)E * segw + 1, "alloc segment chunks")) ||
+                (rc = dev_alloc(&c->ss.cnt_l, (size_t)chunks + 1, "alloc segment chunks")) ||
+                (rc = dev_alloc(&c->ss.cnt_r, (size_t)chunks + 1, "alloc segment chunks")) ||
+                (rc = dev_alloc(&c->ss.base, (size_t)E * segw * 2, "alloc segment chunks"))) {
+            }
+        }
+        if (rc != PB_OK) {
+            for (int i = 0; i < 2; ++i) {
+                (void)hipFree(c->sb[i].bins);
+                (void)hipFree(c->sb[i].g);
+                (void)hipFree(c->sb[i].row);
+                (void)hipFree(c->sb[i].tnode);
+                (void)hipFree(c->seg[i]);
+                c->sb[i] = pb::SegBuffers{};
+                c->seg[i] = nullptr;
+            }
+            (void)hipFree(c->ss.cp);
+            (void)hipFree(c->ss.cnt_l);
+            (void)hipFree(c->ss.cnt_r);
+            (void)hipFree(c->ss.base);
+            c->ss = pb::SegState{};
+            return rc;
+        }
+    }
+    c->ss.N = N;
+    c->ss.ld = c->d.ld;
+    c->ss.E = E;
+    c->ss.segw = segw;
+    c->ss.era_off = c->era_off_dev;
+    c->ss.st = c->st;
+    c->ss.rules = c->rules;
+    c->seg_from = std::min<int32_t>(from, c->d.max_depth);
+    c->seg_mode = true;
+    return PB_OK;
+}
+
 int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int32_t K,
                   pb_decision* dec, pb_round_header* header, void* stream) {
     if (!c || !b || !feats || !dec || !header) return fail(PB_ERR_INVALID, "pb_grow_round: null argument");
@@ -622,8 +765,22 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
         return fail(PB_ERR_INVALID, "pb_grow_round: the nibble bin layout needs max_bins <= 16");
     if (nib && (reinterpret_cast<uintptr_t>(b->bins4_dev) & 15))
         return fail(PB_ERR_INVALID, "pb_grow_round: bins4 must be 16-byte aligned");
+    const bool seg = c->seg_mode;
+    if (seg) {
+        const int32_t full = std::max(1, c->d.max_bins - 1);
+        if (b->params.k_cuts > 0 && b->params.k_cuts < full)
+            return fail(PB_ERR_UNSUPPORTED, "pb_grow_round: segment mode scores every threshold (k_cuts 0)");
+    }
     int rc = pb_round_begin(c, b->preds_dev, b->y_dev, b->grad_dev, b->nid_dev, b->tnode_dev, stream);
     if (rc) return rc;
+    if (seg) {
+        c->seg_cur = 0;
+        pb::SegBuffers& cur = c->sb[0];
+        PB_HIP(pb::launch_seg_begin(b->grad_dev, cur.row, cur.g, cur.tnode, c->d.num_rows, c->era_off_dev,
+                                    c->d.num_eras, c->ss.segw, c->seg[0], (hipStream_t)stream),
+               "segment round begin launch");
+    }
+    const int32_t fused_from = seg ? c->seg_from : c->d.max_depth;
     for (int d = 0; d < c->d.max_depth; ++d) {
         const int32_t m = max_nodes_at(c, d);
         const int32_t* f = feats + (int64_t)d * K;
@@ -646,21 +803,53 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
             if (prof && i < n_ev) PB_HIP(hipEventRecord(ev[i], (hipStream_t)stream), "profile event record");
             return PB_OK;
         };
+        const bool fused = d >= fused_from;
         if ((rc = mark(0))) return rc;
-        if ((rc = hist_build(c, bins, ld_bytes, nib, b->grad_dev, b->nid_dev, f, K, d, m,
-                             b->hist_cnt_dev, b->hist_grad_dev, stream)))
-            return rc;
-        if ((rc = mark(1))) return rc;
-        if ((rc = pb_des_score(c, b->hist_cnt_dev, b->hist_grad_dev, f, K, d, m, &b->params, nullptr,
-                               stream)))
-            return rc;
+        if (fused) {
+            if (d == fused_from)  // every feature column in the sorted row order
+                PB_HIP(pb::launch_seg_gather(b->bins_dev, c->d.ld, c->d.num_features, c->sb[c->seg_cur].row,
+                                             c->sb[c->seg_cur].bins, c->d.num_rows, (hipStream_t)stream),
+                       "segment gather launch");
+            // one fused launch: its time is the histogram phase, the scorer phase is empty
+            if ((rc = seg_score(c, f, K, d, m, &b->params, stream))) return rc;
+            if ((rc = mark(1))) return rc;
+        } else {
+            if ((rc = hist_build(c, bins, ld_bytes, nib, b->grad_dev, b->nid_dev, f, K, d, m,
+                                 b->hist_cnt_dev, b->hist_grad_dev, stream)))
+                return rc;
+            if ((rc = mark(1))) return rc;
+            if ((rc = pb_des_score(c, b->hist_cnt_dev, b->hist_grad_dev, f, K, d, m, &b->params, nullptr,
+                                   stream)))
+                return rc;
+        }
         if ((rc = mark(2))) return rc;
         if ((rc = pb_decide(c, d, m, &b->params, dec, b->values_dev, stream))) return rc;
         if ((rc = mark(3))) return rc;
-        if ((rc = partition(c, bins, ld_bytes, nib, d, b->nid_dev, b->tnode_dev, stream))) return rc;
+        if (seg) {
+            const bool last = d + 1 == c->d.max_depth;
+            const int i = c->seg_cur;
+            // the columns move once they are sorted (from the first fused depth on)
+            PB_HIP(pb::launch_seg_partition(c->ss, c->seg[i], c->seg[1 - i], c->sb[i], c->sb[1 - i],
+                                            fused ? nullptr : b->bins_dev, fused ? c->d.num_features : 0, d,
+                                            last, (hipStream_t)stream),
+                   "segment partition launch");
+            if (!last) c->seg_cur = 1 - i;
+        }
+        // the plane path's row ids: every depth without segments (the last one leaves the
+        // leaves for pb_round_end), else while a later depth's histogram still reads them
+        if ((!seg || d + 1 < fused_from) &&
+            (rc = partition(c, bins, ld_bytes, nib, d, b->nid_dev, b->tnode_dev, stream)))
+            return rc;
         if ((rc = mark(4))) return rc;
     }
     PB_HIP(pb::launch_round_header(c->st, header, (hipStream_t)stream), "round header launch");
+    if (seg) {
+        const pb::SegBuffers& cur = c->sb[c->seg_cur];
+        PB_HIP(pb::launch_seg_round_end(cur.tnode, cur.row, b->values_dev, b->pack_size, b->learning_rate,
+                                        b->preds_dev, c->d.num_rows, (hipStream_t)stream),
+               "segment round end launch");
+        return PB_OK;
+    }
     return pb_round_end(c, b->tnode_dev, b->values_dev, b->pack_size, b->learning_rate, b->preds_dev,
                         stream);
 }

@@ -222,16 +222,8 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             for (int j = 0; j < 4; ++j) {
                 const uint32_t nj = ok[j] ? n4[j] - (uint32_t)u0 : 0u;  // node within the tile
                 base[j] = __umul24(nj, cells_c8) + copy8;  // nj < 2^16, cells_c8 < 2^24
-                // (q << 16) + 1 as two 32-bit halves: the count 1 in the low 16 bits, the
-                // fixed-point grad q = round(g * 2^sh) above it (|q| < 2^45); 0 if not counted.
-                // In float, exactly: xq = q, xh = floor(q / 2^16) (the high word), xl = q - xh *
-                // 2^16 in [0, 2^16) (the grad's bits in the low word).
-                const float xq = rintf(g4[j] * scale);
-                const float xh = floorf(xq * (1.0f / 65536.0f));
-                const float xl = xq - xh * 65536.0f;
-                const uint32_t lo = ((uint32_t)xl << kCountBits) | 1u;
-                const uint32_t hi = (uint32_t)(int32_t)xh;
-                qv[j] = ((unsigned long long)(ok[j] ? hi : 0u) << 32) | (ok[j] ? lo : 0u);
+                // (q << 16) + 1 with q = round(g * 2^sh) (grad_addend); 0 if not counted
+                qv[j] = ok[j] ? grad_addend(g4[j], scale) : 0ull;
                 if (!NIB) keep |= ok[j] ? (0xffu << (8 * j)) : 0u;
             }
             const bool any = ok[0] || ok[1] || ok[2] || ok[3];  // some row of the quad is counted

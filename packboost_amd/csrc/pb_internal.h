@@ -39,6 +39,19 @@ __device__ __forceinline__ int era_grad_scale(double bound) {
     return min(44 - ex, 126);
 }
 
+// One row's 64-bit histogram addend (q << 16) + 1 with q = round(g * scale) (|q| < 2^45): the
+// count 1 in the low 16 bits, the fixed-point grad above it, built from two 32-bit halves. In
+// float, exactly: xq = q, xh = floor(q / 2^16) (the high word), xl = q - xh * 2^16 in [0, 2^16)
+// (the grad's bits in the low word).
+__device__ __forceinline__ unsigned long long grad_addend(float g, float scale) {
+    const float xq = rintf(g * scale);
+    const float xh = floorf(xq * (1.0f / 65536.0f));
+    const float xl = xq - xh * 65536.0f;
+    const uint32_t lo = ((uint32_t)xl << kCountBits) | 1u;
+    const uint32_t hi = (uint32_t)(int32_t)xh;
+    return ((unsigned long long)hi << 32) | lo;
+}
+
 // Per active node of the current depth, read by the partition kernel.
 struct SplitRule {
     int32_t feature;    // -1: node did not split
@@ -201,6 +214,76 @@ hipError_t launch_decide(const DecideCands& dc, int32_t max_nodes, const NodeTot
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
                          hipStream_t s);
+// Segment mode (segment.hip, score.hip). Rows are kept sorted by (era, frontier slot): in era
+// e, slot u's rows are [seg[e * segw + u], seg[e * segw + u + 1]) of the sorted buffers, and
+// [seg[e * segw + U], era end) holds the rows no longer in the frontier (U = active slots).
+// One workgroup per (slot, tile of FT features) walks the eras in order, builds each era's
+// histogram of its node's rows in LDS and runs the DES recurrence on it: the candidates and
+// wavefront winners are those of the plane scorers, bit for bit, without the planes.
+struct SegScoreArgs {
+    const uint8_t* bins;   // sorted bins, uint8 [F][ld]
+    int64_t ld;
+    const float* g;        // sorted gradients [N]
+    const int32_t* seg;    // [E][segw] segment starts of the current depth
+    int32_t segw;
+    const int32_t* sh_era;  // per-era fixed-point scale exponent
+    const int32_t* feats;
+    int32_t K;
+    int32_t E, nb, T;       // T = nb - 1 thresholds (full sweep)
+    float lambda_l2, lambda_dro, dir_w, era_alpha;
+    int32_t msl;
+    const Frontier* st;
+    int32_t depth;
+    pb_candidate* cand_w;  // [U][ntiles * wpt]
+    int32_t ntiles, wpt, fts;
+    SeqCands seq;
+    NodeTotal* ntot;
+    int32_t rt;            // size of the 1/n table (equal era weights)
+};
+constexpr int kSegMaxFt = 8;
+// The sorted rows of segment mode: bins [F][ld] and per row its gradient, original row id and
+// tree node id.
+struct SegBuffers {
+    uint8_t* bins;
+    float* g;
+    int32_t* row;
+    uint16_t* tnode;
+};
+// The partition's shape and workspace (segment.hip).
+struct SegState {
+    int64_t N, ld;
+    int32_t E, segw;
+    const int32_t* era_off;
+    const Frontier* st;
+    const SplitRule* rules;
+    int32_t* cp;     // [E * segw + 1] chunk prefix per (era, slot)
+    int32_t* cnt_l;  // [seg_chunk_bound + 1] left rows per chunk, then their prefix
+    int32_t* cnt_r;
+    int32_t* base;   // [E * segw][2] first destination row of each (era, slot, side)
+};
+__device__ __forceinline__ bool bins_le(const uint8_t* bins, int64_t ld, const SplitRule& r, int32_t row) {
+    return (int32_t)bins[(int64_t)r.feature * ld + row] <= r.threshold;
+}
+int64_t seg_chunk_bound(int64_t N, int32_t E, int32_t segw);
+hipError_t launch_seg_begin(const float* grad, int32_t* srow, float* gs, uint16_t* stn, int64_t N,
+                            const int32_t* era_off, int32_t E, int32_t segw, int32_t* seg, hipStream_t s);
+hipError_t launch_seg_gather(const uint8_t* bins, int64_t ld, int32_t F, const int32_t* row, uint8_t* sorted,
+                             int64_t N, hipStream_t s);
+// Partition of depth `depth` from src (segments seg) into dst (segments seg_next), moving the
+// first F sorted columns with the rows; at the last depth (`last`) only the tree nodes of src
+// change. orig non-null: the sorted columns are not gathered yet, the rules read orig [F][ld]
+// at the rows' ids (F must then be 0).
+hipError_t launch_seg_partition(const SegState& st, const int32_t* seg, int32_t* seg_next, const SegBuffers& src,
+                                const SegBuffers& dst, const uint8_t* orig, int32_t F, int32_t depth, bool last,
+                                hipStream_t s);
+hipError_t launch_seg_round_end(const uint16_t* stn, const int32_t* srow, const float* values, int32_t B,
+                                float lr, float* preds, int64_t N, hipStream_t s);
+// Features per workgroup for `nodes` active slots and K features: enough workgroups to fill
+// the device (about 1024), at most kSegMaxFt.
+int32_t seg_score_fts(int32_t nodes, int32_t K);
+size_t seg_score_lds_bytes(int32_t fts, int32_t rt);
+hipError_t launch_seg_score(const SegScoreArgs& a, int32_t max_nodes, hipStream_t s);
+
 // One winner per node of candidate records [M][n] in visiting order, by the reference's
 // sequential scan (band: int32 [M][n] scratch).
 hipError_t launch_pick_sequential(const pb_candidate* cand, int32_t M, int64_t n, int32_t* band,

@@ -1291,6 +1291,235 @@ __global__ __launch_bounds__(kBlock) void pick_sequential_kernel(const pb_candid
     if (lane == 0) store_cand(out + u, cur);
 }
 
+
+// Segment-mode scorer (SegScoreArgs). Workgroup (slot u, feature tile): thread i owns the
+// candidates c = i + 256 j (feature c / T of the tile, threshold c % T). Per era with rows of
+// the node: (1) every thread adds its rows' addends (grad_addend, the era's scale) into the
+// tile's LDS histogram [FT][256]; (2) wave w scans the bins of features w, w + 4, ... exactly
+// (64-bit integer prefixes), writes each prefix count and its grad rounded once to float (the
+// values the plane path writes) and clears the histogram; (3) every thread runs the wide
+// scorer's era step on its candidates. Two barriers per era: the next era's histogram is built
+// while no thread still reads the prefixes of this one only after the barrier that ends (1).
+// DIR: the direction term is on (dir_w != 0); UNIT: equal era weights (era_alpha <= 0).
+template <int FT, bool DIR, bool UNIT>
+__global__ __launch_bounds__(kBlock) void seg_score_kernel(SegScoreArgs a) {
+    constexpr int kCpt = (FT * 254 + kBlock - 1) / kBlock;  // candidates per thread (T <= 254)
+    extern __shared__ unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int u = blockIdx.x / a.ntiles;
+    const int tile = blockIdx.x - u * a.ntiles;
+    const int Ua = a.st->u_active[a.depth];
+    if (u >= Ua) return;
+    const int k0 = tile * FT;
+    const int nf = min(FT, a.K - k0);
+    if (nf <= 0) return;
+    const int nb = a.nb;
+    const int T = a.T;
+    const int ncand = nf * T;
+    const int RT = a.rt;
+    unsigned long long* hist = reinterpret_cast<unsigned long long*>(smem);  // [FT][256]
+    int32_t* pc = reinterpret_cast<int32_t*>(hist + FT * 256);                 // [FT][256]
+    float* pg = reinterpret_cast<float*>(pc + FT * 256);                       // [FT][256]
+    float* eg = pg + FT * 256;                                                 // [2]: Gt, parent
+    float* recip = eg + 4;                                                     // [RT]
+    for (int i = tid; i < FT * 256; i += kBlock) hist[i] = 0ull;
+    for (int i = tid; i < RT; i += kBlock) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
+
+    const uint8_t* col[FT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f) col[f] = a.bins + (int64_t)a.feats[k0 + min(f, nf - 1)] * a.ld;
+
+    const float lam = a.lambda_l2;
+    const float alpha = a.era_alpha;
+    float wsum[kCpt], mean[kCpt], M2[kCpt], agn[kCpt], agd[kCpt], lg[kCpt];
+    int lt[kCpt];
+#pragma unroll
+    for (int j = 0; j < kCpt; ++j) {
+        wsum[j] = mean[j] = M2[j] = agn[j] = agd[j] = lg[j] = 0.0f;
+        lt[j] = 0;
+    }
+    int tc = 0;
+    float tg = 0.0f;
+    int coff[kCpt];  // LDS index f * 256 + t of each candidate (0 past the last: never stored)
+#pragma unroll
+    for (int j = 0; j < kCpt; ++j) {
+        const int c = tid + j * kBlock;
+        const int f = c / T;
+        coff[j] = c < ncand ? f * 256 + (c - f * T) : 0;
+    }
+    __syncthreads();
+
+    for (int e = 0; e < a.E; ++e) {
+        const int s0 = a.seg[(int64_t)e * a.segw + u];
+        const int s1 = a.seg[(int64_t)e * a.segw + u + 1];
+        const int ctot = s1 - s0;
+        if (ctot <= 0) continue;  // workgroup-uniform: the node has no rows in this era
+        const int sh = a.sh_era[e];
+        const float scale = ldexpf(1.0f, sh);
+        const double inv_scale = ldexp(1.0, -sh);
+        // (1) histogram of the node's rows of this era
+        // four rows per thread per step, all loads issued before the atomics
+        for (int r0 = s0 + tid; r0 < s1; r0 += 4 * kBlock) {
+            float gv[4];
+            uint32_t bv[4][FT];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = min(r0 + q * kBlock, s1 - 1);
+                gv[q] = a.g[r];
+#pragma unroll
+                for (int f = 0; f < FT; ++f) bv[q][f] = col[f][r];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (r0 + q * kBlock >= s1) break;
+                const unsigned long long add = grad_addend(gv[q], scale);
+#pragma unroll
+                for (int f = 0; f < FT; ++f)
+                    if (f < nf) atomicAdd(hist + f * 256 + bv[q][f], add);
+            }
+        }
+        __syncthreads();
+        // (2) exact prefixes, one wave per feature; the era total from the tile's first feature
+        for (int f = wave; f < nf; f += kBlock / kWave) {
+            unsigned long long v[4];
+            unsigned long long run = 0ull;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                unsigned long long* cell = hist + f * 256 + 4 * lane + j;
+                run += *cell;
+                v[j] = run;
+                *cell = 0ull;
+            }
+            unsigned long long excl = run;  // inclusive scan of the lane totals, then shifted
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) {
+                const unsigned long long o = __shfl_up(excl, m);
+                if (lane >= m) excl += o;
+            }
+            excl -= run;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int b = 4 * lane + j;
+                const unsigned long long tot = excl + v[j];
+                const uint32_t cnt = (uint32_t)(tot & ((1ull << kCountBits) - 1ull));
+                const long long Q = ((long long)(tot - cnt)) >> kCountBits;
+                const float gs = (float)((double)Q * inv_scale);
+                if (b < T) {
+                    pc[f * 256 + b] = (int32_t)cnt;
+                    pg[f * 256 + b] = gs;
+                } else if (b == nb - 1 && f == 0) {
+                    const float pden = (float)ctot + lam;
+                    eg[0] = gs;
+                    eg[1] = (pden > 0.0f) ? (0.5f * (gs * gs)) / pden : 0.0f;
+                }
+            }
+        }
+        __syncthreads();
+        // (3) the era step of every candidate (the wide scorer's operations)
+        const float Gt = eg[0];
+        const float parent = eg[1];
+        tc += ctot;
+        tg = tg + Gt;
+        const float wera = UNIT ? 1.0f : (float)ctot + alpha;
+        // branch-free: every candidate evaluates the era record and selects (the same float
+        // operations as the wide scorer where it is taken)
+#pragma unroll
+        for (int j = 0; j < kCpt; ++j) {
+            const int L = pc[coff[j]];
+            const float GL = pg[coff[j]];
+            const int R = ctot - L;
+            const float GR = Gt - GL;
+            const bool act = L > 0 && R > 0;
+            const float w = act ? wera : 0.0f;
+            const float dL = (float)L + lam;
+            const float dR = (float)R + lam;
+            const float gfull = 0.5f * ((GL * GL) / dL + (GR * GR) / dR) - parent;
+            const float gain = act ? gfull : 0.0f;
+            lt[j] += L;
+            lg[j] = lg[j] + GL;
+            const float wn = wsum[j] + w;
+            float fac;
+            if (UNIT) {
+                const int wi = (int)wn;
+                fac = wi < RT ? recip[act ? wi : 0] : w / (act ? wn : 1.0f);
+            } else {
+                fac = w / (act ? wn : 1.0f);
+            }
+            wsum[j] = act ? wn : wsum[j];
+            const float delta = gain - mean[j];
+            const float mean_n = mean[j] + fac * delta;
+            const float M2_n = M2[j] + (w * delta) * (gain - mean_n);
+            mean[j] = act ? mean_n : mean[j];
+            M2[j] = act ? M2_n : M2[j];
+            if (DIR) {
+                const float lv = -GL / dL;
+                const float rv = -GR / dR;
+                const bool pos = lv > rv;
+                agn[j] = act ? agn[j] + w * (pos ? 1.0f : -1.0f) : agn[j];
+                agd[j] = act ? agd[j] + w : agd[j];
+            }
+        }
+    }
+
+    // scores, the visiting-order records, and one winner per wavefront
+    Cand best;
+    best.score = 0.0f;
+    best.lt = 0;
+    best.lg = 0.0f;
+    best.f = -1;
+    best.thr = -1;
+    best.valid = 0;
+    float mine[kCpt];
+#pragma unroll
+    for (int j = 0; j < kCpt; ++j) {
+        const int c = tid + j * kBlock;
+        mine[j] = -INFINITY;
+        if (c >= ncand) continue;
+        const int f = c / T;
+        const int t = c - f * T;
+        Cand cc;
+        cc.lt = lt[j];
+        cc.lg = lg[j];
+        cc.f = a.feats[k0 + f];
+        cc.thr = t;
+        const int rt = tc - lt[j];
+        const float ws = (wsum[j] < 1e-12f) ? 1e-12f : wsum[j];
+        const float var = M2[j] / ws;
+        const float sd = sqrtf((0.0f < var) ? var : 0.0f);
+        float score = mean[j] - a.lambda_dro * sd;
+        if (DIR && agd[j] > 0.0f) score = score + a.dir_w * (agn[j] / agd[j]);
+        cc.score = score;
+        cc.valid = (tc > 0 && lt[j] >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
+        const int64_t i = ((int64_t)u * a.K + k0 + f) * T + t;
+        a.seq.score[i] = cc.valid ? cc.score : -INFINITY;
+        a.seq.lt[i] = cc.lt;
+        a.seq.lg[i] = cc.lg;
+        mine[j] = cc.valid ? cc.score : -INFINITY;
+        take_if(better(cc, best), cc, best);
+    }
+    if (tile == 0 && tid == 0) {
+        a.ntot[u].count = tc;
+        a.ntot[u].grad = tg;
+    }
+    if (wave < a.wpt) {
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const Cand o = shfl_xor_cand(best, m);
+            take_if(better(o, best), o, best);
+        }
+        // this wave's candidates below its winner but within kTieBand0 of it
+        int band = 0;
+#pragma unroll
+        for (int j = 0; j < kCpt; ++j)
+            band += (best.valid && mine[j] < best.score && (double)mine[j] >= (double)best.score - kTieBand0) ? 1 : 0;
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) band += __shfl_xor(band, m);
+        if (lane == 0) store_winner(a.cand_w + (int64_t)u * (a.ntiles * a.wpt) + tile * a.wpt + wave, best, band);
+    }
+}
+
 }  // namespace
 
 ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t target_wgs) {
@@ -1382,6 +1611,46 @@ hipError_t launch_pick_sequential(const pb_candidate* cand, int32_t M, int64_t n
     hipLaunchKernelGGL(pick_sequential_kernel, dim3((M + per_block - 1) / per_block), dim3(kBlock), 0, s, cand, M,
                        n, band, out);
     return hipGetLastError();
+}
+
+int32_t seg_score_fts(int32_t nodes, int32_t K) {
+    int32_t ft = kSegMaxFt;
+    while (ft > 1 && (int64_t)nodes * ((K + ft - 1) / ft) < 1024) ft /= 2;
+    return ft;
+}
+
+size_t seg_score_lds_bytes(int32_t fts, int32_t rt) {
+    return (size_t)fts * 256 * (8 + 4 + 4) + 4 * 4 + (size_t)rt * 4;
+}
+
+hipError_t launch_seg_score(const SegScoreArgs& a, int32_t max_nodes, hipStream_t s) {
+    const int64_t grid = (int64_t)max_nodes * a.ntiles;
+    if (grid <= 0) return hipSuccess;
+    if (grid > INT32_MAX || a.T > 254 || a.T != a.nb - 1) return hipErrorInvalidValue;
+    const size_t lds = seg_score_lds_bytes(a.fts, a.rt);
+    auto go = [&](auto kern) -> hipError_t {
+        const void* fn = reinterpret_cast<const void*>(kern);
+        if (lds > 64 * 1024) {
+            hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+        }
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kBlock), lds, s, a);
+        return hipGetLastError();
+    };
+    const bool dir = a.dir_w != 0.0f;
+    const bool unit = !(a.era_alpha > 0.0f);
+    auto pick = [&](auto ft) -> hipError_t {
+        constexpr int FT = decltype(ft)::value;
+        if (dir) return unit ? go(seg_score_kernel<FT, true, true>) : go(seg_score_kernel<FT, true, false>);
+        return unit ? go(seg_score_kernel<FT, false, true>) : go(seg_score_kernel<FT, false, false>);
+    };
+    switch (a.fts) {
+        case 1: return pick(std::integral_constant<int, 1>{});
+        case 2: return pick(std::integral_constant<int, 2>{});
+        case 4: return pick(std::integral_constant<int, 4>{});
+        case 8: return pick(std::integral_constant<int, 8>{});
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace pb

@@ -1,0 +1,352 @@
+// Segment mode: from a chosen depth on, a round keeps the fit's rows sorted by (era, frontier
+// slot) in buffers of the context, so that the fused scorer (seg_score_kernel) reads a node's
+// rows of an era as one contiguous run of every feature column. Every round starts from the
+// caller's era-major order (seg_begin). After each depth every era's rows are partitioned
+// stably into the next depth's slots: for each era, the slots' left and right children that
+// stay in the frontier, in next-slot order, then every row that left the frontier (rows of
+// nodes that did not split or of children below 2 * min_samples_leaf, then the rows that had
+// already left). Before the fused depths only the row ids, gradients and tree nodes move; at
+// the first fused depth seg_gather fetches every feature column in the sorted order, and from
+// then on the partition moves the columns too.
+//
+// The partition works on chunks of up to 256 rows of one (era, slot) segment, the slots
+// counted 0 .. U with U standing for the era's tail of rows no longer in the frontier:
+//   seg_chunks   (one workgroup)    exclusive prefix of the chunk counts per (era, slot);
+//   seg_count    (one per chunk)    rows of the chunk that go left (bin <= threshold);
+//   seg_scan     (one workgroup)    exclusive prefixes of the left and right counts over chunks;
+//   seg_bases    (one per era)      the first destination row of each (era, slot, side);
+//   seg_scatter  (one per chunk)    every row to its place (a ballot ranks it among the rows
+//                                   of its side in the chunk), with its bins, gradient, row id
+//                                   and tree node (the child's id for a split node).
+// At the last depth no row moves: seg_final sets the tree node of each split node's rows.
+// Row counts are 32-bit: N < 2^31.
+#include <algorithm>
+
+#include "pb_internal.h"
+
+namespace pb {
+namespace {
+
+constexpr int kSegChunk = kBlock;  // rows per chunk, one per thread
+
+// end of segment `x` (era e, slot v <= U): the next slot's start, or the era's end for the tail
+__device__ __forceinline__ int32_t seg_end(const SegState& s, const int32_t* seg, int e, int v, int U) {
+    return v < U ? seg[(int64_t)e * s.segw + v + 1] : s.era_off[e + 1];
+}
+
+// the (era, slot) entry of chunk q: the last x with cp[x] <= q (cp ascending, cp[0] = 0)
+__device__ __forceinline__ int chunk_entry(const int32_t* cp, int n, int q) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (cp[mid] <= q) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Exclusive scan of n int32 values in place by one workgroup: vals[i] <- sum of vals[0 .. i-1],
+// vals[n] <- the total.
+__device__ void block_scan_excl(int32_t* vals, int n) {
+    __shared__ int32_t s_part[kBlock];
+    const int tid = threadIdx.x;
+    const int per = (n + kBlock - 1) / kBlock;
+    const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
+    int32_t sum = 0;
+    for (int i = i0; i < i1; ++i) sum += vals[i];
+    s_part[tid] = sum;
+    __syncthreads();
+    if (tid == 0) {
+        int32_t run = 0;
+        for (int i = 0; i < kBlock; ++i) {
+            const int32_t v = s_part[i];
+            s_part[i] = run;
+            run += v;
+        }
+        vals[n] = run;
+    }
+    __syncthreads();
+    int32_t run = s_part[tid];
+    for (int i = i0; i < i1; ++i) {
+        const int32_t v = vals[i];
+        vals[i] = run;
+        run += v;
+    }
+}
+
+// Round start: the rows in the caller's (era-major) order, with their gradients and the root
+// as tree node.
+__global__ __launch_bounds__(kBlock) void seg_begin_kernel(const float* __restrict__ grad, int32_t* __restrict__ srow,
+                                                     float* __restrict__ gs, uint16_t* __restrict__ stn, int64_t N,
+                                                     const int32_t* __restrict__ era_off, int32_t E, int32_t segw,
+                                                     int32_t* __restrict__ seg) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < N; i += stride) {
+        srow[i] = (int32_t)i;
+        gs[i] = grad[i];
+        stn[i] = 0;
+    }
+    // the root: slot 0 of era e is the whole era (an inactive root has U = 0 slots, and the
+    // same entry is the start of the tail)
+    for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < E; e += stride) {
+        seg[e * segw] = era_off[e];
+        seg[e * segw + 1] = era_off[e + 1];
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void seg_chunks_kernel(SegState s, const int32_t* __restrict__ seg,
+                                                      int32_t depth) {
+    const int U = s.st->u_active[depth];
+    const int n = s.E * (U + 1);
+    for (int x = threadIdx.x; x < n; x += kBlock) {
+        const int e = x / (U + 1);
+        const int v = x - e * (U + 1);
+        const int32_t len = seg_end(s, seg, e, v, U) - seg[(int64_t)e * s.segw + v];
+        s.cp[x] = (len + kSegChunk - 1) / kSegChunk;
+    }
+    __syncthreads();
+    block_scan_excl(s.cp, n);
+}
+
+// the chunk's segment, its rows [r0, r1), and whether its slot split (then rule)
+struct ChunkInfo {
+    int x, e, v, U;
+    int32_t r0, r1;
+    bool split;
+    SplitRule rule;
+};
+
+__device__ __forceinline__ bool chunk_info(const SegState& s, const int32_t* seg, int32_t depth, int q,
+                                           ChunkInfo& ci) {
+    ci.U = s.st->u_active[depth];
+    const int n = s.E * (ci.U + 1);
+    if (q >= s.cp[n]) return false;
+    ci.x = chunk_entry(s.cp, n, q);
+    ci.e = ci.x / (ci.U + 1);
+    ci.v = ci.x - ci.e * (ci.U + 1);
+    const int32_t start = seg[(int64_t)ci.e * s.segw + ci.v];
+    ci.r0 = start + (q - s.cp[ci.x]) * kSegChunk;
+    ci.r1 = min(ci.r0 + kSegChunk, seg_end(s, seg, ci.e, ci.v, ci.U));
+    ci.split = false;
+    if (ci.v < ci.U) {
+        ci.rule = s.rules[ci.v];
+        ci.split = ci.rule.feature >= 0;
+    }
+    return true;
+}
+
+// Whether sorted row r goes left under the slot's rule: from the sorted columns, or, before
+// they are gathered (orig non-null), from the caller's columns at the row's id.
+__device__ __forceinline__ bool seg_goes_left(const SegState& s, const SegBuffers& src, const uint8_t* orig,
+                                              const SplitRule& rule, int32_t r) {
+    if (orig) return (int32_t)orig[(int64_t)rule.feature * s.ld + src.row[r]] <= rule.threshold;
+    return bins_le(src.bins, s.ld, rule, r);
+}
+
+__global__ __launch_bounds__(kBlock) void seg_count_kernel(SegState s, const int32_t* __restrict__ seg,
+                                                     SegBuffers src, const uint8_t* __restrict__ orig,
+                                                     int32_t depth) {
+    ChunkInfo ci;
+    if (!chunk_info(s, seg, depth, blockIdx.x, ci)) return;
+    const int32_t r = ci.r0 + (int32_t)threadIdx.x;
+    const bool in = r < ci.r1;
+    int left = 0;
+    if (in) left = ci.split ? (seg_goes_left(s, src, orig, ci.rule, r) ? 1 : 0) : 1;
+    __shared__ int s_cnt[kBlock / kWave];
+    int c = __popcll(__ballot(left != 0));
+    if ((threadIdx.x & (kWave - 1)) == 0) s_cnt[threadIdx.x / kWave] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int nl = 0;
+        for (int w = 0; w < kBlock / kWave; ++w) nl += s_cnt[w];
+        s.cnt_l[blockIdx.x] = nl;
+        s.cnt_r[blockIdx.x] = (ci.r1 - ci.r0) - nl;  // 0 unless the slot split
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void seg_scan_kernel(SegState s, int32_t depth) {
+    const int U = s.st->u_active[depth];
+    const int nq = s.cp[s.E * (U + 1)];
+    block_scan_excl(s.cnt_l, nq);
+    __syncthreads();
+    block_scan_excl(s.cnt_r, nq);
+}
+
+// One thread per era: the first destination row of each (slot, side), the next depth's
+// segment starts, then the tail.
+__global__ __launch_bounds__(kBlock) void seg_bases_kernel(SegState s, const int32_t* __restrict__ seg,
+                                                     int32_t* __restrict__ seg_next, int32_t depth) {
+    const int e = blockIdx.x * kBlock + threadIdx.x;
+    const int U = s.st->u_active[depth];
+    const int Un = s.st->u_active[depth + 1];
+    if (e >= s.E) return;
+    const int64_t xb = (int64_t)e * (U + 1);
+    auto tot = [&](int v, int side) -> int32_t {
+        const int32_t* p = side ? s.cnt_r : s.cnt_l;
+        return p[s.cp[xb + v + 1]] - p[s.cp[xb + v]];
+    };
+    int32_t pos = s.era_off[e];
+    int slot = 0;
+    for (int v = 0; v < U; ++v) {
+        const SplitRule r = s.rules[v];
+        if (r.feature < 0) continue;
+        for (int side = 0; side < 2; ++side) {
+            if (r.next_slot[side] == PB_INACTIVE) continue;
+            s.base[(xb + v) * 2 + side] = pos;
+            seg_next[(int64_t)e * s.segw + slot] = pos;  // slots are assigned in this order
+            ++slot;
+            pos += tot(v, side);
+        }
+    }
+    seg_next[(int64_t)e * s.segw + Un] = pos;  // start of the tail
+    for (int v = 0; v < U; ++v) {
+        const SplitRule r = s.rules[v];
+        for (int side = 0; side < 2; ++side) {
+            if (r.feature >= 0 && r.next_slot[side] != PB_INACTIVE) continue;
+            if (r.feature < 0 && side == 1) continue;  // a leaf's rows all count as left
+            s.base[(xb + v) * 2 + side] = pos;
+            pos += tot(v, side);
+        }
+    }
+    s.base[(xb + U) * 2] = pos;  // the rows already in the tail keep their order
+}
+
+__global__ __launch_bounds__(kBlock) void seg_scatter_kernel(SegState s, const int32_t* __restrict__ seg,
+                                                       SegBuffers src, SegBuffers dst,
+                                                       const uint8_t* __restrict__ orig, int32_t F,
+                                                       int32_t depth) {
+    ChunkInfo ci;
+    if (!chunk_info(s, seg, depth, blockIdx.x, ci)) return;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1);
+    const int wave = tid / kWave;
+    const int32_t r = ci.r0 + tid;
+    const bool in = r < ci.r1;
+    int side = 0;
+    if (in && ci.split) side = seg_goes_left(s, src, orig, ci.rule, r) ? 0 : 1;
+    // rank among the rows of the same side before this one in the chunk
+    __shared__ int s_cnt[2][kBlock / kWave];
+    const unsigned long long m1 = __ballot(in && side == 1);
+    const unsigned long long m0 = __ballot(in && side == 0);
+    const unsigned long long below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+    if (lane == 0) {
+        s_cnt[0][wave] = __popcll(m0);
+        s_cnt[1][wave] = __popcll(m1);
+    }
+    __syncthreads();
+    if (!in) return;
+    int rank = __popcll((side ? m1 : m0) & below);
+    for (int w = 0; w < wave; ++w) rank += s_cnt[side][w];
+    const int32_t* pre = side ? s.cnt_r : s.cnt_l;
+    const int32_t d = s.base[(int64_t)ci.x * 2 + side] + (pre[blockIdx.x] - pre[s.cp[ci.x]]) + rank;
+    if ((uint32_t)d >= (uint32_t)s.N) return;  // only reachable with inconsistent segments
+    // 16 columns' loads in flight before their stores
+    int f0 = 0;
+    for (; f0 + 16 <= F; f0 += 16) {
+        uint8_t v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = src.bins[(int64_t)(f0 + k) * s.ld + r];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) dst.bins[(int64_t)(f0 + k) * s.ld + d] = v[k];
+    }
+    for (; f0 < F; ++f0) dst.bins[(int64_t)f0 * s.ld + d] = src.bins[(int64_t)f0 * s.ld + r];
+    dst.g[d] = src.g[r];
+    dst.row[d] = src.row[r];
+    dst.tnode[d] = ci.split ? (uint16_t)(ci.rule.left_id + side) : src.tnode[r];
+}
+
+__global__ __launch_bounds__(kBlock) void seg_final_kernel(SegState s, const int32_t* __restrict__ seg,
+                                                     SegBuffers cur, const uint8_t* __restrict__ orig,
+                                                     int32_t depth) {
+    ChunkInfo ci;
+    if (!chunk_info(s, seg, depth, blockIdx.x, ci)) return;
+    const int32_t r = ci.r0 + (int32_t)threadIdx.x;
+    if (r >= ci.r1 || !ci.split) return;
+    cur.tnode[r] = (uint16_t)(ci.rule.left_id + (seg_goes_left(s, cur, orig, ci.rule, r) ? 0 : 1));
+}
+
+// preds[row] += float32(lr) * (B float32 adds of the leaf value), the operations of
+// round_end_kernel, through the sorted rows' ids
+__global__ __launch_bounds__(kBlock) void seg_round_end_kernel(const uint16_t* __restrict__ stn,
+                                                         const int32_t* __restrict__ srow,
+                                                         const float* __restrict__ values, int32_t B,
+                                                         float lr, float* __restrict__ preds, int64_t N) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < N; i += stride) {
+        const float v = values[stn[i]];
+        float sum = 0.0f;
+        for (int t = 0; t < B; ++t) sum = sum + v;
+        const float tmp = lr * sum;
+        const int32_t r = srow[i];
+        preds[r] = preds[r] + tmp;
+    }
+}
+
+// The sorted bins of every feature: sorted[f][i] = bins[f][row[i]] (rows of one era stay in
+// the era's byte range of each column, so the reads hit few lines).
+__global__ __launch_bounds__(kBlock) void seg_gather_kernel(const uint8_t* __restrict__ bins, int64_t ld, int32_t F,
+                                                      const int32_t* __restrict__ row, uint8_t* __restrict__ sorted,
+                                                      int64_t N) {
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < N; i += stride) {
+        const int64_t r = row[i];
+        int f0 = 0;
+        for (; f0 + 16 <= F; f0 += 16) {
+            uint8_t v[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = bins[(int64_t)(f0 + k) * ld + r];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) sorted[(int64_t)(f0 + k) * ld + i] = v[k];
+        }
+        for (; f0 < F; ++f0) sorted[(int64_t)f0 * ld + i] = bins[(int64_t)f0 * ld + r];
+    }
+}
+
+int grid_of_rows(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>((n + kBlock - 1) / kBlock, 8192)); }
+
+}  // namespace
+
+int64_t seg_chunk_bound(int64_t N, int32_t E, int32_t segw) {
+    return (N + kSegChunk - 1) / kSegChunk + (int64_t)E * segw;
+}
+
+hipError_t launch_seg_gather(const uint8_t* bins, int64_t ld, int32_t F, const int32_t* row, uint8_t* sorted,
+                             int64_t N, hipStream_t s) {
+    hipLaunchKernelGGL(seg_gather_kernel, dim3(grid_of_rows(N)), dim3(kBlock), 0, s, bins, ld, F, row, sorted, N);
+    return hipGetLastError();
+}
+
+hipError_t launch_seg_begin(const float* grad, int32_t* srow, float* gs, uint16_t* stn, int64_t N,
+                            const int32_t* era_off, int32_t E, int32_t segw, int32_t* seg, hipStream_t s) {
+    hipLaunchKernelGGL(seg_begin_kernel, dim3(grid_of_rows(std::max<int64_t>(N, E))), dim3(kBlock), 0, s, grad,
+                       srow, gs, stn, N, era_off, E, segw, seg);
+    return hipGetLastError();
+}
+
+hipError_t launch_seg_partition(const SegState& st, const int32_t* seg, int32_t* seg_next, const SegBuffers& src,
+                                const SegBuffers& dst, const uint8_t* orig, int32_t F, int32_t depth, bool last,
+                                hipStream_t s) {
+    if (orig && F != 0) return hipErrorInvalidValue;  // unsorted columns are not moved
+    const int64_t bound = seg_chunk_bound(st.N, st.E, st.segw);
+    if (bound > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(seg_chunks_kernel, dim3(1), dim3(kBlock), 0, s, st, seg, depth);
+    if (last) {
+        hipLaunchKernelGGL(seg_final_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, orig, depth);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL(seg_count_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, orig, depth);
+    hipLaunchKernelGGL(seg_scan_kernel, dim3(1), dim3(kBlock), 0, s, st, depth);
+    hipLaunchKernelGGL(seg_bases_kernel, dim3((st.E + kBlock - 1) / kBlock), dim3(kBlock), 0, s, st, seg, seg_next,
+                       depth);
+    hipLaunchKernelGGL(seg_scatter_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, dst, orig, F,
+                       depth);
+    return hipGetLastError();
+}
+
+hipError_t launch_seg_round_end(const uint16_t* stn, const int32_t* srow, const float* values, int32_t B,
+                                float lr, float* preds, int64_t N, hipStream_t s) {
+    hipLaunchKernelGGL(seg_round_end_kernel, dim3(grid_of_rows(N)), dim3(kBlock), 0, s, stn, srow, values, B, lr,
+                       preds, N);
+    return hipGetLastError();
+}
+
+}  // namespace pb

@@ -24,6 +24,7 @@ is enqueued again with the generator rewound, so results never depend on the spe
 from __future__ import annotations
 
 import ctypes
+import os
 import math
 from dataclasses import dataclass
 
@@ -108,9 +109,17 @@ class DeviceFit:
 
     def __init__(self, bins_fm: torch.Tensor, num_rows: int, y: torch.Tensor,
                  era_offsets: np.ndarray, cfg: PackBoostConfig, *,
-                 stream: torch.cuda.Stream | None = None, bin_layout: str = "auto") -> None:
+                 stream: torch.cuda.Stream | None = None, bin_layout: str = "auto",
+                 fit_mode: str | None = None) -> None:
         """bin_layout: "u8" (the histogram reads bins_fm), "nibble" (a two-rows-per-byte copy,
-        pb_pack_bins4, max_bins <= 16) or "auto" (nibble whenever max_bins <= 16)."""
+        pb_pack_bins4, max_bins <= 16) or "auto" (nibble whenever max_bins <= 16).
+
+        fit_mode: "planes" (histogram planes in HBM, then the scorer), "segments" (from a
+        depth on, rows kept sorted by frontier node and one fused histogram + scorer kernel
+        per depth: pb_set_segment_mode; PB_SEG_FROM_DEPTH sets that depth, else the first
+        whose planes would pass 4 GiB) or "auto" (default; the environment variable
+        PB_FIT_MODE overrides it): segments when the deepest depth's planes would pass 4 GiB
+        and the fit allows them (full threshold sweep, eras of at most 65535 rows)."""
         lib = _hip.load()
         if bins_fm.dtype != torch.uint8 or bins_fm.dim() != 2 or not bins_fm.is_cuda:
             raise ValueError("bins_fm must be a CUDA uint8 tensor [F, ld]")
@@ -165,9 +174,31 @@ class DeviceFit:
         self.nid = rows(torch.int16)    # uint16 ids carried in int16 storage
         self.tnode = rows(torch.int16)
         self.max_nodes = [int(lib.pb_max_nodes(ctx, d)) for d in range(self.D)]
-        plane = max(int(lib.pb_hist_plane_elems(ctx, m)) for m in self.max_nodes)
+        mode = fit_mode or os.environ.get("PB_FIT_MODE", "auto")
+        if mode not in ("auto", "planes", "segments"):
+            raise ValueError(f"fit_mode must be 'auto', 'planes' or 'segments', got {mode!r}")
+        full_sweep = not (0 < int(cfg.k_cuts) < self.nb - 1)
+        era_rows = int(np.max(np.diff(np.asarray(era_offsets, dtype=np.int64)))) if self.E else 0
+        segments_ok = full_sweep and era_rows <= 65535
+        if mode == "segments" and not segments_ok:
+            raise ValueError("fit_mode 'segments' needs k_cuts 0 and eras of at most 65535 rows")
+        plane_bytes = [self.E * m * self.K * max(1, self.nb - 1) * 6 for m in self.max_nodes]
+        self.segments = mode == "segments" or (mode == "auto" and segments_ok and plane_bytes[-1] >= (4 << 30))
+        # histogram planes for the depths the plane path scores (all of them, or those before
+        # the first fused depth of a segment-mode fit: the deepest planes can take tens of GB)
+        plane_depths = self.D
+        if self.segments:
+            env = os.environ.get("PB_SEG_FROM_DEPTH")
+            if env is not None:
+                plane_depths = min(self.D, max(0, int(env)))
+            else:
+                plane_depths = next((d for d, b in enumerate(plane_bytes) if b >= (4 << 30)), self.D)
+            _hip.check(lib.pb_set_segment_mode(ctx, 1, plane_depths), "pb_set_segment_mode")
+        self.seg_from = plane_depths if self.segments else None
+        plane = max(int(lib.pb_hist_plane_elems(ctx, m)) for m in self.max_nodes[:max(1, plane_depths)])
         self.hist_cnt = torch.empty(plane, dtype=torch.int32, device=dev)
         self.hist_g = torch.empty(plane, dtype=torch.float32, device=dev)
+
         self.values = torch.zeros(1 << (self.D + 1), dtype=torch.float32, device=dev)
         n_dec = (1 << self.D) - 1
         self.dec_dev = torch.zeros(n_dec * _hip.DECISION_DTYPE.itemsize, dtype=torch.uint8, device=dev)
@@ -241,6 +272,8 @@ class DeviceFit:
         events: optional list that receives (phase, depth, start, end) timing events
         recorded on the fit's stream around every kernel phase.
         """
+        if self.segments and self._root_splittable:
+            raise RuntimeError("a segment-mode fit runs whole rounds (pb_grow_round) only")
         lib, ctx, s = self.lib, self.ctx, _hip.stream_ptr(self.stream)
         chk = _hip.check
         self.feats_host.numpy()[...] = subsets
