@@ -166,19 +166,19 @@ int pb_des_score(pb_ctx* ctx, const int32_t* hist_cnt_dev, const float* hist_gra
                  const pb_split_params* params, pb_candidate* cand_all_dev, void* stream);
 
 /* Segment mode (no counterpart in the reference's data structures; its semantics are
- * pb_grow_round's): from depth from_depth on, pb_grow_round keeps the round's rows sorted by
- * (era, frontier slot) in buffers of the context and scores each depth with one fused kernel
- * per (node, feature tile) that streams the node's rows era by era, builds each era's histogram
- * in LDS and runs the DES recurrence on it (frontier_cpu.cpp:261-444): those depths' histogram
- * planes are never written, and the candidates, decisions and predictions are bit-identical to
- * the plane path's. The shallower depths use the plane path while the context tracks the row
- * order; between fused depths the rows are partitioned stably into the next frontier's slots,
- * all feature columns with them. For many bins and nodes, where the planes dominate (BASELINE
- * config 4: 255 bins, 128 nodes, 200 eras). from_depth < 0 picks the first depth whose planes
- * would pass 4 GiB. The context then holds 2 x F x ld bytes more. Requires eras of at most
- * 65535 rows; pb_grow_round then scores every threshold (k_cuts 0), maintains preds_dev
- * through the rows' ids and leaves nid_dev / tnode_dev unspecified. enable 0 returns to the
- * plane path. */
+ * pb_grow_round's): from depth from_depth on, pb_grow_round keeps the round's row ids and
+ * gradients sorted by (era, frontier slot) in buffers of the context and scores each depth with
+ * one fused kernel per (node, feature tile) that streams the node's rows era by era (reading
+ * their bins from bins_dev through the ids), builds each era's histogram in LDS and runs the DES
+ * recurrence on it (frontier_cpu.cpp:261-444): those depths' histogram planes are never
+ * written, and the candidates, decisions and predictions are bit-identical to the plane path's.
+ * The shallower depths use the plane path while the context tracks the row order; between
+ * depths the rows are partitioned stably into the next frontier's slots. For many bins and
+ * nodes, where the planes dominate (255 bins, 128 nodes, 200 eras).
+ * from_depth < 0 picks the first depth whose planes would pass 1 GiB. The context then holds
+ * 2 x 10 bytes per row more. Requires eras of at most 65535 rows; pb_grow_round then scores
+ * every threshold (k_cuts 0), maintains preds_dev through the rows' ids and leaves nid_dev /
+ * tnode_dev unspecified. enable 0 returns to the plane path. */
 int pb_set_segment_mode(pb_ctx* ctx, int32_t enable, int32_t from_depth);
 
 /* Applies the per-node winners of the last pb_des_score: picks each node's split with the

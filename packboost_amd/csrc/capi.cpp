@@ -140,7 +140,6 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
     for (int i = 0; i < 2; ++i) {
-        (void)hipFree(c->sb[i].bins);
         (void)hipFree(c->sb[i].g);
         (void)hipFree(c->sb[i].row);
         (void)hipFree(c->sb[i].tnode);
@@ -635,11 +634,12 @@ namespace {
 
 // The segment-mode scorer of depth `depth` (pb::launch_seg_score) over the context's sorted rows,
 // leaving what pb_decide reads as pb_des_score does.
-int seg_score(pb_ctx* c, const int32_t* feats, int32_t K, int32_t depth, int32_t max_nodes,
+int seg_score(pb_ctx* c, const uint8_t* bins, const int32_t* feats, int32_t K, int32_t depth, int32_t max_nodes,
               const pb_split_params* p, void* stream) {
     const int nb = c->d.max_bins;
     pb::SegScoreArgs a{};
-    a.bins = c->sb[c->seg_cur].bins;
+    a.bins = bins;
+    a.row = c->sb[c->seg_cur].row;
     a.ld = c->d.ld;
     a.g = c->sb[c->seg_cur].g;
     a.seg = c->seg[c->seg_cur];
@@ -694,12 +694,12 @@ int pb_set_segment_mode(pb_ctx* c, int32_t enable, int32_t from_depth) {
     if (chunks >= INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_set_segment_mode: too many row chunks");
     int32_t from = from_depth;
     if (from < 0) {
-        // the first depth whose planes would pass 4 GiB: the shallower depths' planes cost
-        // less than moving every row's columns between depths
+        // the first depth whose planes would pass 1 GiB: below that, writing and reading the
+        // planes costs less than the fused kernel's per-era histogram passes
         const int64_t cells = (int64_t)E * c->d.max_feats * std::max(1, c->d.max_bins - 1) * 6;
         from = c->d.max_depth;
         for (int dd = 0; dd < c->d.max_depth; ++dd)
-            if ((int64_t)max_nodes_at(c, dd) * cells >= (int64_t(4) << 30)) {
+            if ((int64_t)max_nodes_at(c, dd) * cells >= (int64_t(1) << 30)) {
                 from = dd;
                 break;
             }
@@ -707,8 +707,7 @@ int pb_set_segment_mode(pb_ctx* c, int32_t enable, int32_t from_depth) {
     int rc = PB_OK;
     if (!c->sb[0].row) {
         for (int i = 0; i < 2 && rc == PB_OK; ++i) {
-            if ((rc = dev_alloc(&c->sb[i].bins, (size_t)c->d.num_features * c->d.ld, "alloc sorted bins")) ||
-                (rc = dev_alloc(&c->sb[i].g, (size_t)std::max<int64_t>(1, N), "alloc sorted rows")) ||
+            if ((rc = dev_alloc(&c->sb[i].g, (size_t)std::max<int64_t>(1, N), "alloc sorted rows")) ||
                 (rc = dev_alloc(&c->sb[i].row, (size_t)std::max<int64_t>(1, N), "alloc sorted rows")) ||
                 (rc = dev_alloc(&c->sb[i].tnode, (size_t)std::max<int64_t>(1, N), "alloc sorted rows")) ||
                 (rc = dev_alloc(&c->seg[i], (size_t)E * segw, "alloc segments")))
@@ -723,7 +722,6 @@ int pb_set_segment_mode(pb_ctx* c, int32_t enable, int32_t from_depth) {
         }
         if (rc != PB_OK) {
             for (int i = 0; i < 2; ++i) {
-                (void)hipFree(c->sb[i].bins);
                 (void)hipFree(c->sb[i].g);
                 (void)hipFree(c->sb[i].row);
                 (void)hipFree(c->sb[i].tnode);
@@ -806,12 +804,8 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
         const bool fused = d >= fused_from;
         if ((rc = mark(0))) return rc;
         if (fused) {
-            if (d == fused_from)  // every feature column in the sorted row order
-                PB_HIP(pb::launch_seg_gather(b->bins_dev, c->d.ld, c->d.num_features, c->sb[c->seg_cur].row,
-                                             c->sb[c->seg_cur].bins, c->d.num_rows, (hipStream_t)stream),
-                       "segment gather launch");
             // one fused launch: its time is the histogram phase, the scorer phase is empty
-            if ((rc = seg_score(c, f, K, d, m, &b->params, stream))) return rc;
+            if ((rc = seg_score(c, b->bins_dev, f, K, d, m, &b->params, stream))) return rc;
             if ((rc = mark(1))) return rc;
         } else {
             if ((rc = hist_build(c, bins, ld_bytes, nib, b->grad_dev, b->nid_dev, f, K, d, m,
@@ -828,10 +822,8 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
         if (seg) {
             const bool last = d + 1 == c->d.max_depth;
             const int i = c->seg_cur;
-            // the columns move once they are sorted (from the first fused depth on)
-            PB_HIP(pb::launch_seg_partition(c->ss, c->seg[i], c->seg[1 - i], c->sb[i], c->sb[1 - i],
-                                            fused ? nullptr : b->bins_dev, fused ? c->d.num_features : 0, d,
-                                            last, (hipStream_t)stream),
+            PB_HIP(pb::launch_seg_partition(c->ss, c->seg[i], c->seg[1 - i], c->sb[i], c->sb[1 - i], b->bins_dev,
+                                            d, last, (hipStream_t)stream),
                    "segment partition launch");
             if (!last) c->seg_cur = 1 - i;
         }

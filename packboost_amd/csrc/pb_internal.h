@@ -218,10 +218,12 @@ hipError_t launch_decide(const DecideCands& dc, int32_t max_nodes, const NodeTot
 // e, slot u's rows are [seg[e * segw + u], seg[e * segw + u + 1]) of the sorted buffers, and
 // [seg[e * segw + U], era end) holds the rows no longer in the frontier (U = active slots).
 // One workgroup per (slot, tile of FT features) walks the eras in order, builds each era's
-// histogram of its node's rows in LDS and runs the DES recurrence on it: the candidates and
-// wavefront winners are those of the plane scorers, bit for bit, without the planes.
+// histogram of its node's rows in LDS (bins read from the caller's columns through the sorted
+// row ids) and runs the DES recurrence on it: the candidates and wavefront winners are those of
+// the plane scorers, bit for bit, without the planes.
 struct SegScoreArgs {
-    const uint8_t* bins;   // sorted bins, uint8 [F][ld]
+    const uint8_t* bins;   // the caller's bins, uint8 [F][ld]
+    const int32_t* row;    // the sorted rows' ids
     int64_t ld;
     const float* g;        // sorted gradients [N]
     const int32_t* seg;    // [E][segw] segment starts of the current depth
@@ -241,10 +243,8 @@ struct SegScoreArgs {
     int32_t rt;            // size of the 1/n table (equal era weights)
 };
 constexpr int kSegMaxFt = 8;
-// The sorted rows of segment mode: bins [F][ld] and per row its gradient, original row id and
-// tree node id.
+// The sorted rows of segment mode: per row its gradient, original row id and tree node id.
 struct SegBuffers {
-    uint8_t* bins;
     float* g;
     int32_t* row;
     uint16_t* tnode;
@@ -261,20 +261,14 @@ struct SegState {
     int32_t* cnt_r;
     int32_t* base;   // [E * segw][2] first destination row of each (era, slot, side)
 };
-__device__ __forceinline__ bool bins_le(const uint8_t* bins, int64_t ld, const SplitRule& r, int32_t row) {
-    return (int32_t)bins[(int64_t)r.feature * ld + row] <= r.threshold;
-}
 int64_t seg_chunk_bound(int64_t N, int32_t E, int32_t segw);
 hipError_t launch_seg_begin(const float* grad, int32_t* srow, float* gs, uint16_t* stn, int64_t N,
                             const int32_t* era_off, int32_t E, int32_t segw, int32_t* seg, hipStream_t s);
-hipError_t launch_seg_gather(const uint8_t* bins, int64_t ld, int32_t F, const int32_t* row, uint8_t* sorted,
-                             int64_t N, hipStream_t s);
-// Partition of depth `depth` from src (segments seg) into dst (segments seg_next), moving the
-// first F sorted columns with the rows; at the last depth (`last`) only the tree nodes of src
-// change. orig non-null: the sorted columns are not gathered yet, the rules read orig [F][ld]
-// at the rows' ids (F must then be 0).
+// Partition of depth `depth` from src (segments seg) into dst (segments seg_next); at the last
+// depth (`last`) only the tree nodes of src change. The split rules read bins [F][ld] at the
+// rows' ids.
 hipError_t launch_seg_partition(const SegState& st, const int32_t* seg, int32_t* seg_next, const SegBuffers& src,
-                                const SegBuffers& dst, const uint8_t* orig, int32_t F, int32_t depth, bool last,
+                                const SegBuffers& dst, const uint8_t* bins, int32_t depth, bool last,
                                 hipStream_t s);
 hipError_t launch_seg_round_end(const uint16_t* stn, const int32_t* srow, const float* values, int32_t B,
                                 float lr, float* preds, int64_t N, hipStream_t s);

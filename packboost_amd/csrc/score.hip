@@ -1302,7 +1302,7 @@ __global__ __launch_bounds__(kBlock) void pick_sequential_kernel(const pb_candid
 // while no thread still reads the prefixes of this one only after the barrier that ends (1).
 // DIR: the direction term is on (dir_w != 0); UNIT: equal era weights (era_alpha <= 0).
 template <int FT, bool DIR, bool UNIT>
-__global__ __launch_bounds__(kBlock) void seg_score_kernel(SegScoreArgs a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void seg_score_kernel(SegScoreArgs a) {
     constexpr int kCpt = (FT * 254 + kBlock - 1) / kBlock;  // candidates per thread (T <= 254)
     extern __shared__ unsigned char smem[];
     const int tid = threadIdx.x;
@@ -1360,24 +1360,40 @@ __global__ __launch_bounds__(kBlock) void seg_score_kernel(SegScoreArgs a) {
         const float scale = ldexpf(1.0f, sh);
         const double inv_scale = ldexp(1.0, -sh);
         // (1) histogram of the node's rows of this era
-        // four rows per thread per step, all loads issued before the atomics
-        for (int r0 = s0 + tid; r0 < s1; r0 += 4 * kBlock) {
-            float gv[4];
-            uint32_t bv[4][FT];
+        if (ctot <= kBlock) {  // one row per thread (waves past the rows skip it)
+            const int r = s0 + tid;
+            if (r < s1) {
+                const float gv = a.g[r];
+                const int rb = a.row[r];
+                uint32_t bv[FT];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int r = min(r0 + q * kBlock, s1 - 1);
-                gv[q] = a.g[r];
-#pragma unroll
-                for (int f = 0; f < FT; ++f) bv[q][f] = col[f][r];
-            }
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                if (r0 + q * kBlock >= s1) break;
-                const unsigned long long add = grad_addend(gv[q], scale);
+                for (int f = 0; f < FT; ++f) bv[f] = col[f][rb];
+                const unsigned long long add = grad_addend(gv, scale);
 #pragma unroll
                 for (int f = 0; f < FT; ++f)
-                    if (f < nf) atomicAdd(hist + f * 256 + bv[q][f], add);
+                    if (f < nf) atomicAdd(hist + f * 256 + bv[f], add);
+            }
+        } else {
+            // four rows per thread per step, all loads issued before the atomics
+            for (int r0 = s0 + tid; r0 < s1; r0 += 4 * kBlock) {
+                float gv[4];
+                uint32_t bv[4][FT];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = min(r0 + q * kBlock, s1 - 1);
+                    gv[q] = a.g[r];
+                    const int rb = a.row[r];
+#pragma unroll
+                    for (int f = 0; f < FT; ++f) bv[q][f] = col[f][rb];
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (r0 + q * kBlock >= s1) break;
+                    const unsigned long long add = grad_addend(gv[q], scale);
+#pragma unroll
+                    for (int f = 0; f < FT; ++f)
+                        if (f < nf) atomicAdd(hist + f * 256 + bv[q][f], add);
+                }
             }
         }
         __syncthreads();

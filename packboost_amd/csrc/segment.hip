@@ -1,13 +1,12 @@
 // Segment mode: from a chosen depth on, a round keeps the fit's rows sorted by (era, frontier
-// slot) in buffers of the context, so that the fused scorer (seg_score_kernel) reads a node's
-// rows of an era as one contiguous run of every feature column. Every round starts from the
-// caller's era-major order (seg_begin). After each depth every era's rows are partitioned
-// stably into the next depth's slots: for each era, the slots' left and right children that
-// stay in the frontier, in next-slot order, then every row that left the frontier (rows of
-// nodes that did not split or of children below 2 * min_samples_leaf, then the rows that had
-// already left). Before the fused depths only the row ids, gradients and tree nodes move; at
-// the first fused depth seg_gather fetches every feature column in the sorted order, and from
-// then on the partition moves the columns too.
+// slot) in buffers of the context, so that the fused scorer (seg_score_kernel) finds a node's
+// rows of an era as one contiguous run of row ids (and gradients) and reads their bins from the
+// caller's columns through the ids. Every round starts from the caller's era-major order
+// (seg_begin). After each depth every era's rows are partitioned stably into the next depth's
+// slots: for each era, the slots' left and right children that stay in the frontier, in
+// next-slot order, then every row that left the frontier (rows of nodes that did not split or
+// of children below 2 * min_samples_leaf, then the rows that had already left). Only the row
+// ids, gradients and tree nodes move; the split rules read the caller's columns at the ids.
 //
 // The partition works on chunks of up to 256 rows of one (era, slot) segment, the slots
 // counted 0 .. U with U standing for the era's tail of rows no longer in the frontier:
@@ -16,8 +15,8 @@
 //   seg_scan     (one workgroup)    exclusive prefixes of the left and right counts over chunks;
 //   seg_bases    (one per era)      the first destination row of each (era, slot, side);
 //   seg_scatter  (one per chunk)    every row to its place (a ballot ranks it among the rows
-//                                   of its side in the chunk), with its bins, gradient, row id
-//                                   and tree node (the child's id for a split node).
+//                                   of its side in the chunk), with its gradient, row id and
+//                                   tree node (the child's id for a split node).
 // At the last depth no row moves: seg_final sets the tree node of each split node's rows.
 // Row counts are 32-bit: N < 2^31.
 #include <algorithm>
@@ -134,23 +133,21 @@ __device__ __forceinline__ bool chunk_info(const SegState& s, const int32_t* seg
     return true;
 }
 
-// Whether sorted row r goes left under the slot's rule: from the sorted columns, or, before
-// they are gathered (orig non-null), from the caller's columns at the row's id.
-__device__ __forceinline__ bool seg_goes_left(const SegState& s, const SegBuffers& src, const uint8_t* orig,
+// Whether sorted row r goes left under the slot's rule (the caller's column at the row's id).
+__device__ __forceinline__ bool seg_goes_left(const SegState& s, const SegBuffers& src, const uint8_t* bins,
                                               const SplitRule& rule, int32_t r) {
-    if (orig) return (int32_t)orig[(int64_t)rule.feature * s.ld + src.row[r]] <= rule.threshold;
-    return bins_le(src.bins, s.ld, rule, r);
+    return (int32_t)bins[(int64_t)rule.feature * s.ld + src.row[r]] <= rule.threshold;
 }
 
 __global__ __launch_bounds__(kBlock) void seg_count_kernel(SegState s, const int32_t* __restrict__ seg,
-                                                     SegBuffers src, const uint8_t* __restrict__ orig,
+                                                     SegBuffers src, const uint8_t* __restrict__ bins,
                                                      int32_t depth) {
     ChunkInfo ci;
     if (!chunk_info(s, seg, depth, blockIdx.x, ci)) return;
     const int32_t r = ci.r0 + (int32_t)threadIdx.x;
     const bool in = r < ci.r1;
     int left = 0;
-    if (in) left = ci.split ? (seg_goes_left(s, src, orig, ci.rule, r) ? 1 : 0) : 1;
+    if (in) left = ci.split ? (seg_goes_left(s, src, bins, ci.rule, r) ? 1 : 0) : 1;
     __shared__ int s_cnt[kBlock / kWave];
     int c = __popcll(__ballot(left != 0));
     if ((threadIdx.x & (kWave - 1)) == 0) s_cnt[threadIdx.x / kWave] = c;
@@ -212,8 +209,7 @@ __global__ __launch_bounds__(kBlock) void seg_bases_kernel(SegState s, const int
 
 __global__ __launch_bounds__(kBlock) void seg_scatter_kernel(SegState s, const int32_t* __restrict__ seg,
                                                        SegBuffers src, SegBuffers dst,
-                                                       const uint8_t* __restrict__ orig, int32_t F,
-                                                       int32_t depth) {
+                                                       const uint8_t* __restrict__ bins, int32_t depth) {
     ChunkInfo ci;
     if (!chunk_info(s, seg, depth, blockIdx.x, ci)) return;
     const int tid = threadIdx.x;
@@ -222,7 +218,7 @@ __global__ __launch_bounds__(kBlock) void seg_scatter_kernel(SegState s, const i
     const int32_t r = ci.r0 + tid;
     const bool in = r < ci.r1;
     int side = 0;
-    if (in && ci.split) side = seg_goes_left(s, src, orig, ci.rule, r) ? 0 : 1;
+    if (in && ci.split) side = seg_goes_left(s, src, bins, ci.rule, r) ? 0 : 1;
     // rank among the rows of the same side before this one in the chunk
     __shared__ int s_cnt[2][kBlock / kWave];
     const unsigned long long m1 = __ballot(in && side == 1);
@@ -239,29 +235,19 @@ __global__ __launch_bounds__(kBlock) void seg_scatter_kernel(SegState s, const i
     const int32_t* pre = side ? s.cnt_r : s.cnt_l;
     const int32_t d = s.base[(int64_t)ci.x * 2 + side] + (pre[blockIdx.x] - pre[s.cp[ci.x]]) + rank;
     if ((uint32_t)d >= (uint32_t)s.N) return;  // only reachable with inconsistent segments
-    // 16 columns' loads in flight before their stores
-    int f0 = 0;
-    for (; f0 + 16 <= F; f0 += 16) {
-        uint8_t v[16];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) v[k] = src.bins[(int64_t)(f0 + k) * s.ld + r];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) dst.bins[(int64_t)(f0 + k) * s.ld + d] = v[k];
-    }
-    for (; f0 < F; ++f0) dst.bins[(int64_t)f0 * s.ld + d] = src.bins[(int64_t)f0 * s.ld + r];
     dst.g[d] = src.g[r];
     dst.row[d] = src.row[r];
     dst.tnode[d] = ci.split ? (uint16_t)(ci.rule.left_id + side) : src.tnode[r];
 }
 
 __global__ __launch_bounds__(kBlock) void seg_final_kernel(SegState s, const int32_t* __restrict__ seg,
-                                                     SegBuffers cur, const uint8_t* __restrict__ orig,
+                                                     SegBuffers cur, const uint8_t* __restrict__ bins,
                                                      int32_t depth) {
     ChunkInfo ci;
     if (!chunk_info(s, seg, depth, blockIdx.x, ci)) return;
     const int32_t r = ci.r0 + (int32_t)threadIdx.x;
     if (r >= ci.r1 || !ci.split) return;
-    cur.tnode[r] = (uint16_t)(ci.rule.left_id + (seg_goes_left(s, cur, orig, ci.rule, r) ? 0 : 1));
+    cur.tnode[r] = (uint16_t)(ci.rule.left_id + (seg_goes_left(s, cur, bins, ci.rule, r) ? 0 : 1));
 }
 
 // preds[row] += float32(lr) * (B float32 adds of the leaf value), the operations of
@@ -281,38 +267,12 @@ __global__ __launch_bounds__(kBlock) void seg_round_end_kernel(const uint16_t* _
     }
 }
 
-// The sorted bins of every feature: sorted[f][i] = bins[f][row[i]] (rows of one era stay in
-// the era's byte range of each column, so the reads hit few lines).
-__global__ __launch_bounds__(kBlock) void seg_gather_kernel(const uint8_t* __restrict__ bins, int64_t ld, int32_t F,
-                                                      const int32_t* __restrict__ row, uint8_t* __restrict__ sorted,
-                                                      int64_t N) {
-    const int64_t stride = (int64_t)gridDim.x * kBlock;
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < N; i += stride) {
-        const int64_t r = row[i];
-        int f0 = 0;
-        for (; f0 + 16 <= F; f0 += 16) {
-            uint8_t v[16];
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = bins[(int64_t)(f0 + k) * ld + r];
-#pragma unroll
-            for (int k = 0; k < 16; ++k) sorted[(int64_t)(f0 + k) * ld + i] = v[k];
-        }
-        for (; f0 < F; ++f0) sorted[(int64_t)f0 * ld + i] = bins[(int64_t)f0 * ld + r];
-    }
-}
-
 int grid_of_rows(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>((n + kBlock - 1) / kBlock, 8192)); }
 
 }  // namespace
 
 int64_t seg_chunk_bound(int64_t N, int32_t E, int32_t segw) {
     return (N + kSegChunk - 1) / kSegChunk + (int64_t)E * segw;
-}
-
-hipError_t launch_seg_gather(const uint8_t* bins, int64_t ld, int32_t F, const int32_t* row, uint8_t* sorted,
-                             int64_t N, hipStream_t s) {
-    hipLaunchKernelGGL(seg_gather_kernel, dim3(grid_of_rows(N)), dim3(kBlock), 0, s, bins, ld, F, row, sorted, N);
-    return hipGetLastError();
 }
 
 hipError_t launch_seg_begin(const float* grad, int32_t* srow, float* gs, uint16_t* stn, int64_t N,
@@ -323,22 +283,20 @@ hipError_t launch_seg_begin(const float* grad, int32_t* srow, float* gs, uint16_
 }
 
 hipError_t launch_seg_partition(const SegState& st, const int32_t* seg, int32_t* seg_next, const SegBuffers& src,
-                                const SegBuffers& dst, const uint8_t* orig, int32_t F, int32_t depth, bool last,
+                                const SegBuffers& dst, const uint8_t* bins, int32_t depth, bool last,
                                 hipStream_t s) {
-    if (orig && F != 0) return hipErrorInvalidValue;  // unsorted columns are not moved
     const int64_t bound = seg_chunk_bound(st.N, st.E, st.segw);
     if (bound > INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL(seg_chunks_kernel, dim3(1), dim3(kBlock), 0, s, st, seg, depth);
     if (last) {
-        hipLaunchKernelGGL(seg_final_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, orig, depth);
+        hipLaunchKernelGGL(seg_final_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, bins, depth);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL(seg_count_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, orig, depth);
+    hipLaunchKernelGGL(seg_count_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, bins, depth);
     hipLaunchKernelGGL(seg_scan_kernel, dim3(1), dim3(kBlock), 0, s, st, depth);
     hipLaunchKernelGGL(seg_bases_kernel, dim3((st.E + kBlock - 1) / kBlock), dim3(kBlock), 0, s, st, seg, seg_next,
                        depth);
-    hipLaunchKernelGGL(seg_scatter_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, dst, orig, F,
-                       depth);
+    hipLaunchKernelGGL(seg_scatter_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, dst, bins, depth);
     return hipGetLastError();
 }
 

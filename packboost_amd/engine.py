@@ -117,8 +117,8 @@ class DeviceFit:
         fit_mode: "planes" (histogram planes in HBM, then the scorer), "segments" (from a
         depth on, rows kept sorted by frontier node and one fused histogram + scorer kernel
         per depth: pb_set_segment_mode; PB_SEG_FROM_DEPTH sets that depth, else the first
-        whose planes would pass 4 GiB) or "auto" (default; the environment variable
-        PB_FIT_MODE overrides it): segments when the deepest depth's planes would pass 4 GiB
+        whose planes would pass 1 GiB) or "auto" (default; the environment variable
+        PB_FIT_MODE overrides it): segments when the deepest depth's planes would pass 1 GiB
         and the fit allows them (full threshold sweep, eras of at most 65535 rows)."""
         lib = _hip.load()
         if bins_fm.dtype != torch.uint8 or bins_fm.dim() != 2 or not bins_fm.is_cuda:
@@ -183,7 +183,7 @@ class DeviceFit:
         if mode == "segments" and not segments_ok:
             raise ValueError("fit_mode 'segments' needs k_cuts 0 and eras of at most 65535 rows")
         plane_bytes = [self.E * m * self.K * max(1, self.nb - 1) * 6 for m in self.max_nodes]
-        self.segments = mode == "segments" or (mode == "auto" and segments_ok and plane_bytes[-1] >= (4 << 30))
+        self.segments = mode == "segments" or (mode == "auto" and segments_ok and plane_bytes[-1] >= (1 << 30))
         # histogram planes for the depths the plane path scores (all of them, or those before
         # the first fused depth of a segment-mode fit: the deepest planes can take tens of GB)
         plane_depths = self.D
@@ -192,7 +192,7 @@ class DeviceFit:
             if env is not None:
                 plane_depths = min(self.D, max(0, int(env)))
             else:
-                plane_depths = next((d for d, b in enumerate(plane_bytes) if b >= (4 << 30)), self.D)
+                plane_depths = next((d for d, b in enumerate(plane_bytes) if b >= (1 << 30)), self.D)
             _hip.check(lib.pb_set_segment_mode(ctx, 1, plane_depths), "pb_set_segment_mode")
         self.seg_from = plane_depths if self.segments else None
         plane = max(int(lib.pb_hist_plane_elems(ctx, m)) for m in self.max_nodes[:max(1, plane_depths)])
