@@ -12,6 +12,9 @@
   oracle scorer on the whole device planes of sampled nodes (every candidate bit-identical,
   the decision equal), every node's decision a top-scoring device candidate, and the
   partition rule with exact left/right counts.
+- Config 4 whole rounds: 3 rounds of the full workload (B 64, D 8) in segment mode (fused
+  kernel from depth 3, the default there) and on the plane path: every decision record and the
+  training predictions bit-identical.
 - Config 5 (5,000,000 x 2376 uint8 bins, 250 packs x 8 distinct depth-6 trees): the full
   prediction, compared on a 50,000-row sample with the oracle's tree-order float32 sum
   (booster.py:709-712) within 1e-5, and leaf indices of every tree bit-exact on that sample
@@ -206,6 +209,49 @@ def test_config4_depth7_fullsize(hip, oracle_mod):
 
 
 # ----------------------------------------------------------------------------- config 5
+def test_config4_rounds_segments_match_planes(hip):
+    """Config 4's whole rounds (B 64, D 8, 1M x 500, 255 bins, 200 eras) in segment mode and on
+    the plane path of the same data: the decision logs and predictions are equal bit for bit."""
+    import torch
+
+    from packboost_amd import PackBoostConfig
+    from packboost_amd.engine import DeviceFit
+
+    ld = (N4 + 15) // 16 * 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(45)
+    bins = torch.randint(0, NB4, (F4, ld), dtype=torch.uint8, device="cuda", generator=g)
+    bins[:, N4:] = 0
+    noise = torch.randn(N4, device="cuda", generator=g)
+    b0, b1, b2 = (bins[k, :N4].float() for k in (0, 1, 2))
+    y = ((b0 - 127.0) / 128.0 + 0.5 * (b1 > 100).float() - 0.3 * (b2 < 40).float() + 0.5 * noise).contiguous()
+    sizes = np.array([len(a) for a in np.array_split(np.arange(N4), E4)], dtype=np.int64)
+    offs = np.zeros(E4 + 1, np.int64)
+    np.cumsum(sizes, out=offs[1:])
+    cfg = PackBoostConfig(pack_size=64, max_depth=8, learning_rate=0.1, lambda_l2=1e-6, lambda_dro=0.0,
+                          min_samples_leaf=20, max_bins=NB4, layer_feature_fraction=1.0, random_state=42,
+                          prebinned=True)
+    out = {}
+    for mode in ("segments", "planes"):
+        print(f"[config4 rounds] {mode}", flush=True)
+        fit = DeviceFit(bins, N4, y, offs.astype(np.int32), cfg, fit_mode=mode)
+        try:
+            assert fit.segments == (mode == "segments")
+            if mode == "segments":
+                assert fit.seg_from == 3
+            logs = [log.decisions.copy() for log, _, _ in fit.rounds(torch.Generator().manual_seed(7), 3)]
+            torch.cuda.synchronize()
+            out[mode] = (logs, fit.preds[:N4].cpu().numpy().copy())
+        finally:
+            fit.close()
+    seg_logs, seg_preds = out["segments"]
+    pl_logs, pl_preds = out["planes"]
+    for r, (a, b) in enumerate(zip(seg_logs, pl_logs)):
+        assert a.tobytes() == b.tobytes(), f"round {r}: decision records differ"
+    assert int(np.count_nonzero(pl_logs[0]["split"])) > 64  # the trees grow past depth 6
+    np.testing.assert_array_equal(seg_preds, pl_preds)
+
+
 def test_config5_predict(hip, oracle_mod):
     import torch
 
