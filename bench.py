@@ -303,8 +303,10 @@ def bench_predict(args, c: dict) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed rounds (default 20; config 4: 10, the rounds before its default learning "
+                         "rate x B = 6.4 diverges and the trees stop at the root)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed rounds first (default 3; config 4: 1)")
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--rows", type=int, default=0, help="override row count (quick runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -329,6 +331,10 @@ def main() -> int:
     c = dict(CONFIGS[args.config])
     if args.rows:
         c["rows"] = args.rows
+    if args.steps is None:
+        args.steps = 10 if args.config == 4 else 20
+    if args.warmup is None:
+        args.warmup = 1 if args.config == 4 else 3
     torch.cuda.set_device(0)
     copy_gbs = copy_peak_gbs()
     if args.config == 5:
@@ -375,6 +381,34 @@ def main() -> int:
         tree_arrays_from_log(log, cfg, N)
     torch.cuda.synchronize()
     phase_raw, _ = read_profile()
+    fit.close()
+
+    # Untimed for `value`: the same rounds with the per-round train era correlation that
+    # PackBoost.fit logs (pb_era_corr on a side stream, read back each round), the reference's
+    # log_metrics outside its round_seconds span (booster.py:654-655).
+    from packboost_amd.booster import _era_corr_device
+
+    fit = DeviceFit(bins, N, y, off, cfg)
+    side = torch.cuda.Stream()
+    era_off_dev = torch.from_numpy(np.asarray(off, dtype=np.int32)).cuda()
+    corr_scratch = torch.empty(len(off), dtype=torch.float64, device="cuda")
+    rng_m = torch.Generator().manual_seed(42)
+    corr = float("nan")
+
+    def rounds_with_metrics(n: int) -> None:
+        nonlocal corr
+        for log, preds_after, ready in fit.rounds(rng_m, n):
+            tree_arrays_from_log(log, cfg, N)
+            with torch.cuda.stream(side):
+                side.wait_event(ready)
+                corr = _era_corr_device(y, preds_after, era_off_dev, corr_scratch)
+
+    rounds_with_metrics(args.warmup)
+    torch.cuda.synchronize()
+    t_m = time.perf_counter()  # the same rounds as the timed region, bracketed the same way
+    rounds_with_metrics(args.steps)
+    torch.cuda.synchronize()
+    with_metrics_s = time.perf_counter() - t_m
 
     # histogram roofline, summed over the profiled rounds. Algorithmic bytes per launch, with the
     # reference formats' per-unit figures: rows of active nodes x K (one byte per bin code)
@@ -401,8 +435,14 @@ def main() -> int:
             rows = int(log.decisions[base: base + u]["node_count"].astype(np.int64).sum())
             hist_bytes += rows * K + rows * 8 + u * E * K * nb * 8
             moved_bytes += rows * K * bin_bytes + rows * 6 + u * E * (K * (nb - 1) * 6 + 8)
+    # launches per depth that had active nodes (a round that stops early still launches its
+    # deeper depths, which exit at once; they are not counted as launches of the kernel)
+    n_act = np.zeros(D, dtype=np.int64)
+    for r, log in enumerate(logs):
+        if r % PROFILE_EVERY == 0:
+            n_act += (np.asarray(log.u_active[:D]) > 0)
     hist_ms = float(prof_ms[0][:hist_depths].sum())
-    n_hist = int(prof_n[0][:hist_depths].sum())
+    n_hist = int(n_act[:hist_depths].sum())
     achieved = moved_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     ref_format_gbs = hist_bytes / (hist_ms * 1e-3) / 1e9 if hist_ms > 0 else 0.0
     rounds_per_s = args.steps / elapsed
@@ -453,11 +493,18 @@ def main() -> int:
             "reference_format_frac": round(ref_format_gbs / HBM_PEAK_GBS, 4),
             "reference_format_bytes": "rows*K*1 + rows*8 + U*E*K*nb*8 per depth (reference layouts, no hess)",
         },
+        "with_round_metrics": {
+            "rounds_per_s": round(args.steps / with_metrics_s, 4),
+            "ms_per_round": round(with_metrics_s * 1e3 / args.steps, 4),
+            "metric": "train era correlation per round on the device (pb_era_corr), as PackBoost.fit logs it",
+            "last_train_corr": round(corr, 6),
+        },
         "profiled_rounds": {"hist_events": f"every {PROFILE_EVERY}th timed round",
                             "phase_breakdown": f"first {n_phase} rounds replayed untimed"},
         "phase_ms_per_round": {k: round(v / n_phase, 4) for k, v in phase_ms.items()},
-        "hist_ms_per_depth": [round(float(prof_ms[0, d]) / max(1, int(prof_n[0, d])), 4)
+        "hist_ms_per_depth": [round(float(prof_ms[0, d]) / max(1, int(n_act[d])), 4)
                               for d in range(D)],
+        "full_depth_rounds": int(sum(1 for log in logs if int(log.u_active[D - 1]) > 0)),
         "cpu_baseline": None,
     }
     fit.close()

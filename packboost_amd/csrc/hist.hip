@@ -60,15 +60,6 @@ struct DivU16 {
     __device__ uint32_t div(uint32_t n) const { return one ? n : __umulhi(n, m); }
 };
 
-// v moved across lanes by the DPP control CTRL (both 32-bit halves); lanes with no source in
-// range, and the rows outside ROW_MASK, read 0 (bound_ctrl, old value 0).
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, true);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf, true);
-    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
-}
-
 // Byte-wise x * m + y for four bytes at once, when every byte's result stays below 256: in
 // each 16-bit half (hi * 256 + lo) * m + (yh * 256 + yl) = (hi * m + yh) * 256 + (lo * m + yl)
 // with no carry out of the low byte, so one full-rate packed 16-bit multiply-add

@@ -39,6 +39,27 @@ __device__ __forceinline__ int era_grad_scale(double bound) {
     return min(44 - ex, 126);
 }
 
+// v moved across lanes by the DPP control CTRL (both 32-bit halves); lanes with no source in
+// range, and the rows outside ROW_MASK, read 0 (bound_ctrl, old value 0).
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, ROW_MASK, 0xf, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)(v >> 32), CTRL, ROW_MASK, 0xf, true);
+    return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// Inclusive scan of v over the 64 lanes of a wavefront: a scan inside each 16-lane row by DPP
+// row shifts, then the row totals broadcast across rows (no LDS round trip).
+__device__ __forceinline__ unsigned long long wave_scan_incl_u64(unsigned long long v) {
+    v += dpp_u64<0x111>(v);       // row_shr:1
+    v += dpp_u64<0x112>(v);       // row_shr:2
+    v += dpp_u64<0x114>(v);       // row_shr:4
+    v += dpp_u64<0x118>(v);       // row_shr:8
+    v += dpp_u64<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_u64<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 // One row's 64-bit histogram addend (q << 16) + 1 with q = round(g * scale) (|q| < 2^45): the
 // count 1 in the low 16 bits, the fixed-point grad above it, built from two 32-bit halves. In
 // float, exactly: xq = q, xh = floor(q / 2^16) (the high word), xl = q - xh * 2^16 in [0, 2^16)

@@ -1408,13 +1408,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
                 v[j] = run;
                 *cell = 0ull;
             }
-            unsigned long long excl = run;  // inclusive scan of the lane totals, then shifted
-#pragma unroll
-            for (int m = 1; m < kWave; m <<= 1) {
-                const unsigned long long o = __shfl_up(excl, m);
-                if (lane >= m) excl += o;
-            }
-            excl -= run;
+            const unsigned long long excl = wave_scan_incl_u64(run) - run;  // lanes before this one
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int b = 4 * lane + j;

@@ -508,26 +508,36 @@ def tree_arrays_from_log(log: RoundLog, cfg: PackBoostConfig, num_rows: int) -> 
     if num_rows > 0:
         value[0] = -float(np.float32(log.root_grad)) / (float(np.float32(num_rows)) + lam)
     D = int(cfg.max_depth)
+    # one depth at a time (a depth's leaf values overwrite the child values its parents set),
+    # each as whole-array float64 operations: the same IEEE results as Python floats
     for d in range(D):
         ua = int(log.u_active[d])
         if ua <= 0:
             break
         recs = log.decisions[(1 << d) - 1: (1 << d) - 1 + ua]
-        for r in recs:
-            nid = int(r["node_id"])
-            if int(r["split"]):
-                feature[nid] = int(r["feature"])
-                threshold[nid] = int(r["threshold"])
-                is_leaf[nid] = False
-                li, ri = int(r["left_id"]), int(r["right_id"])
-                left[nid], right[nid] = li, ri
-                value[li] = -float(r["left_grad"]) / (float(r["left_hess"]) + lam)
-                value[ri] = -float(r["right_grad"]) / (float(r["right_hess"]) + lam)
-            else:
-                cnt = int(r["node_count"])
-                value[nid] = 0.0 if cnt == 0 else -float(r["node_grad"]) / (float(np.float32(cnt)) + lam)
-                feature[nid], threshold[nid], left[nid], right[nid] = -1, 0, -1, -1
-                is_leaf[nid] = True
+        nid = recs["node_id"].astype(np.int64)
+        sp = recs["split"] != 0
+        sn = nid[sp]
+        if sn.size:
+            r = recs[sp]
+            li = r["left_id"].astype(np.int64)
+            ri = r["right_id"].astype(np.int64)
+            feature[sn] = r["feature"]
+            threshold[sn] = r["threshold"]
+            is_leaf[sn] = False
+            left[sn], right[sn] = li, ri
+            value[li] = -r["left_grad"].astype(np.float64) / (r["left_hess"].astype(np.float64) + lam)
+            value[ri] = -r["right_grad"].astype(np.float64) / (r["right_hess"].astype(np.float64) + lam)
+        ln = nid[~sp]
+        if ln.size:
+            r = recs[~sp]
+            cnt = r["node_count"].astype(np.int64)
+            den = cnt.astype(np.float32).astype(np.float64) + lam
+            with np.errstate(divide="ignore", invalid="ignore"):
+                v = -r["node_grad"].astype(np.float64) / den
+            value[ln] = np.where(cnt == 0, 0.0, v)
+            feature[ln], threshold[ln], left[ln], right[ln] = -1, 0, -1, -1
+            is_leaf[ln] = True
     return {"feature": feature, "threshold": threshold, "left": left, "right": right,
             "value": value, "is_leaf": is_leaf}
 
