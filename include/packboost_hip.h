@@ -213,7 +213,10 @@ int pb_round_end(pb_ctx* ctx, const uint16_t* tnode_dev, const float* values_dev
 typedef struct {
     int32_t u_active[PB_MAX_DEPTH + 1];  /* active unique nodes per depth */
     int32_t tree_size;                   /* nodes in each tree of the round */
-    int32_t reserved[6];
+    int32_t reserved[6];                 /* [0]: 1 when the round's gradients (preds - y) were
+                                          * not all finite; its histograms have no meaning then
+                                          * (the fixed-point sums hold no NaN or infinity) and the
+                                          * caller should stop. [1..5]: 0 */
 } pb_round_header;  /* 96 bytes */
 
 /* Device buffers of one fit, bound once for pb_grow_round. All row arrays hold rows_padded

@@ -319,6 +319,13 @@ class PackBoost:
                 self._round_metrics.append(metrics)
                 if round_callback is not None:
                     round_callback(round_idx + 1, metrics)
+        except BaseException:
+            # e.g. FloatingPointError from a round with non-finite gradients: release the
+            # fit's device state before the error propagates
+            torch.cuda.synchronize(device)
+            fitter.close()
+            self._fitter = None
+            raise
         finally:
             torch.cuda.synchronize(device)
         self._train_preds = fitter.preds[:N].clone()

@@ -92,6 +92,7 @@ __global__ void reset_kernel(Frontier* st, int32_t root_active, int32_t* cur_ids
         for (int d = 0; d <= PB_MAX_DEPTH; ++d) st->u_active[d] = 0;
         st->u_active[0] = root_active;
         st->tree_size = 1;
+        st->reserved[kNonFinite] = 0;
         cur_ids[0] = 0;
     }
 }
@@ -141,15 +142,18 @@ __global__ __launch_bounds__(kBlock) void round_begin_kernel(const float* __rest
 
 // One thread per era: the era's |grad| sum is at most the sum over the windows it overlaps;
 // sh_era[e] = era_grad_scale of that bound.
+// Also flags the round (Frontier::reserved[kNonFinite]) when an era's |grad| bound is not finite:
+// a NaN or infinite gradient (or one whose window sum overflows float) has no fixed-point value.
 __global__ __launch_bounds__(kBlock) void era_scale_kernel(const int32_t* __restrict__ era_off, int32_t E,
                                                        const float* __restrict__ win_sum,
-                                                       int32_t* __restrict__ sh_era) {
+                                                       int32_t* __restrict__ sh_era, Frontier* st) {
     const int e = blockIdx.x * kBlock + threadIdx.x;
     if (e >= E) return;
     const int64_t r0 = era_off[e], r1 = era_off[e + 1];
     double b = 0.0;
     if (r1 > r0)
         for (int64_t w = r0 / kGradWinRows; w <= (r1 - 1) / kGradWinRows; ++w) b += (double)win_sum[w];
+    if (!isfinite(b)) st->reserved[kNonFinite] = 1;
     sh_era[e] = era_grad_scale(b * (1.0 + 1.0 / 1024.0));
 }
 
@@ -186,7 +190,7 @@ __global__ void round_header_kernel(const Frontier* st, pb_round_header* h) {
     const int i = threadIdx.x;
     if (i <= PB_MAX_DEPTH) h->u_active[i] = st->u_active[i];
     if (i == 0) h->tree_size = st->tree_size;
-    if (i < 6) h->reserved[i] = 0;
+    if (i < 6) h->reserved[i] = i == 0 ? st->reserved[kNonFinite] : 0;
 }
 
 int grid_for(int64_t work, int per_block, int cap) {
@@ -226,7 +230,7 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(era_scale_kernel, dim3((E + kBlock - 1) / kBlock), dim3(kBlock), 0, s, era_off,
-                       E, win_sum, sh_era);
+                       E, win_sum, sh_era, st);
     return hipGetLastError();
 }
 

@@ -20,8 +20,9 @@ constexpr int kGradWinRows = kBlock * 4;  // rows per window of the round's |gra
 struct Frontier {
     int32_t u_active[PB_MAX_DEPTH + 1];  // active nodes per depth
     int32_t tree_size;                   // next TreeBuilder id
-    int32_t reserved[7];
+    int32_t reserved[7];                 // [kNonFinite]: the round's gradients were not all finite
 };
+constexpr int kNonFinite = 0;
 
 // Fixed-point gradient scale of one era: rows add q = round(g * 2^sh) into the 48-bit grad field
 // of a histogram word. round_begin sums |g| over windows of kGradWinRows consecutive rows, and

@@ -58,6 +58,14 @@ def subset_size(cfg: PackBoostConfig, num_features: int) -> int:
     return min(k, num_features)
 
 
+# A round whose gradients (preds - y) are not all finite: the predictions overflowed (a learning
+# rate x pack_size that overshoots) or the targets hold NaN/inf. The histograms are exact
+# fixed-point sums and hold no NaN or infinity, so such a round cannot follow the reference's
+# float arithmetic (whose NaN scores end the splits); the fit stops with this error instead.
+NONFINITE_MSG = ("gradients are not finite (the predictions overflowed or y holds NaN/inf); "
+                 "lower learning_rate x pack_size or clean the targets")
+
+
 @dataclass
 class RoundLog:
     """Decisions of one round, as the host reads them back."""
@@ -365,6 +373,8 @@ class DeviceFit:
         nd = self._n_dec * _hip.DECISION_DTYPE.itemsize
         dec = np.frombuffer(raw[:nd].tobytes(), dtype=_hip.DECISION_DTYPE)
         hdr = np.frombuffer(raw[nd:].tobytes(), dtype=_hip.HEADER_DTYPE)[0]
+        if int(hdr["reserved"][0]):
+            raise FloatingPointError(NONFINITE_MSG)
         u = np.asarray(hdr["u_active"], dtype=np.int32)
         drawn = int(np.count_nonzero(u[: self.D] > 0))
         return RoundLog(u_active=u[: self.D + 1].copy(), tree_size=int(hdr["tree_size"]),
@@ -467,6 +477,8 @@ class DeviceFit:
         _hip.check(self.lib.pb_frontier_counts(self.ctx, u.ctypes.data, ctypes.byref(ts),
                                                _hip.stream_ptr(self.stream)), "pb_frontier_counts")
         dec = np.frombuffer(self.dec_host.numpy().tobytes(), dtype=_hip.DECISION_DTYPE).copy()
+        if not bool(torch.isfinite(self.grad[: self.N]).all()):
+            raise FloatingPointError(NONFINITE_MSG)
         drawn = int(np.count_nonzero(u[: self.D] > 0))
         if u[0] > 0:
             root_grad = float(dec[0]["node_grad"])

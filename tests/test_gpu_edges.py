@@ -187,3 +187,38 @@ def test_255_bins_fit(hip, oracle_mod):
     ref = oracle_mod.fit(bins, y, era.astype(np.int64), num_rounds=3, **kw)
     _compare_rounds(model._rounds, ref.rounds)
     np.testing.assert_allclose(model.predict(X), oracle_mod.predict(ref.rounds, 2, 0.1, bins), atol=1e-5)
+
+
+@pytest.mark.parametrize("case", ["nan_target", "overflowing_predictions", "root_too_small"])
+def test_nonfinite_gradients_stop_the_fit(hip, case):
+    """Gradients that are not finite have no fixed-point value: the round is flagged on the
+    device (pb_round_header.reserved[0]; the per-phase path checks the gradients) and the fit
+    raises FloatingPointError instead of growing trees from meaningless histograms. The
+    reference's float sums would carry the NaN into its scores instead; this build stops."""
+    from packboost_amd import PackBoost, PackBoostConfig
+
+    rng = np.random.default_rng(11)
+    N, F = 3000, 6
+    X = rng.standard_normal((N, F)).astype(np.float32)
+    y = (X[:, 0] + 0.1 * rng.standard_normal(N)).astype(np.float32)
+    era = np.repeat(np.arange(6), N // 6)
+    kw = dict(max_depth=3, max_bins=16, min_samples_leaf=10, random_state=0)
+    if case == "nan_target":
+        y[17] = np.nan
+        cfg, rounds = PackBoostConfig(pack_size=2, learning_rate=0.1, **kw), 2
+    elif case == "overflowing_predictions":
+        # learning_rate x pack_size = 128: the residuals grow ~127x per round and the
+        # predictions pass float32's range within about 20 rounds
+        cfg, rounds = PackBoostConfig(pack_size=64, learning_rate=2.0, **kw), 60
+    else:  # a root below 2 x min_samples_leaf runs the per-phase path
+        y[5] = np.inf
+        cfg, rounds = PackBoostConfig(pack_size=2, learning_rate=0.1, **{**kw, "min_samples_leaf": 2000}), 2
+    print(f"[nonfinite] {case}", flush=True)
+    model = PackBoost(cfg)
+    with pytest.raises(FloatingPointError, match="not finite"):
+        model.fit(X, y, era, num_rounds=rounds)
+    assert model._fitter is None
+    # the same model object fits again on finite data
+    y_ok = np.nan_to_num(y, nan=0.0, posinf=0.0)
+    model2 = PackBoost(PackBoostConfig(pack_size=2, learning_rate=0.1, **kw)).fit(X, y_ok, era, num_rounds=2)
+    assert np.all(np.isfinite(model2.predict(X[:100])))
