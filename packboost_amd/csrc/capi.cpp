@@ -61,6 +61,7 @@ struct pb_ctx {
     // segment mode (pb_set_segment_mode): rows sorted by (era, slot) in two buffer sets
     bool seg_mode;
     int32_t seg_from;           // first depth scored by the fused kernel
+    int32_t seg_ft;             // cap on the fused kernel's features per workgroup (0: rule)
     int32_t seg_cur;            // buffer set holding the current depth's rows
     pb::SegBuffers sb[2];
     int32_t* seg[2];            // [E][segw] segment starts of the rows in sb[i]
@@ -225,8 +226,7 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
                                                         c->score_wgs);
             c->wmax = std::max(c->wmax, sh.ntiles * sh.wpt);
         }
-    for (int dd = 0; dd < d.max_depth; ++dd) {  // the segment-mode scorer's winners
-        const int32_t ft = pb::seg_score_fts(max_nodes_at(c, dd), d.max_feats);
+    for (int32_t ft = 1; ft <= pb::kSegMaxFt; ft *= 2) {  // the segment-mode scorer's winners, any tile width
         const int32_t nt = (d.max_feats + ft - 1) / ft;
         c->wmax = std::max(c->wmax, nt * std::min(4, (ft * std::max(1, d.max_bins - 1) + pb::kWave - 1) / pb::kWave));
     }
@@ -659,6 +659,7 @@ int seg_score(pb_ctx* c, const uint8_t* bins, const int32_t* feats, int32_t K, i
     a.depth = depth;
     a.cand_w = c->cand_w;
     a.fts = pb::seg_score_fts(max_nodes, K);
+    if (c->seg_ft > 0) a.fts = std::min<int32_t>(a.fts, c->seg_ft);  // PB_SEG_FT: at most this many
     a.ntiles = (K + a.fts - 1) / a.fts;
     a.wpt = std::min(4, (a.fts * a.T + pb::kWave - 1) / pb::kWave);
     a.seq = c->seq;
@@ -745,6 +746,9 @@ int pb_set_segment_mode(pb_ctx* c, int32_t enable, int32_t from_depth) {
     c->ss.st = c->st;
     c->ss.rules = c->rules;
     c->seg_from = std::min<int32_t>(from, c->d.max_depth);
+    c->seg_ft = (int32_t)env_int("PB_SEG_FT", 0);
+    if (c->seg_ft != 0 && c->seg_ft != 1 && c->seg_ft != 2 && c->seg_ft != 4)
+        return fail(PB_ERR_INVALID, "pb_set_segment_mode: PB_SEG_FT must be 1, 2 or 4");
     c->seg_mode = true;
     return PB_OK;
 }

@@ -264,7 +264,7 @@ struct SegScoreArgs {
     NodeTotal* ntot;
     int32_t rt;            // size of the 1/n table (equal era weights)
 };
-constexpr int kSegMaxFt = 8;
+constexpr int kSegMaxFt = 4;  // 8 measured slower: 123 VGPRs hold it to 4 waves per SIMD (FT 4: 6)
 // The sorted rows of segment mode: per row its gradient, original row id and tree node id.
 struct SegBuffers {
     float* g;

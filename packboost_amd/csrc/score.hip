@@ -1658,7 +1658,6 @@ hipError_t launch_seg_score(const SegScoreArgs& a, int32_t max_nodes, hipStream_
         case 1: return pick(std::integral_constant<int, 1>{});
         case 2: return pick(std::integral_constant<int, 2>{});
         case 4: return pick(std::integral_constant<int, 4>{});
-        case 8: return pick(std::integral_constant<int, 8>{});
         default: return hipErrorInvalidValue;
     }
 }
