@@ -1301,8 +1301,13 @@ __global__ __launch_bounds__(kBlock) void pick_sequential_kernel(const pb_candid
 // scorer's era step on its candidates. Two barriers per era: the next era's histogram is built
 // while no thread still reads the prefixes of this one only after the barrier that ends (1).
 // DIR: the direction term is on (dir_w != 0); UNIT: equal era weights (era_alpha <= 0).
+// Occupancy targets: 4 features fit 64 VGPRs (8 waves per SIMD) without the direction term and
+// 77 with it (6 waves); narrower tiles keep the compiler's own allocation (4 = no constraint).
+template <int FT, bool DIR>
+constexpr int seg_waves_per_eu() { return FT == 4 ? (DIR ? 6 : 8) : 4; }
+
 template <int FT, bool DIR, bool UNIT>
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void seg_score_kernel(SegScoreArgs a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(seg_waves_per_eu<FT, DIR>()))) void seg_score_kernel(SegScoreArgs a) {
     constexpr int kCpt = (FT * 254 + kBlock - 1) / kBlock;  // candidates per thread (T <= 254)
     extern __shared__ unsigned char smem[];
     const int tid = threadIdx.x;
