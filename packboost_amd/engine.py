@@ -126,8 +126,9 @@ class DeviceFit:
         depth on, rows kept sorted by frontier node and one fused histogram + scorer kernel
         per depth: pb_set_segment_mode; PB_SEG_FROM_DEPTH sets that depth, else the first
         whose planes would pass 1 GiB) or "auto" (default; the environment variable
-        PB_FIT_MODE overrides it): segments when the deepest depth's planes would pass 1 GiB
-        and the fit allows them (full threshold sweep, eras of at most 65535 rows)."""
+        PB_FIT_MODE overrides it): segments when the deepest depth's planes would pass 1 GiB,
+        there are 64 or more thresholds per feature and the fit allows them (full threshold
+        sweep, eras of at most 65535 rows)."""
         lib = _hip.load()
         if bins_fm.dtype != torch.uint8 or bins_fm.dim() != 2 or not bins_fm.is_cuda:
             raise ValueError("bins_fm must be a CUDA uint8 tensor [F, ld]")
@@ -191,7 +192,10 @@ class DeviceFit:
         if mode == "segments" and not segments_ok:
             raise ValueError("fit_mode 'segments' needs k_cuts 0 and eras of at most 65535 rows")
         plane_bytes = [self.E * m * self.K * max(1, self.nb - 1) * 6 for m in self.max_nodes]
-        self.segments = mode == "segments" or (mode == "auto" and segments_ok and plane_bytes[-1] >= (1 << 30))
+        # auto: only where the fused kernel's threads have thresholds to score (one per threshold,
+        # 4 features per workgroup: with few bins most of a workgroup would idle)
+        self.segments = mode == "segments" or (mode == "auto" and segments_ok and self.nb - 1 >= 64
+                                               and plane_bytes[-1] >= (1 << 30))
         # histogram planes for the depths the plane path scores (all of them, or those before
         # the first fused depth of a segment-mode fit: the deepest planes can take tens of GB)
         plane_depths = self.D

@@ -81,3 +81,19 @@ def test_segments_refuse_k_cuts(hip, monkeypatch):
     with pytest.raises(ValueError, match="segments"):
         _fit("segments", monkeypatch, X, y, era, 1, pack_size=1, max_depth=3, max_bins=255, k_cuts=8,
              min_samples_leaf=10, random_state=1)
+
+
+def test_segments_many_eras(hip, monkeypatch):
+    """5000 eras, more than the 4096 entries of the 1/n table: past the table the fused kernel's
+    Welford factor falls back to IEEE division, as the wide scorer's does."""
+    X, y, era = _data(7, 100_000, 8, 5000)
+    assert np.unique(era).size > 4096
+    kw = dict(pack_size=2, max_depth=4, learning_rate=0.2, min_samples_leaf=5, max_bins=128, random_state=3)
+    planes = _fit("planes", monkeypatch, X, y, era, 2, **kw)
+    for from_depth in (0, 2):
+        seg = _fit("segments", monkeypatch, X, y, era, 2, from_depth, **kw)
+        for r, (a, b) in enumerate(zip(seg._rounds, planes._rounds)):
+            for key in ("feature", "threshold", "value"):
+                np.testing.assert_array_equal(np.asarray(a[key]), np.asarray(b[key]),
+                                              err_msg=f"from {from_depth} round {r} {key}")
+        np.testing.assert_array_equal(seg._train_preds.cpu().numpy(), planes._train_preds.cpu().numpy())
