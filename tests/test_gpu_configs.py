@@ -15,6 +15,10 @@
 - Config 4 whole rounds: 3 rounds of the full workload (B 64, D 8) in segment mode (fused
   kernel from depth 3, the default there) and on the plane path: every decision record and the
   training predictions bit-identical.
+- Config 3 whole rounds: 3 rounds of the full 2.4M x 2376 panel (574 eras, 5 bins, B 8, D 6,
+  238 features per depth, DRO 0.5) on the plane path over the nibble bins and in segment mode
+  (the fused kernel over the uint8 bins from depth 2): two independent device paths, every
+  decision record and the training predictions bit-identical.
 - Config 5 (5,000,000 x 2376 uint8 bins, 250 packs x 8 distinct depth-6 trees): the full
   prediction, compared on a 50,000-row sample with the oracle's tree-order float32 sum
   (booster.py:709-712) within 1e-5, and leaf indices of every tree bit-exact on that sample
@@ -250,6 +254,57 @@ def test_config4_rounds_segments_match_planes(hip):
         assert a.tobytes() == b.tobytes(), f"round {r}: decision records differ"
     assert int(np.count_nonzero(pl_logs[0]["split"])) > 64  # the trees grow past depth 6
     np.testing.assert_array_equal(seg_preds, pl_preds)
+
+
+def test_config3_rounds_segments_match_planes(hip, monkeypatch):
+    """The headline workload's whole rounds through the plane path (nibble bins, joint-bin
+    histograms, the producer/consumer scorer) and through segment mode (the fused kernel from
+    depth 2): the decision logs and the training predictions are equal bit for bit."""
+    import torch
+
+    from packboost_amd import PackBoostConfig
+    from packboost_amd.engine import DeviceFit
+
+    N, F, E, nb = 2_400_000, 2376, 574, 5
+    ld = (N + 15) // 16 * 16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(33)
+    bins = torch.randint(0, nb, (F, ld), dtype=torch.uint8, device="cuda", generator=g)
+    bins[:, N:] = 0
+    sizes = np.array([len(a) for a in np.array_split(np.arange(N), E)], dtype=np.int64)
+    offs = np.zeros(E + 1, np.int64)
+    np.cumsum(sizes, out=offs[1:])
+    era_id = torch.from_numpy(np.repeat(np.arange(E), sizes)).cuda()
+    rng = np.random.default_rng(33)
+    sel = rng.permutation(F)[:50]
+    w = rng.standard_normal(50)
+    flip = torch.from_numpy(np.where(rng.random((E, 10)) < 0.5, -1.0, 1.0).astype(np.float32)).cuda()
+    lin = torch.zeros(N, device="cuda")
+    for j in range(50):
+        col = bins[int(sel[j]), :N].float() - 2.0
+        lin += float(w[j]) * col * (flip[era_id, j] if j < 10 else 1.0)
+    lin += 0.5 * float(lin.std()) * torch.randn(N, device="cuda", generator=g)
+    q = torch.quantile(lin[::12], torch.tensor([0.2, 0.4, 0.6, 0.8], device="cuda"))
+    y = (torch.bucketize(lin, q).float() / 4.0).contiguous()
+    cfg = PackBoostConfig(pack_size=8, max_depth=6, learning_rate=0.01, lambda_l2=1e-6, lambda_dro=0.5,
+                          min_samples_leaf=20, max_bins=nb, layer_feature_fraction=0.1, random_state=42,
+                          prebinned=True)
+    out = {}
+    for mode in ("planes", "segments"):
+        print(f"[config3 rounds] {mode}", flush=True)
+        monkeypatch.setenv("PB_SEG_FROM_DEPTH", "2")
+        fit = DeviceFit(bins, N, y, offs.astype(np.int32), cfg, fit_mode=mode)
+        try:
+            assert fit.segments == (mode == "segments") and fit.bins4 is not None
+            logs = [log.decisions.copy() for log, _, _ in fit.rounds(torch.Generator().manual_seed(5), 3)]
+            torch.cuda.synchronize()
+            out[mode] = (logs, fit.preds[:N].cpu().numpy().copy())
+        finally:
+            fit.close()
+    for r, (a, b) in enumerate(zip(out["segments"][0], out["planes"][0])):
+        assert a.tobytes() == b.tobytes(), f"round {r}: decision records differ"
+    assert int(np.count_nonzero(out["planes"][0][0]["split"])) >= 32  # deep trees
+    np.testing.assert_array_equal(out["segments"][1], out["planes"][1])
 
 
 def test_config5_predict(hip, oracle_mod):
