@@ -168,43 +168,93 @@ __global__ __launch_bounds__(kBlock) void seg_scan_kernel(SegState s, int32_t de
     block_scan_excl(s.cnt_r, nq);
 }
 
-// One thread per era: the first destination row of each (slot, side), the next depth's
-// segment starts, then the tail.
+// Exclusive prefix of one value per thread over the workgroup; *total gets the sum. Ends with
+// a barrier, so the next call may reuse the scratch.
+__device__ __forceinline__ int32_t wg_scan_excl(int32_t v, int32_t* total) {
+    __shared__ int32_t s_w[kBlock / kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int32_t incl = v;
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        const int32_t o = __shfl_up(incl, m);
+        if (lane >= m) incl += o;
+    }
+    if (lane == kWave - 1) s_w[wave] = incl;
+    __syncthreads();
+    int32_t before = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < kBlock / kWave; ++w) {
+        before += w < wave ? s_w[w] : 0;
+        sum += s_w[w];
+    }
+    *total = sum;
+    __syncthreads();
+    return before + incl - v;
+}
+
+// One workgroup per era: the first destination row of each (slot, side) and the next depth's
+// segment starts. The children that stay in the frontier come first, in (slot, side) order (the
+// order in which the decision step numbers the next slots), then the rows that leave it (a
+// non-split slot's rows count as its left side), then the era's old tail.
 __global__ __launch_bounds__(kBlock) void seg_bases_kernel(SegState s, const int32_t* __restrict__ seg,
                                                      int32_t* __restrict__ seg_next, int32_t depth) {
-    const int e = blockIdx.x * kBlock + threadIdx.x;
+    const int e = blockIdx.x;
     const int U = s.st->u_active[depth];
     const int Un = s.st->u_active[depth + 1];
-    if (e >= s.E) return;
     const int64_t xb = (int64_t)e * (U + 1);
+    const int n = 2 * U;  // (slot, side) items, item i = 2 slot + side
     auto tot = [&](int v, int side) -> int32_t {
         const int32_t* p = side ? s.cnt_r : s.cnt_l;
         return p[s.cp[xb + v + 1]] - p[s.cp[xb + v]];
     };
-    int32_t pos = s.era_off[e];
-    int slot = 0;
-    for (int v = 0; v < U; ++v) {
-        const SplitRule r = s.rules[v];
-        if (r.feature < 0) continue;
-        for (int side = 0; side < 2; ++side) {
-            if (r.next_slot[side] == PB_INACTIVE) continue;
-            s.base[(xb + v) * 2 + side] = pos;
-            seg_next[(int64_t)e * s.segw + slot] = pos;  // slots are assigned in this order
-            ++slot;
-            pos += tot(v, side);
+    const int32_t e0 = s.era_off[e];
+    // pass 1: the children that stay in the frontier
+    int32_t carry = 0, slots = 0;
+    for (int i0 = 0; i0 < n; i0 += kBlock) {
+        const int i = i0 + (int)threadIdx.x;
+        int32_t sz = 0, keep = 0;
+        int v = 0, side = 0;
+        if (i < n) {
+            v = i >> 1;
+            side = i & 1;
+            const SplitRule r = s.rules[v];
+            if (r.feature >= 0 && r.next_slot[side] != PB_INACTIVE) {
+                keep = 1;
+                sz = tot(v, side);
+            }
         }
-    }
-    seg_next[(int64_t)e * s.segw + Un] = pos;  // start of the tail
-    for (int v = 0; v < U; ++v) {
-        const SplitRule r = s.rules[v];
-        for (int side = 0; side < 2; ++side) {
-            if (r.feature >= 0 && r.next_slot[side] != PB_INACTIVE) continue;
-            if (r.feature < 0 && side == 1) continue;  // a leaf's rows all count as left
-            s.base[(xb + v) * 2 + side] = pos;
-            pos += tot(v, side);
+        int32_t ts, tk;
+        const int32_t off = wg_scan_excl(sz, &ts);
+        const int32_t rank = wg_scan_excl(keep, &tk);
+        if (keep) {
+            s.base[(xb + v) * 2 + side] = e0 + carry + off;
+            seg_next[(int64_t)e * s.segw + slots + rank] = e0 + carry + off;
         }
+        carry += ts;
+        slots += tk;
     }
-    s.base[(xb + U) * 2] = pos;  // the rows already in the tail keep their order
+    if (threadIdx.x == 0) seg_next[(int64_t)e * s.segw + Un] = e0 + carry;  // start of the tail
+    // pass 2: the rows that leave the frontier
+    for (int i0 = 0; i0 < n; i0 += kBlock) {
+        const int i = i0 + (int)threadIdx.x;
+        int32_t sz = 0, leave = 0;
+        int v = 0, side = 0;
+        if (i < n) {
+            v = i >> 1;
+            side = i & 1;
+            const SplitRule r = s.rules[v];
+            if (r.feature >= 0 ? r.next_slot[side] == PB_INACTIVE : side == 0) {
+                leave = 1;
+                sz = tot(v, side);
+            }
+        }
+        int32_t ts;
+        const int32_t off = wg_scan_excl(sz, &ts);
+        if (leave) s.base[(xb + v) * 2 + side] = e0 + carry + off;
+        carry += ts;
+    }
+    if (threadIdx.x == 0) s.base[(xb + U) * 2] = e0 + carry;  // the rows already in the tail keep their order
 }
 
 __global__ __launch_bounds__(kBlock) void seg_scatter_kernel(SegState s, const int32_t* __restrict__ seg,
@@ -294,7 +344,7 @@ hipError_t launch_seg_partition(const SegState& st, const int32_t* seg, int32_t*
     }
     hipLaunchKernelGGL(seg_count_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, bins, depth);
     hipLaunchKernelGGL(seg_scan_kernel, dim3(1), dim3(kBlock), 0, s, st, depth);
-    hipLaunchKernelGGL(seg_bases_kernel, dim3((st.E + kBlock - 1) / kBlock), dim3(kBlock), 0, s, st, seg, seg_next,
+    hipLaunchKernelGGL(seg_bases_kernel, dim3(st.E), dim3(kBlock), 0, s, st, seg, seg_next,
                        depth);
     hipLaunchKernelGGL(seg_scatter_kernel, dim3((unsigned)bound), dim3(kBlock), 0, s, st, seg, src, dst, bins, depth);
     return hipGetLastError();
