@@ -167,95 +167,95 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
     #pragma unroll
             for (int h = 0; h < RL / 4; ++h) gg[h] = *reinterpret_cast<const float4*>(a.grad + cl + 4 * h);
         }
-        for (; c < r1; c += kStride) {
-            // Unconditional loads keep the wait counts exact (a branch around them makes the
-            // compiler wait for everything): a lane's last pass re-reads offset 0 of each array,
-            // one hot line, and never uses the values.
-            const int cn = c + kStride;
-            const uint32_t on = (uint32_t)(cn < r1 ? cn : 0);
-            uint32_t wn[FT];
+        // One pass over a lane's RL rows from row cc: bins wv, node ids nv and grads gv.
+        const uint32_t seg_len = (uint32_t)(r1 - r0);
+        auto pass = [&](const uint32_t (&wv)[FT], const uint4& nv, const float4 (&gv)[RL / 4], int cc) {
     #pragma unroll
-            for (int kk = 0; kk < FT; ++kk)
-                wn[kk] = __builtin_nontemporal_load(
-                    reinterpret_cast<const uint32_t*>(col[kk] + (on >> kByteShift)));
-            uint4 nnn;
-            if (NIB) {
-                nnn = *reinterpret_cast<const uint4*>(a.nid + on);
-            } else {
-                const uint2 n2 = *reinterpret_cast<const uint2*>(a.nid + on);
-                nnn = make_uint4(n2.x, n2.y, 0u, 0u);
-            }
-            float4 ggn[RL / 4];
-    #pragma unroll
-            for (int h = 0; h < RL / 4; ++h) ggn[h] = *reinterpret_cast<const float4*>(a.grad + on + 4 * h);
-            // only a lane of the first or last pass holds rows outside the segment
-            const bool full = (c >= r0) && (c + RL <= r1);
-    #pragma unroll
-          for (int h = 0; h < RL / 4; ++h) {  // quads of rows c + 4h .. c + 4h + 3
-            const uint32_t nq0 = h ? nn.z : nn.x;
-            const uint32_t nq1 = h ? nn.w : nn.y;
-            const uint32_t n4[4] = {nq0 & 0xffffu, nq0 >> 16, nq1 & 0xffffu, nq1 >> 16};
-            const float g4[4] = {gg[h].x, gg[h].y, gg[h].z, gg[h].w};
-            bool ok[4];  // row c+4h+j is counted: in the segment and in one of the item's nodes
-    #pragma unroll
-            for (int j = 0; j < 4; ++j) ok[j] = n4[j] - (uint32_t)u0 < (uint32_t)Un;
-            if (!full) {
+            for (int h = 0; h < RL / 4; ++h) {  // quads of rows cc + 4h .. cc + 4h + 3
+                const uint32_t nq0 = h ? nv.z : nv.x;
+                const uint32_t nq1 = h ? nv.w : nv.y;
+                const uint32_t n4[4] = {nq0 & 0xffffu, nq0 >> 16, nq1 & 0xffffu, nq1 >> 16};
+                const float g4[4] = {gv[h].x, gv[h].y, gv[h].z, gv[h].w};
+                const uint32_t rq = (uint32_t)(cc + 4 * h - r0);  // first row of the quad, from r0
+                uint32_t base[4];  // byte offset of (node, cell 0, this lane's copy) in a group's block
+                unsigned long long qv[4];
+                uint32_t keep = 0u;  // uint8 bins: 0xff in byte j iff row cc+4h+j is counted
     #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int r = c + 4 * h + j;
-                    ok[j] = ok[j] && r >= r0 && r < r1;
+                    // row cc+4h+j is counted: in the segment and in one of the item's nodes (each
+                    // test one unsigned compare; the flag stays a lane mask, no branch per row)
+                    const uint32_t nj = n4[j] - (uint32_t)u0;  // node within the tile
+                    const bool ok = (nj < (uint32_t)Un) & (rq + (uint32_t)j < seg_len);
+                    base[j] = __umul24(ok ? nj : 0u, cells_c8) + copy8;  // nj < 2^16, cells_c8 < 2^24
+                    // (q << 16) + 1 with q = round(g * 2^sh) (grad_addend), computed for every row
+                    // and masked to 0 if not counted
+                    qv[j] = grad_addend(g4[j], scale) & (0ull - (unsigned long long)ok);
+                    if (!NIB) keep |= ok ? (0xffu << (8 * j)) : 0u;
                 }
-            }
-            uint32_t base[4];  // byte offset of (node, cell 0, this lane's copy) in a group's block
-            unsigned long long qv[4];
-            uint32_t keep = 0u;  // uint8 bins: 0xff in byte j iff row c+4h+j is counted
+                // some row of the quad is counted (a counted row's addend has its low bit set)
+                const bool any = ((uint32_t)(qv[0] | qv[1] | qv[2] | qv[3]) & 1u) != 0u;
+                // this quad's byte-per-row bin dwords. uint8 columns: bytes of uncounted rows are
+                // masked to bin 0 (the caller's padding rows may hold anything). Nibble columns:
+                // every row holds a valid bin (rows past N are zero, pb_pack_bins4), and uncounted
+                // rows add zero, so no mask is needed.
+                const uint32_t kmask = NIB ? 0xffffffffu : keep;
+                auto wq = [&](int kk) -> uint32_t {
+                    return NIB ? ((wv[kk] >> (4 * h)) & 0x0f0f0f0fu) : (wv[kk] & kmask);
+                };
+                if (any) {  // lanes without a counted row skip the atomics
     #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t nj = ok[j] ? n4[j] - (uint32_t)u0 : 0u;  // node within the tile
-                base[j] = __umul24(nj, cells_c8) + copy8;  // nj < 2^16, cells_c8 < 2^24
-                // (q << 16) + 1 with q = round(g * 2^sh) (grad_addend); 0 if not counted
-                qv[j] = ok[j] ? grad_addend(g4[j], scale) : 0ull;
-                if (!NIB) keep |= ok[j] ? (0xffu << (8 * j)) : 0u;
-            }
-            const bool any = ok[0] || ok[1] || ok[2] || ok[3];  // some row of the quad is counted
-            // this quad's byte-per-row bin dwords. uint8 columns: bytes of uncounted rows are
-            // masked to bin 0 (the caller's padding rows may hold anything). Nibble columns: every
-            // row holds a valid bin (rows past N are zero, pb_pack_bins4), and uncounted rows add
-            // zero, so no mask is needed.
-            const uint32_t kmask = NIB ? 0xffffffffu : keep;
-            auto wq = [&](int kk) -> uint32_t {
-                return NIB ? ((w[kk] >> (4 * h)) & 0x0f0f0f0fu) : (w[kk] & kmask);
-            };
-            if (any) {  // lanes without a counted row skip the atomics
+                    for (int gi = 0; gi < G; ++gi) {
+                        const int kk = gi * P;
+                        char* hk = lds_bytes + (uint32_t)(gi * words_group) * 8u;
+                        // Joint index per byte, below 256 so no byte carries into the next row's:
+                        // (b1 * nb + b2) * nb + b3 <= nb^3 - 1 <= 215 for nb <= 6, b1 * nb + b2 <=
+                        // 255 for nb <= 16. A group's partners past the tile's last feature read
+                        // that feature's column (valid bins); the flush sums the partners out of
+                        // the marginals of the real features.
+                        uint32_t wk;
+                        if (P == 3)
+                            wk = mad_bytes(mad_bytes(wq(kk), (uint32_t)nb, wq(kk + 1)), (uint32_t)nb, wq(kk + 2));
+                        else if (P == 2)
+                            wk = mad_bytes(wq(kk), (uint32_t)nb, wq(kk + 1));
+                        else
+                            wk = wq(kk);
     #pragma unroll
-                for (int gi = 0; gi < G; ++gi) {
-                    const int kk = gi * P;
-                    char* hk = lds_bytes + (uint32_t)(gi * words_group) * 8u;
-                    // Joint index per byte, below 256 so no byte carries into the next row's:
-                    // (b1 * nb + b2) * nb + b3 <= nb^3 - 1 <= 215 for nb <= 6, b1 * nb + b2 <= 255
-                    // for nb <= 16. A group's partners past the tile's last feature read that
-                    // feature's column (valid bins); the flush sums the partners out of the
-                    // marginals of the real features.
-                    uint32_t wk;
-                    if (P == 3)
-                        wk = mad_bytes(mad_bytes(wq(kk), (uint32_t)nb, wq(kk + 1)), (uint32_t)nb, wq(kk + 2));
-                    else if (P == 2)
-                        wk = mad_bytes(wq(kk), (uint32_t)nb, wq(kk + 1));
-                    else
-                        wk = wq(kk);
-    #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t boff = ((wk >> (8 * j)) & 0xffu) << bin_shift;
-                        atomicAdd(reinterpret_cast<unsigned long long*>(hk + base[j] + boff), qv[j]);
+                        for (int j = 0; j < 4; ++j) {
+                            const uint32_t boff = ((wk >> (8 * j)) & 0xffu) << bin_shift;
+                            atomicAdd(reinterpret_cast<unsigned long long*>(hk + base[j] + boff), qv[j]);
+                        }
                     }
                 }
+            }  // quads
+        };
+        // The pass's loads for row cn. Unconditional loads keep the wait counts exact (a branch
+        // around them makes the compiler wait for everything): a lane past the segment re-reads
+        // offset 0 of each array, one hot line, and never uses the values.
+        auto load = [&](uint32_t (&wv)[FT], uint4& nv, float4 (&gv)[RL / 4], int cn) {
+            const uint32_t on = (uint32_t)(cn < r1 ? cn : 0);
+    #pragma unroll
+            for (int kk = 0; kk < FT; ++kk)
+                wv[kk] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(col[kk] + (on >> kByteShift)));
+            if (NIB) {
+                nv = *reinterpret_cast<const uint4*>(a.nid + on);
+            } else {
+                const uint2 n2 = *reinterpret_cast<const uint2*>(a.nid + on);
+                nv = make_uint4(n2.x, n2.y, 0u, 0u);
             }
-          }  // quads
     #pragma unroll
-            for (int kk = 0; kk < FT; ++kk) w[kk] = wn[kk];
-            nn = nnn;
-    #pragma unroll
-            for (int h = 0; h < RL / 4; ++h) gg[h] = ggn[h];
+            for (int h = 0; h < RL / 4; ++h) gv[h] = *reinterpret_cast<const float4*>(a.grad + on + 4 * h);
+        };
+        // Software pipeline, unrolled by two so the two register sets alternate without copies:
+        // the next pass's loads are in flight while this pass does its atomics.
+        uint32_t w2[FT];
+        uint4 nn2;
+        float4 gg2[RL / 4];
+        for (; c < r1; c += 2 * kStride) {
+            load(w2, nn2, gg2, c + kStride);
+            pass(w, nn, gg, c);
+            if (c + kStride >= r1) break;
+            load(w, nn, gg, c + 2 * kStride);
+            pass(w2, nn2, gg2, c + kStride);
         }
         __syncthreads();
 
@@ -372,6 +372,20 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             __syncthreads();
         }
         const int items = Un * nf * nb;
+        // Sums over one partner's nb bins are read as one batch of W loads (clamped to the last
+        // bin, the extra values dropped), so their LDS round trips overlap: the LDS is busy with
+        // the other workgroups' atomics, and a dependent read per cell made the flush a chain of
+        // nb^(P-1) round trips.
+        auto rsum = [&](const unsigned long long* base, int step, auto width) -> unsigned long long {
+            constexpr int W = decltype(width)::value;
+            unsigned long long v[W];
+    #pragma unroll
+            for (int o = 0; o < W; ++o) v[o] = base[min(o, nb - 1) * step];
+            unsigned long long r = 0ull;
+    #pragma unroll
+            for (int o = 0; o < W; ++o) r += (o < nb) ? v[o] : 0ull;
+            return r;
+        };
         // marginal of element (u, kk, bb) alone, or (prefix) its bins 0..bb; P == 1: the prefix,
         // already in place
         auto marginal = [&](const Digits& d, bool prefix) -> unsigned long long {
@@ -382,20 +396,6 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             const int bb = d.bb;
             const int b_lo = prefix ? 0 : bb;
             unsigned long long tot = 0ull;
-            // Sums over one partner's nb bins are read as one batch of W loads (clamped to the
-            // last bin, the extra values dropped), so their LDS round trips overlap: the LDS is
-            // busy with the other workgroups' atomics, and a dependent read per cell made the
-            // flush a chain of nb^(P-1) round trips.
-            auto run = [&](const unsigned long long* base, int step, auto width) -> unsigned long long {
-                constexpr int W = decltype(width)::value;
-                unsigned long long v[W];
-    #pragma unroll
-                for (int o = 0; o < W; ++o) v[o] = base[min(o, nb - 1) * step];
-                unsigned long long r = 0ull;
-    #pragma unroll
-                for (int o = 0; o < W; ++o) r += (o < nb) ? v[o] : 0ull;
-                return r;
-            };
             if (P == 3) {
                 const int nb2 = nb * nb;
                 const int stride = side == 0 ? nb2 : (side == 1 ? nb : 1);
@@ -404,18 +404,18 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 for (int b = b_lo; b <= bb; ++b)
                     for (int o1 = 0; o1 < nb; ++o1) {
                         const unsigned long long* base = hc + (b * stride + o1 * s1) * C;
-                        tot += (nb <= 4) ? run(base, s2 * C, std::integral_constant<int, 4>{})
-                                         : (nb == 5) ? run(base, s2 * C, std::integral_constant<int, 5>{})
-                                                     : run(base, s2 * C, std::integral_constant<int, 6>{});
+                        tot += (nb <= 4) ? rsum(base, s2 * C, std::integral_constant<int, 4>{})
+                                         : (nb == 5) ? rsum(base, s2 * C, std::integral_constant<int, 5>{})
+                                                     : rsum(base, s2 * C, std::integral_constant<int, 6>{});
                     }
             } else if (P == 2) {
                 const int step = (side == 0 ? 1 : nb) * C;  // the partner's bins
                 for (int b = b_lo; b <= bb; ++b) {
                     const unsigned long long* base = hc + (side == 0 ? b * nb : b) * C;
-                    tot += (nb <= 4)   ? run(base, step, std::integral_constant<int, 4>{})
-                           : (nb == 5) ? run(base, step, std::integral_constant<int, 5>{})
-                           : (nb <= 8) ? run(base, step, std::integral_constant<int, 8>{})
-                                       : run(base, step, std::integral_constant<int, 16>{});
+                    tot += (nb <= 4)   ? rsum(base, step, std::integral_constant<int, 4>{})
+                           : (nb == 5) ? rsum(base, step, std::integral_constant<int, 5>{})
+                           : (nb <= 8) ? rsum(base, step, std::integral_constant<int, 8>{})
+                                       : rsum(base, step, std::integral_constant<int, 16>{});
                 }
             } else {
                 tot = hc[bb * C];
@@ -460,7 +460,32 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             }
         };
         constexpr int kMaxItems = 8;  // marginals a thread holds in registers
-        if (P == 1) {
+        if (P == 2 && nb <= 8) {
+            // One thread per (node, feature) of a pair: it reads the pair's nb x nb joint cells
+            // once, sums its feature's marginals (side 0 over rows of the cell block, side 1 over
+            // columns), and emits the running sums. Every cell is read twice (once per side)
+            // instead of once per marginal element and again for its prefix.
+            const int ng2 = ng * 2;
+            const DivU16 div_ng2(ng2);
+            for (int t = (int)threadIdx.x; t < Un * ng2; t += BS) {
+                const int u = (int)div_ng2.div((uint32_t)t);
+                const int kk = t - u * ng2;  // feature of the tile: group kk / 2, side kk % 2
+                if (kk >= nf) continue;       // the partner past the tile's last feature
+                const int side = kk & 1;
+                const unsigned long long* hc =
+                    lds + ((int64_t)(kk >> 1) * words_group + (int64_t)u * cells_node * C);
+                const int s_out = (side ? 1 : nb) * C;  // from one marginal bin to the next
+                const int s_in = (side ? nb : 1) * C;   // over the partner's bins
+                unsigned long long run = 0ull;
+                for (int bb = 0; bb < nb; ++bb) {
+                    const unsigned long long* base = hc + bb * s_out;
+                    run += (nb <= 4)   ? rsum(base, s_in, std::integral_constant<int, 4>{})
+                           : (nb == 5) ? rsum(base, s_in, std::integral_constant<int, 5>{})
+                                       : rsum(base, s_in, std::integral_constant<int, 8>{});
+                    emit(Digits{u, kk, bb}, run);
+                }
+            }
+        } else if (P == 1) {
             // kEmitBatch elements per thread at a time: their LDS reads first, then the stores
             constexpr int kEmitBatch = 4;
             for (int it0 = threadIdx.x; it0 < items; it0 += kEmitBatch * BS) {
