@@ -372,6 +372,11 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             __syncthreads();
         }
         const int items = Un * nf * nb;
+        // The thread's element indices below depend only on the thread and nb, so the compiler
+        // would hoist their digit divisions out of the item loop and hold them in registers across
+        // the row passes; an opaque copy of the thread index keeps them here.
+        int tx = (int)threadIdx.x;
+        __asm__ volatile("" : "+v"(tx));
         // Sums over one partner's nb bins are read as one batch of W loads (clamped to the last
         // bin, the extra values dropped), so their LDS round trips overlap: the LDS is busy with
         // the other workgroups' atomics, and a dependent read per cell made the flush a chain of
@@ -429,7 +434,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             // part of a split era: add this segment's per-bin cells, exact integers, into the
             // era's sums (integer adds: the order of the segments does not matter)
             const int64_t srow0 = ((int64_t)slot * a.acc_U + u0) * a.acc_K + k0;
-            for (int it = threadIdx.x; it < items; it += BS) {
+            for (int it = tx; it < items; it += BS) {
                 const Digits d = split(it);
                 const unsigned long long m = marginal(d, false);
                 const uint32_t cnt = (uint32_t)(m & ((1ull << kCountBits) - 1ull));
@@ -467,7 +472,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             // instead of once per marginal element and again for its prefix.
             const int ng2 = ng * 2;
             const DivU16 div_ng2(ng2);
-            for (int t = (int)threadIdx.x; t < Un * ng2; t += BS) {
+            for (int t = tx; t < Un * ng2; t += BS) {
                 const int u = (int)div_ng2.div((uint32_t)t);
                 const int kk = t - u * ng2;  // feature of the tile: group kk / 2, side kk % 2
                 if (kk >= nf) continue;       // the partner past the tile's last feature
@@ -488,7 +493,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         } else if (P == 1) {
             // kEmitBatch elements per thread at a time: their LDS reads first, then the stores
             constexpr int kEmitBatch = 4;
-            for (int it0 = threadIdx.x; it0 < items; it0 += kEmitBatch * BS) {
+            for (int it0 = tx; it0 < items; it0 += kEmitBatch * BS) {
                 Digits dd[kEmitBatch];
                 unsigned long long v[kEmitBatch];
     #pragma unroll
@@ -506,13 +511,13 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             unsigned long long m[kMaxItems];
     #pragma unroll
             for (int i = 0; i < kMaxItems; ++i) {
-                const int it = (int)threadIdx.x + i * BS;
+                const int it = tx + i * BS;
                 m[i] = (it < items) ? marginal(split(it), false) : 0ull;
             }
             __syncthreads();
     #pragma unroll
             for (int i = 0; i < kMaxItems; ++i) {
-                const int it = (int)threadIdx.x + i * BS;
+                const int it = tx + i * BS;
                 if (it < items) lds[it] = m[i];
             }
             __syncthreads();
@@ -527,7 +532,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 for (int o = 0; o < W; ++o) r += (o <= bb) ? v[o] : 0ull;
                 return r;
             };
-            for (int it = threadIdx.x; it < items; it += BS) {
+            for (int it = tx; it < items; it += BS) {
                 const Digits d = split(it);
                 const unsigned long long tot =
                     (nb <= 4)   ? prefix(it, d.bb, std::integral_constant<int, 4>{})
@@ -537,7 +542,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 emit(d, tot);
             }
         } else {
-            for (int it = threadIdx.x; it < items; it += BS) {
+            for (int it = tx; it < items; it += BS) {
                 const Digits d = split(it);
                 emit(d, marginal(d, true));
             }

@@ -62,16 +62,19 @@ __device__ __forceinline__ unsigned long long wave_scan_incl_u64(unsigned long l
 }
 
 // One row's 64-bit histogram addend (q << 16) + 1 with q = round(g * scale) (|q| < 2^45): the
-// count 1 in the low 16 bits, the fixed-point grad above it, built from two 32-bit halves. In
-// float, exactly: xq = q, xh = floor(q / 2^16) (the high word), xl = q - xh * 2^16 in [0, 2^16)
-// (the grad's bits in the low word).
+// count 1 in the low 16 bits, the fixed-point grad above it. g * scale is exact in float (scale
+// is a power of two); adding 1.5 * 2^52 to it in double rounds it to an integer with ties to
+// even (as rintf does) and leaves that integer in the low mantissa bits, so the double's bit
+// pattern minus that of 1.5 * 2^52 (low word 0) is q in two's complement for |q| < 2^51. Six
+// instructions where float floor/split conversions took nine; double adds issue at the full
+// rate on gfx950.
 __device__ __forceinline__ unsigned long long grad_addend(float g, float scale) {
-    const float xq = rintf(g * scale);
-    const float xh = floorf(xq * (1.0f / 65536.0f));
-    const float xl = xq - xh * 65536.0f;
-    const uint32_t lo = ((uint32_t)xl << kCountBits) | 1u;
-    const uint32_t hi = (uint32_t)(int32_t)xh;
-    return ((unsigned long long)hi << 32) | lo;
+    const double y = (double)(g * scale) + 6755399441055744.0;
+    const unsigned long long b = (unsigned long long)__double_as_longlong(y);
+    const uint32_t lo = (uint32_t)b;                       // q's low word
+    const uint32_t hi = (uint32_t)(b >> 32) - 0x43380000u;  // q's high word
+    const uint32_t ahi = __builtin_amdgcn_alignbit(hi, lo, 32 - kCountBits);  // (q << 16) >> 32
+    return ((unsigned long long)ahi << 32) | ((lo << kCountBits) | 1u);
 }
 
 // Per active node of the current depth, read by the partition kernel.
