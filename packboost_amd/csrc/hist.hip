@@ -464,6 +464,29 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 a.out_tot_g[o] = gs;
             }
         };
+        // 5 bins (config of the 2.4M x 2376 panel): a (node, feature)'s 4 prefixes go out as one
+        // 8-byte count store and one 16-byte grad store (the run of 4 is aligned: its element
+        // index is a multiple of 4), instead of 8 scalar stores
+        const bool vec5 = nb == 5 && !a.out_cnt32 && !(reinterpret_cast<uintptr_t>(a.out_cnt) & 7) &&
+                          !(reinterpret_cast<uintptr_t>(a.out_g) & 15);
+        auto emit5 = [&](int u, int kk, const unsigned long long (&m)[5]) {
+            unsigned long long run = 0ull;
+            ushort4 cv;
+            float4 gv;
+            uint16_t* cp = reinterpret_cast<uint16_t*>(&cv);
+            float* gp = reinterpret_cast<float*>(&gv);
+    #pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                run += m[bb];
+                const uint32_t cnt = (uint32_t)(run & ((1ull << kCountBits) - 1ull));
+                cp[bb] = (uint16_t)cnt;
+                gp[bb] = (float)((double)(((long long)(run - cnt)) >> kCountBits) * inv_scale);
+            }
+            const int64_t o = (row0 + (int64_t)u * a.K + kk) * 4;
+            *reinterpret_cast<ushort4*>(a.out_cnt + o) = cv;
+            *reinterpret_cast<float4*>(a.out_g + o) = gv;
+            if (k0 + kk == 0) emit(Digits{u, kk, 4}, run + m[4]);
+        };
         constexpr int kMaxItems = 8;  // marginals a thread holds in registers
         if (P == 2 && nb <= 8) {
             // One thread per (node, feature) of a pair: it reads the pair's nb x nb joint cells
@@ -481,6 +504,14 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                     lds + ((int64_t)(kk >> 1) * words_group + (int64_t)u * cells_node * C);
                 const int s_out = (side ? 1 : nb) * C;  // from one marginal bin to the next
                 const int s_in = (side ? nb : 1) * C;   // over the partner's bins
+                if (vec5) {  // all 25 cells read as one batch
+                    unsigned long long m[5];
+    #pragma unroll
+                    for (int bb = 0; bb < 5; ++bb)
+                        m[bb] = rsum(hc + bb * s_out, s_in, std::integral_constant<int, 5>{});
+                    emit5(u, kk, m);
+                    continue;
+                }
                 unsigned long long run = 0ull;
                 for (int bb = 0; bb < nb; ++bb) {
                     const unsigned long long* base = hc + bb * s_out;
@@ -532,6 +563,16 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 for (int o = 0; o < W; ++o) r += (o <= bb) ? v[o] : 0ull;
                 return r;
             };
+            if (vec5) {
+                // one thread per (node, feature): its 5 compacted marginals, then emit5
+                for (int t = tx; t < Un * nf; t += BS) {
+                    const int u = (int)div_nf.div((uint32_t)t);
+                    unsigned long long m[5];
+    #pragma unroll
+                    for (int bb = 0; bb < 5; ++bb) m[bb] = lds[t * 5 + bb];
+                    emit5(u, t - u * nf, m);
+                }
+            } else
             for (int it = tx; it < items; it += BS) {
                 const Digits d = split(it);
                 const unsigned long long tot =
