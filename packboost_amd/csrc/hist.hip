@@ -10,9 +10,9 @@
 // Design (gfx950):
 //  * One workgroup owns one (era, feature tile). Rows are era-major, so an era is a
 //    contiguous byte range of every feature column: loads are coalesced dwords (4 rows per
-//    lane, 1024 rows per workgroup pass) and no global atomics are needed.
-//  * Each lane keeps the row state of its 4 rows (LDS byte offset of the row's node and the
-//    packed value below) in registers and reuses it across all features of the tile.
+//    lane in uint8 columns, 8 in nibble columns) and no global atomics are needed.
+//  * Each lane forms the row state of its rows (LDS byte offset of the row's node and the
+//    packed value below) once per pass and reuses it across all features of the tile.
 //  * One 64-bit LDS atomic carries (fixed-point grad << 16) + 1, so the count (low 16 bits)
 //    and the grad sum (high 48 bits) accumulate in a single ds_add_u64. Integer addition is
 //    order-independent, so the result is deterministic run to run; grad is quantised as
