@@ -616,43 +616,48 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
         slot_off[i] = (int32_t)((int64_t)my_el * estride + node_off + (int64_t)k * pt + thr);
     }
 
-    // next chunk's inputs: this thread's era totals, and per pair the prefix count and grad
-    int pct = 0;
-    float pGt = 0.0f;
-    int pL[kPcPairs];
-    float pGL[kPcPairs];
-    auto prefetch = [&](int chunk) {
+    // inputs of the next two chunks, in two register sets (chunk c in set c % 2, the set index
+    // always a compile-time constant): this thread's era totals, and per pair the prefix count
+    // and grad. Loading two chunks ahead covers the plane loads' latency when three workgroups
+    // per CU stream a deep frontier's planes.
+    int pct[2] = {0, 0};
+    float pGt[2] = {0.0f, 0.0f};
+    int pL[2][kPcPairs];
+    float pGL[2][kPcPairs];
+    auto prefetch = [&](int chunk, auto set) {
+        constexpr int S = decltype(set)::value;
         const int e0 = chunk * kPcEras;
         const int ne = min(kPcEras, a.E - e0);
         const int64_t eoff = (int64_t)e0 * estride;
         const bool live = chunk < nchunks;
-        pct = 0;
-        pGt = 0.0f;
+        pct[S] = 0;
+        pGt[S] = 0.0f;
         if (live && slot_el[0] < ne) {  // slot 0 is valid whenever any slot of the thread is
             const int64_t to = (int64_t)(e0 + my_el) * a.U + u;  // era total
-            pct = a.tot_cnt[to];
-            pGt = a.tot_g[to];
+            pct[S] = a.tot_cnt[to];
+            pGt[S] = a.tot_g[to];
         }
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
             if (i >= np) break;
-            pL[i] = 0;
-            pGL[i] = 0.0f;
+            pL[S][i] = 0;
+            pGL[S][i] = 0.0f;
             if (live && slot_el[i] < ne) {
                 const int64_t off = eoff + slot_off[i];
-                pL[i] = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
-                pGL[i] = a.g[off];
+                pL[S][i] = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
+                pGL[S][i] = a.g[off];
             }
         }
     };
     // Branch-free per pair (the same float operations as the reference, evaluated for every
     // pair and selected), so the divide sequences of all pairs interleave. The parent term
     // depends on the era only and is computed once per thread, with the same operations.
-    auto produce = [&](int chunk) {
+    auto produce = [&](int chunk, auto set) {
+        constexpr int S = decltype(set)::value;
         float4* buf = ring + (chunk & 1) * kPcEras * kWave;
-        const int ctot = pct;
+        const int ctot = pct[S];
         const bool has = ctot != 0;
-        const float Gt = pGt;
+        const float Gt = pGt[S];
         const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
         const float pden = (float)ctot + lam;
         const float pq = (0.5f * (Gt * Gt)) / pden;
@@ -660,8 +665,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
             if (i >= np) break;
-            const int Lc = pL[i];
-            const float GLc = pGL[i];
+            const int Lc = pL[S][i];
+            const float GLc = pGL[S][i];
             const int R = ctot - Lc;
             const float GR = Gt - GLc;
             const float w = (has && Lc > 0 && R > 0) ? wera : 0.0f;
@@ -773,14 +778,22 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
             }
         }
     };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
     if (!consumer) {
-        prefetch(0);
-        produce(0);
-        prefetch(1);
+        prefetch(0, S0{});
+        prefetch(1, S1{});
+        produce(0, S0{});
+        prefetch(2, S0{});
     }
     __syncthreads();
-    for (int ch = 0; ch < nchunks; ++ch) {
-        if (consumer) {
+    // Chunk ch: the consumer runs it while the producers make chunk ch + 1 (register set
+    // (ch + 1) % 2) and then load chunk ch + 3 into the set they just used. The two roles run
+    // separate loops (whole wavefronts, so each role's registers are its own) that pass the same
+    // number of barriers: one per chunk. The role is read from the first lane, so the branch is
+    // a scalar one: a wavefront runs only its own loop and its own barriers.
+    if (__builtin_amdgcn_readfirstlane(consumer ? 1 : 0) != 0) {
+        for (int ch = 0; ch < nchunks; ++ch) {
             if (owner || tid == kWave - 1) {
                 if (table) {
                     if (use_dir)
@@ -794,11 +807,23 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
                         consume(ch, std::false_type{}, std::false_type{});
                 }
             }
-        } else if (ch + 1 < nchunks) {
-            produce(ch + 1);
-            prefetch(ch + 2);
+            __syncthreads();
         }
-        __syncthreads();
+    } else {
+        for (int ch = 0; ch < nchunks; ch += 2) {
+            if (ch + 1 < nchunks) {
+                produce(ch + 1, S1{});
+                prefetch(ch + 3, S1{});
+            }
+            __syncthreads();
+            if (ch + 1 < nchunks) {
+                if (ch + 2 < nchunks) {
+                    produce(ch + 2, S0{});
+                    prefetch(ch + 4, S0{});
+                }
+                __syncthreads();
+            }
+        }
     }
     if (consumer) {
         if (table) wsum = (float)nact;  // exact: a sum of ones below 2^24
