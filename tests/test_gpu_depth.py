@@ -206,6 +206,31 @@ def test_hist_copies(hip, oracle_mod, monkeypatch, pairs, copies, block):
         g.close()
 
 
+@pytest.mark.parametrize("layout", ["u8", "nibble"])
+@pytest.mark.parametrize("pairs,nb", [(2, 2), (2, 3), (2, 4), (2, 5), (2, 6), (2, 7), (2, 8), (2, 9),
+                                      (3, 2), (3, 3), (3, 4), (3, 6)])
+def test_hist_joint_flush_bins(hip, oracle_mod, monkeypatch, pairs, nb, layout):
+    """The joint-bin flush at every small bin count: pairs (one thread per (node, feature) over
+    the pair's nb x nb cells for nb <= 8, the element-wise path above) and triples (marginal
+    elements compacted, then prefixes per (node, feature)), with an odd feature count so the last
+    group's partners run past the tile. Counts bit-exact, grads within the per-cell mass bar."""
+    monkeypatch.setenv("PB_HIST_PAIRS", str(pairs))
+    print(f"[hist joint flush] P={pairs} nb={nb} {layout}", flush=True)
+    p = make_problem(60 + 10 * pairs + nb, 7000, 15, 6, nb, 3, empty_era=True)
+    feats = np.random.default_rng(nb).permutation(15)[:11].astype(np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, want_planes=True)
+    g = GpuDepth(hip, p, 11, msl=3, layout=layout)
+    try:
+        g.hist(feats)
+        cnt, gp = g.planes()
+        np.testing.assert_array_equal(cnt, ref.planes[0])
+        mass = _abs_mass(p, 3)[:, :, None, None]
+        err = np.abs(gp.astype(np.float64) - ref.planes[1].astype(np.float64))
+        assert np.all(err <= 1e-5 * np.maximum(mass, 1.0))
+    finally:
+        g.close()
+
+
 WIDE_CASES = [c for c in CASES if c[4] - 1 >= 64]
 
 
