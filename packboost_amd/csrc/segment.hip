@@ -43,28 +43,43 @@ __device__ __forceinline__ int chunk_entry(const int32_t* cp, int n, int q) {
     return lo;
 }
 
+// Exclusive prefix of one value per thread over the workgroup; *total gets the sum. Ends with
+// a barrier, so the next call may reuse the scratch.
+__device__ __forceinline__ int32_t wg_scan_excl(int32_t v, int32_t* total) {
+    __shared__ int32_t s_w[kBlock / kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    int32_t incl = v;
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) {
+        const int32_t o = __shfl_up(incl, m);
+        if (lane >= m) incl += o;
+    }
+    if (lane == kWave - 1) s_w[wave] = incl;
+    __syncthreads();
+    int32_t before = 0, sum = 0;
+#pragma unroll
+    for (int w = 0; w < kBlock / kWave; ++w) {
+        before += w < wave ? s_w[w] : 0;
+        sum += s_w[w];
+    }
+    *total = sum;
+    __syncthreads();
+    return before + incl - v;
+}
+
 // Exclusive scan of n int32 values in place by one workgroup: vals[i] <- sum of vals[0 .. i-1],
-// vals[n] <- the total.
+// vals[n] <- the total. Each thread sums a contiguous strip, the strip sums are scanned across
+// the workgroup by wavefront shuffles, and each thread rewrites its strip from its offset.
 __device__ void block_scan_excl(int32_t* vals, int n) {
-    __shared__ int32_t s_part[kBlock];
     const int tid = threadIdx.x;
     const int per = (n + kBlock - 1) / kBlock;
     const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
     int32_t sum = 0;
     for (int i = i0; i < i1; ++i) sum += vals[i];
-    s_part[tid] = sum;
-    __syncthreads();
-    if (tid == 0) {
-        int32_t run = 0;
-        for (int i = 0; i < kBlock; ++i) {
-            const int32_t v = s_part[i];
-            s_part[i] = run;
-            run += v;
-        }
-        vals[n] = run;
-    }
-    __syncthreads();
-    int32_t run = s_part[tid];
+    int32_t total;
+    int32_t run = wg_scan_excl(sum, &total);
+    if (tid == 0) vals[n] = total;
     for (int i = i0; i < i1; ++i) {
         const int32_t v = vals[i];
         vals[i] = run;
@@ -166,31 +181,6 @@ __global__ __launch_bounds__(kBlock) void seg_scan_kernel(SegState s, int32_t de
     block_scan_excl(s.cnt_l, nq);
     __syncthreads();
     block_scan_excl(s.cnt_r, nq);
-}
-
-// Exclusive prefix of one value per thread over the workgroup; *total gets the sum. Ends with
-// a barrier, so the next call may reuse the scratch.
-__device__ __forceinline__ int32_t wg_scan_excl(int32_t v, int32_t* total) {
-    __shared__ int32_t s_w[kBlock / kWave];
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    int32_t incl = v;
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) {
-        const int32_t o = __shfl_up(incl, m);
-        if (lane >= m) incl += o;
-    }
-    if (lane == kWave - 1) s_w[wave] = incl;
-    __syncthreads();
-    int32_t before = 0, sum = 0;
-#pragma unroll
-    for (int w = 0; w < kBlock / kWave; ++w) {
-        before += w < wave ? s_w[w] : 0;
-        sum += s_w[w];
-    }
-    *total = sum;
-    __syncthreads();
-    return before + incl - v;
 }
 
 // One workgroup per era: the first destination row of each (slot, side) and the next depth's
