@@ -27,15 +27,26 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
     const int Ua = st->u_active[depth];
     if (Ua <= 0) return;
     const bool in_lds = Ua <= kMaxRulesLds;
+    // 8 rows per thread (rows_padded is a multiple of 16): one 16-byte load of their node ids and
+    // one of their tree nodes, then their bin gathers all in flight before any result is needed.
+    // The first group's node ids and tree nodes are loaded before the rules are staged in LDS, so
+    // the two loads overlap.
+    const int64_t stride = (int64_t)gridDim.x * kBlock * 8;
+    int64_t r = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8;
+    uint4 nn = make_uint4(0u, 0u, 0u, 0u), tt = nn;
+    if (r < rows_padded) {
+        nn = *reinterpret_cast<const uint4*>(nid + r);
+        tt = *reinterpret_cast<const uint4*>(tnode + r);
+    }
     if (in_lds) {
         for (int u = threadIdx.x; u < Ua; u += kBlock) s_rules[u] = rules[u];
         __syncthreads();
     }
-    // 8 rows per thread (rows_padded is a multiple of 16): one 16-byte load of their node ids,
-    // then their bin gathers all in flight before any result is needed.
-    const int64_t stride = (int64_t)gridDim.x * kBlock * 8;
-    for (int64_t r = ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8; r < rows_padded; r += stride) {
-        const uint4 nn = *reinterpret_cast<const uint4*>(nid + r);
+    for (; r < rows_padded; r += stride) {
+        if (r != ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8) {  // later groups
+            nn = *reinterpret_cast<const uint4*>(nid + r);
+            tt = *reinterpret_cast<const uint4*>(tnode + r);
+        }
         uint32_t nw[4] = {nn.x, nn.y, nn.z, nn.w};
         uint32_t n8[8];
 #pragma unroll
@@ -47,7 +58,6 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
 #pragma unroll
         for (int j = 0; j < 8; ++j) any = any || n8[j] < (uint32_t)Ua;
         if (!any) continue;  // PB_INACTIVE or stale rows only
-        const uint4 tt = *reinterpret_cast<const uint4*>(tnode + r);
         uint32_t tw[4] = {tt.x, tt.y, tt.z, tt.w};
         SplitRule rr[8];
         uint32_t bin[8];
