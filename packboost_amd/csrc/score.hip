@@ -1631,10 +1631,13 @@ hipError_t launch_decide(const DecideCands& dc, int32_t max_nodes, const NodeTot
                          const int32_t* cur_ids, int32_t* next_ids, SplitRule* rules,
                          pb_decision* dec, float* values, pb_candidate* node_best,
                          hipStream_t s) {
-    // wide candidate sets: the per-node reductions in parallel, one workgroup per node slot
-    // (one workgroup walking max_nodes x W winners took ~0.1 ms per depth at 128 x 2000)
+    // the per-node reductions in parallel, one workgroup per node slot, for wide candidate sets
+    // (one workgroup walking max_nodes x W winners took ~0.1 ms per depth at 128 x 2000) and
+    // whenever there are more nodes than the decision workgroup has wavefronts (each wavefront
+    // would reduce its nodes one after another: 32 nodes x 24 winners took 17 us in one
+    // workgroup, against about 6 us for both launches)
     int32_t w_decide = dc.W;
-    if ((int64_t)max_nodes * dc.W >= (int64_t)32 * 1024) {
+    if ((int64_t)max_nodes * dc.W >= (int64_t)32 * 1024 || max_nodes > kBlock / kWave) {
         hipLaunchKernelGGL(node_best_kernel, dim3(max_nodes), dim3(kBlock), 0, s, dc, st, depth,
                            node_best);
         w_decide = 0;
