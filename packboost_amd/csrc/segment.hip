@@ -69,18 +69,40 @@ __device__ __forceinline__ int32_t wg_scan_excl(int32_t v, int32_t* total) {
 }
 
 // Exclusive scan of n int32 values in place by one workgroup: vals[i] <- sum of vals[0 .. i-1],
-// vals[n] <- the total. Each thread sums a contiguous strip, the strip sums are scanned across
-// the workgroup by wavefront shuffles, and each thread rewrites its strip from its offset.
+// vals[n] <- the total. Each thread sums a contiguous strip (16-byte aligned, read four values
+// at a time), the strip sums are scanned across the workgroup by wavefront shuffles, and each
+// thread rewrites its strip from its offset.
 __device__ void block_scan_excl(int32_t* vals, int n) {
     const int tid = threadIdx.x;
-    const int per = (n + kBlock - 1) / kBlock;
+    const int per = ((n + kBlock - 1) / kBlock + 3) & ~3;
     const int i0 = min(n, tid * per), i1 = min(n, i0 + per);
     int32_t sum = 0;
-    for (int i = i0; i < i1; ++i) sum += vals[i];
+    int i = i0;
+#pragma unroll 4
+    for (; i + 4 <= i1; i += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(vals + i);
+        sum += v.x + v.y + v.z + v.w;
+    }
+    for (; i < i1; ++i) sum += vals[i];
     int32_t total;
     int32_t run = wg_scan_excl(sum, &total);
     if (tid == 0) vals[n] = total;
-    for (int i = i0; i < i1; ++i) {
+    i = i0;
+#pragma unroll 4
+    for (; i + 4 <= i1; i += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(vals + i);
+        int4 o;
+        o.x = run;
+        run += v.x;
+        o.y = run;
+        run += v.y;
+        o.z = run;
+        run += v.z;
+        o.w = run;
+        run += v.w;
+        *reinterpret_cast<int4*>(vals + i) = o;
+    }
+    for (; i < i1; ++i) {
         const int32_t v = vals[i];
         vals[i] = run;
         run += v;
@@ -109,16 +131,39 @@ __global__ __launch_bounds__(kBlock) void seg_begin_kernel(const float* __restri
 
 __global__ __launch_bounds__(kBlock) void seg_chunks_kernel(SegState s, const int32_t* __restrict__ seg,
                                                       int32_t depth) {
+    // the chunk counts of a contiguous strip of (era, slot) entries per thread, summed, scanned
+    // across the workgroup, then written as exclusive prefixes (the counts are recomputed, not
+    // stored and read back)
     const int U = s.st->u_active[depth];
     const int n = s.E * (U + 1);
-    for (int x = threadIdx.x; x < n; x += kBlock) {
-        const int e = x / (U + 1);
-        const int v = x - e * (U + 1);
+    const int per = (n + kBlock - 1) / kBlock;
+    const int i0 = min(n, (int)threadIdx.x * per), i1 = min(n, i0 + per);
+    auto chunks = [&](int e, int v) -> int32_t {
         const int32_t len = seg_end(s, seg, e, v, U) - seg[(int64_t)e * s.segw + v];
-        s.cp[x] = (len + kSegChunk - 1) / kSegChunk;
+        return (len + kSegChunk - 1) / kSegChunk;
+    };
+    const int e0 = i0 / (U + 1);
+    const int v0 = i0 - e0 * (U + 1);
+    int32_t sum = 0;
+    for (int i = i0, e = e0, v = v0; i < i1; ++i) {
+        sum += chunks(e, v);
+        if (++v > U) {
+            v = 0;
+            ++e;
+        }
     }
-    __syncthreads();
-    block_scan_excl(s.cp, n);
+    int32_t total;
+    int32_t run = wg_scan_excl(sum, &total);
+    if (threadIdx.x == 0) s.cp[n] = total;
+    for (int i = i0, e = e0, v = v0; i < i1; ++i) {
+        const int32_t c = chunks(e, v);
+        s.cp[i] = run;
+        run += c;
+        if (++v > U) {
+            v = 0;
+            ++e;
+        }
+    }
 }
 
 // the chunk's segment, its rows [r0, r1), and whether its slot split (then rule)
