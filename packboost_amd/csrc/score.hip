@@ -400,7 +400,7 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
     const int T = a.T;
     const int RT = a.rt;
     float* recip = reinterpret_cast<float*>(smem);
-    for (int i = tid; i < RT; i += kBlock) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
+    for (int i = tid; i < RT; i += (int)blockDim.x) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
     __syncthreads();
 
     const bool owner = tid < T;
@@ -1605,8 +1605,9 @@ hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStr
     }
     if (a.T < kWave)
         hipLaunchKernelGGL(des_score_pc_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
-    else if (wide)
-        hipLaunchKernelGGL(des_score_wide_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
+    else if (wide)  // one thread per threshold: whole wavefronts up to T (T <= 254)
+        hipLaunchKernelGGL(des_score_wide_kernel<C32>, dim3(grid), dim3((a.T + kWave - 1) / kWave * kWave),
+                           lds_bytes, s, a);
     else
         hipLaunchKernelGGL(des_score_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
     return hipGetLastError();
