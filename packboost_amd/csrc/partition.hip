@@ -97,45 +97,78 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
     }
 }
 
-__global__ void reset_kernel(Frontier* st, int32_t root_active, int32_t* cur_ids) {
-    if (threadIdx.x == 0) {
-        for (int d = 0; d <= PB_MAX_DEPTH; ++d) st->u_active[d] = 0;
-        st->u_active[0] = root_active;
-        st->tree_size = 1;
-        st->reserved[kNonFinite] = 0;
-        cur_ids[0] = 0;
-    }
-}
-
 // grad = preds - y (booster.py:2149-2151); hess == 1 is implicit (counts). Every row starts in
 // the root; the pad rows [N, rows_padded) are parked with grad 0 and PB_INACTIVE. Also the sum
 // of |grad| over each window of kGradWinRows consecutive rows (4 per thread, then a fixed
 // reduction tree, so the sums do not depend on scheduling), which bounds the eras' fixed-point
-// scales.
+// scales. The first thread also resets the frontier of the round. VEC: the 4 rows of a thread
+// move as one 16-byte (grad, preds, y) and 8-byte (node ids, tree nodes) access (the host checks
+// the alignment; rows_padded is a multiple of 16).
+template <bool VEC>
 __global__ __launch_bounds__(kBlock) void round_begin_kernel(const float* __restrict__ preds,
                                                          const float* __restrict__ y,
                                                          float* __restrict__ grad,
                                                          uint16_t* __restrict__ nid,
                                                          uint16_t* __restrict__ tnode, int64_t N,
                                                          int64_t rows_padded, int32_t root_active,
-                                                         float* __restrict__ win_sum) {
+                                                         float* __restrict__ win_sum, Frontier* st,
+                                                         int32_t* cur_ids) {
     __shared__ float s_sum[kBlock / kWave];
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        for (int d = 0; d <= PB_MAX_DEPTH; ++d) st->u_active[d] = 0;
+        st->u_active[0] = root_active;
+        st->tree_size = 1;
+        st->reserved[kNonFinite] = 0;
+        cur_ids[0] = 0;
+    }
+    const uint16_t n_root = root_active ? (uint16_t)0 : (uint16_t)PB_INACTIVE;
     const int64_t nwin = (rows_padded + kGradWinRows - 1) / kGradWinRows;
     for (int64_t w = blockIdx.x; w < nwin; w += gridDim.x) {
         const int64_t r0 = w * kGradWinRows + (int64_t)threadIdx.x * 4;
         float s = 0.0f;
+        if (VEC) {
+            if (r0 < rows_padded) {  // r0 + 3 < rows_padded too
+                float4 gv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                ushort4 nv = make_ushort4(PB_INACTIVE, PB_INACTIVE, PB_INACTIVE, PB_INACTIVE);
+                if (r0 + 3 < N) {
+                    const float4 p = *reinterpret_cast<const float4*>(preds + r0);
+                    const float4 t = *reinterpret_cast<const float4*>(y + r0);
+                    gv = make_float4(p.x - t.x, p.y - t.y, p.z - t.z, p.w - t.w);
+                    s = s + fabsf(gv.x);
+                    s = s + fabsf(gv.y);
+                    s = s + fabsf(gv.z);
+                    s = s + fabsf(gv.w);
+                    nv = make_ushort4(n_root, n_root, n_root, n_root);
+                } else {
+                    float* g4 = reinterpret_cast<float*>(&gv);
+                    uint16_t* n4 = reinterpret_cast<uint16_t*>(&nv);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t r = r0 + j;
-            if (r >= rows_padded) break;
-            float g = 0.0f;
-            if (r < N) {
-                g = preds[r] - y[r];
-                s = s + fabsf(g);
+                    for (int j = 0; j < 4; ++j) {
+                        if (r0 + j < N) {
+                            g4[j] = preds[r0 + j] - y[r0 + j];
+                            s = s + fabsf(g4[j]);
+                            n4[j] = n_root;
+                        }
+                    }
+                }
+                *reinterpret_cast<float4*>(grad + r0) = gv;
+                *reinterpret_cast<ushort4*>(nid + r0) = nv;
+                *reinterpret_cast<ushort4*>(tnode + r0) = make_ushort4(0, 0, 0, 0);
             }
-            grad[r] = g;
-            nid[r] = (r < N && root_active) ? (uint16_t)0 : (uint16_t)PB_INACTIVE;
-            tnode[r] = 0;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t r = r0 + j;
+                if (r >= rows_padded) break;
+                float g = 0.0f;
+                if (r < N) {
+                    g = preds[r] - y[r];
+                    s = s + fabsf(g);
+                }
+                grad[r] = g;
+                nid[r] = r < N ? n_root : (uint16_t)PB_INACTIVE;
+                tnode[r] = 0;
+            }
         }
 #pragma unroll
         for (int m = 1; m < kWave; m <<= 1) s = s + __shfl_xor(s, m);
@@ -181,18 +214,37 @@ __global__ void select_subsets_kernel(const pb_round_header* prev, int32_t D, in
 
 // pack_sum[r] = sum_{t<B} value[leaf(r)] in float32, tree order (booster.py:586-598, the
 // B trees are identical); preds += float32(lr) * pack_sum as two rounded float32 ops
-// (torch: tmp = lr * pack_sum; preds += tmp).
+// (torch: tmp = lr * pack_sum; preds += tmp). VEC: 4 rows per thread with one 8-byte tree-node
+// and one 16-byte prediction access (the host checks the alignment), the last N % 4 rows one by
+// one.
+__device__ __forceinline__ float pack_step(float p, float v, int32_t B, float lr) {
+    float s = 0.0f;
+    for (int t = 0; t < B; ++t) s = s + v;
+    const float tmp = lr * s;
+    return p + tmp;
+}
+
+template <bool VEC>
 __global__ __launch_bounds__(kBlock) void round_end_kernel(const uint16_t* __restrict__ tnode,
                                                        const float* __restrict__ values,
                                                        int32_t B, float lr,
                                                        float* __restrict__ preds, int64_t N) {
     const int64_t stride = (int64_t)gridDim.x * kBlock;
-    for (int64_t r = (int64_t)blockIdx.x * kBlock + threadIdx.x; r < N; r += stride) {
-        const float v = values[tnode[r]];
-        float s = 0.0f;
-        for (int t = 0; t < B; ++t) s = s + v;
-        const float tmp = lr * s;
-        preds[r] = preds[r] + tmp;
+    const int64_t t0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (VEC) {
+        const int64_t n4 = N / 4;
+        for (int64_t q = t0; q < n4; q += stride) {
+            const ushort4 tn = *reinterpret_cast<const ushort4*>(tnode + 4 * q);
+            float4 p = *reinterpret_cast<const float4*>(preds + 4 * q);
+            p.x = pack_step(p.x, values[tn.x], B, lr);
+            p.y = pack_step(p.y, values[tn.y], B, lr);
+            p.z = pack_step(p.z, values[tn.z], B, lr);
+            p.w = pack_step(p.w, values[tn.w], B, lr);
+            *reinterpret_cast<float4*>(preds + 4 * q) = p;
+        }
+        for (int64_t r = 4 * n4 + t0; r < N; r += stride) preds[r] = pack_step(preds[r], values[tnode[r]], B, lr);
+    } else {
+        for (int64_t r = t0; r < N; r += stride) preds[r] = pack_step(preds[r], values[tnode[r]], B, lr);
     }
 }
 
@@ -202,6 +254,8 @@ __global__ void round_header_kernel(const Frontier* st, pb_round_header* h) {
     if (i == 0) h->tree_size = st->tree_size;
     if (i < 6) h->reserved[i] = i == 0 ? st->reserved[kNonFinite] : 0;
 }
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 int grid_for(int64_t work, int per_block, int cap) {
     int64_t g = (work + per_block - 1) / per_block;
@@ -231,13 +285,16 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
                               uint16_t* tnode, int64_t N, int64_t rows_padded, int32_t root_active,
                               const int32_t* era_off, int32_t E, float* win_sum, int32_t* sh_era,
                               Frontier* st, int32_t* cur_ids, hipStream_t s) {
-    hipLaunchKernelGGL(reset_kernel, dim3(1), dim3(64), 0, s, st, root_active, cur_ids);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     const int grid = grid_for(rows_padded, kGradWinRows, 1024);
-    hipLaunchKernelGGL(round_begin_kernel, dim3(grid), dim3(kBlock), 0, s, preds, y, grad, nid,
-                       tnode, N, rows_padded, root_active, win_sum);
-    e = hipGetLastError();
+    const bool vec = (rows_padded % 16 == 0) && aligned(preds, 16) && aligned(y, 16) && aligned(grad, 16) &&
+                     aligned(nid, 8) && aligned(tnode, 8);
+    if (vec)
+        hipLaunchKernelGGL(round_begin_kernel<true>, dim3(grid), dim3(kBlock), 0, s, preds, y, grad, nid,
+                           tnode, N, rows_padded, root_active, win_sum, st, cur_ids);
+    else
+        hipLaunchKernelGGL(round_begin_kernel<false>, dim3(grid), dim3(kBlock), 0, s, preds, y, grad, nid,
+                           tnode, N, rows_padded, root_active, win_sum, st, cur_ids);
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(era_scale_kernel, dim3((E + kBlock - 1) / kBlock), dim3(kBlock), 0, s, era_off,
                        E, win_sum, sh_era, st);
@@ -251,9 +308,15 @@ hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream
 
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
                             float lr, float* preds, int64_t N, hipStream_t s) {
-    const int grid = grid_for(N, kBlock, 8192);
-    hipLaunchKernelGGL(round_end_kernel, dim3(grid), dim3(kBlock), 0, s, tnode, values, pack_size,
-                       lr, preds, N);
+    if (aligned(tnode, 8) && aligned(preds, 16)) {
+        const int grid = grid_for(std::max<int64_t>(1, N / 4), kBlock, 8192);
+        hipLaunchKernelGGL(round_end_kernel<true>, dim3(grid), dim3(kBlock), 0, s, tnode, values, pack_size,
+                           lr, preds, N);
+    } else {
+        const int grid = grid_for(N, kBlock, 8192);
+        hipLaunchKernelGGL(round_end_kernel<false>, dim3(grid), dim3(kBlock), 0, s, tnode, values, pack_size,
+                           lr, preds, N);
+    }
     return hipGetLastError();
 }
 
