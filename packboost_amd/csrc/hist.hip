@@ -406,13 +406,31 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 const int stride = side == 0 ? nb2 : (side == 1 ? nb : 1);
                 const int s1 = side == 0 ? nb : nb2;   // stride of the first other feature
                 const int s2 = side == 2 ? nb : 1;     // stride of the second other feature
-                for (int b = b_lo; b <= bb; ++b)
+                for (int b = b_lo; b <= bb; ++b) {
+                    if (nb == 5) {
+                        // the 25 partner cells of the bin in two batches (15 and 10 reads)
+                        // instead of five dependent ones
+                        auto batch = [&](auto lo, auto hi) {
+                            constexpr int L = decltype(lo)::value, H = decltype(hi)::value;
+                            unsigned long long v[(H - L) * 5];
+#pragma unroll
+                            for (int o1 = L; o1 < H; ++o1)
+#pragma unroll
+                                for (int o2 = 0; o2 < 5; ++o2)
+                                    v[(o1 - L) * 5 + o2] = hc[(b * stride + o1 * s1 + o2 * s2) * C];
+#pragma unroll
+                            for (int o = 0; o < (H - L) * 5; ++o) tot += v[o];
+                        };
+                        batch(std::integral_constant<int, 0>{}, std::integral_constant<int, 3>{});
+                        batch(std::integral_constant<int, 3>{}, std::integral_constant<int, 5>{});
+                        continue;
+                    }
                     for (int o1 = 0; o1 < nb; ++o1) {
                         const unsigned long long* base = hc + (b * stride + o1 * s1) * C;
                         tot += (nb <= 4) ? rsum(base, s2 * C, std::integral_constant<int, 4>{})
-                                         : (nb == 5) ? rsum(base, s2 * C, std::integral_constant<int, 5>{})
-                                                     : rsum(base, s2 * C, std::integral_constant<int, 6>{});
+                                         : rsum(base, s2 * C, std::integral_constant<int, 6>{});
                     }
+                }
             } else if (P == 2) {
                 const int step = (side == 0 ? 1 : nb) * C;  // the partner's bins
                 for (int b = b_lo; b <= bb; ++b) {
