@@ -166,8 +166,6 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     // buffer b: sG, sGL, sL, sWD (each EC x cstride), then sCt, sGt (each EC)
     const int buf_stride = 4 * buf_words + 2 * EC;
 
-    for (int i = tid; i < RT; i += kBlock) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
-
     const float lam = a.lambda_l2;
     const float alpha = a.era_alpha;
     const bool use_dir = a.dir_w != 0.0f;
@@ -292,7 +290,7 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                     const bool act = w > 0.0f;  // implies has; wsum + w > 0 then holds
                     const float wn = wsum + w;
                     const int wi = (int)wn;
-                    facb[j] = (unit_w && wi < RT) ? recip[act ? wi : 0] : w / (act ? wn : 1.0f);
+                    facb[j] = (unit_w && wi < RT) ? (act ? exact_recip(wn) : 0.0f) : w / (act ? wn : 1.0f);
                     wsum = act ? wn : wsum;
                     wb[j] = w;
                     actb[j] = act;
@@ -390,7 +388,6 @@ struct EraBatch {
 
 template <bool C32>
 __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
-    extern __shared__ unsigned char smem[];
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int u = blockIdx.x / a.ntiles;
@@ -399,9 +396,6 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
     if (u >= Ua) return;
     const int T = a.T;
     const int RT = a.rt;
-    float* recip = reinterpret_cast<float*>(smem);
-    for (int i = tid; i < RT; i += (int)blockDim.x) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
-    __syncthreads();
 
     const bool owner = tid < T;
     const int t = owner ? tid : T - 1;  // idle lanes mirror the last threshold (never owners)
@@ -475,7 +469,7 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
         const bool act = w > 0.0f;
         const float wn = wsum + w;
         const int wi = (int)wn;
-        const float fac = (unit_w && wi < RT) ? recip[act ? wi : 0] : w / (act ? wn : 1.0f);
+        const float fac = (unit_w && wi < RT) ? (act ? exact_recip(wn) : 0.0f) : w / (act ? wn : 1.0f);
         wsum = act ? wn : wsum;
         const float delta = gain - mean;
         const float mean_n = mean + fac * delta;
@@ -712,11 +706,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
     float tg = 0.0f;
     const bool owner = tid < ncand;
     // Consumer: eras in batches of 8 — all record reads first, then the weight-sum chain with
-    // its (independent) factor lookups, then the mean/M2 chain. With unit era weights
-    // (TABLE) the factor w / wsum is 1/n, read from the table of IEEE 1/n (bit-identical),
-    // and w * delta == delta; otherwise it is the IEEE division. Inactive eras get factor 0
-    // and keep mean/M2 by selection. TABLE and DIR are compile-time, so the loop has no
-    // branches.
+    // its (independent) factor lookups, then the mean/M2 chain. With unit era weights (TABLE)
+    // the factor w / wsum is 1/n, read from the table of IEEE 1/n (bit-identical), and
+    // w * delta == delta; otherwise it is the IEEE division. The lookups are issued off the
+    // mean/M2 chain (computing 1/n with exact_recip instead measured slower here: more VALU on
+    // the consumer wave). Inactive eras get factor 0 and keep mean/M2 by selection. TABLE and
+    // DIR are compile-time, so the loop has no branches.
     const bool table = unit_w && a.E < RT;
     auto consume = [&](int chunk, auto table_flag, auto dir_flag) {
         constexpr bool TABLE = decltype(table_flag)::value;
@@ -1594,7 +1589,7 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
 template <bool C32>
 hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
     const bool wide = a.T >= kWave && !a.staged;
-    if (wide) lds_bytes = (size_t)a.rt * 4;
+    if (wide) lds_bytes = 0;  // the wide scorer computes 1/n (exact_recip) instead of a table
     const void* fn = (a.T < kWave) ? reinterpret_cast<const void*>(&des_score_pc_kernel<C32>)
                      : wide        ? reinterpret_cast<const void*>(&des_score_wide_kernel<C32>)
                                    : reinterpret_cast<const void*>(&des_score_kernel<C32>);
