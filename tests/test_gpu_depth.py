@@ -231,6 +231,34 @@ def test_hist_joint_flush_bins(hip, oracle_mod, monkeypatch, pairs, nb, layout):
         g.close()
 
 
+def test_wide_scorer_many_eras(hip, oracle_mod):
+    """The many-threshold scorer over 3500 eras with unit era weights, fed the oracle's planes:
+    every candidate bit-identical to the oracle scorer. Its Welford factor 1/n is computed
+    (reciprocal plus one Newton step) for every active-era count n up to 3500, so this pins that
+    computation against the IEEE division the reference uses."""
+    E, nb, U, K = 3500, 70, 2, 2
+    p = make_problem(77, E * 8, 3, E, nb, U, ragged=False, inactive_frac=0.0)
+    feats = np.array([2, 0], np.int32)
+    kw = dict(lambda_l2=1e-6, lambda_dro=0.5, direction_weight=0.0, era_alpha=0.0, min_samples_leaf=1)
+    print(f"[wide many eras] E={E} nb={nb}", flush=True)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, want_planes=True, **kw)
+    rc, rg = ref.planes
+    rg1 = rg.copy()
+    rg1[..., nb - 1] = rg[:, :, :1, nb - 1]
+    g = GpuDepth(hip, p, K, msl=1)
+    try:
+        g.load_planes(rc, rg1)
+        params = split_params(hip, lambda_l2=1e-6, lambda_dro=0.5, msl=1)
+        c = g.score(feats, params, nb - 1)
+        sp = oracle_mod.score_planes(rc, rg1, feats, None, **kw)
+        np.testing.assert_array_equal(c["valid"].astype(bool), sp["valid"].astype(bool))
+        v = sp["valid"].astype(bool)
+        assert v.sum() > 0
+        np.testing.assert_array_equal(c["score"][v].view(np.uint32), sp["score"][v].view(np.uint32))
+    finally:
+        g.close()
+
+
 WIDE_CASES = [c for c in CASES if c[4] - 1 >= 64]
 
 
