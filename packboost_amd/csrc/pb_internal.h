@@ -62,15 +62,14 @@ __device__ __forceinline__ unsigned long long wave_scan_incl_u64(unsigned long l
 }
 
 // One row's 64-bit histogram addend (q << 16) + 1 with q = round(g * scale) (|q| < 2^45): the
-// count 1 in the low 16 bits, the fixed-point grad above it. g * scale is exact in double (scale
-// is a power of two), so one double fma adds 1.5 * 2^52 to the exact product with a single
-// rounding: to an integer with ties to even (as rintf does), left in the low mantissa bits, so
-// the double's bit pattern minus that of 1.5 * 2^52 (low word 0) is q in two's complement for
-// |q| < 2^51. The same value as rounding a float product (exact unless below 2^-126, where both
-// give 0). Five instructions (conversion, fma, subtract, align, shift-or) where float
-// floor/split conversions took nine; double fmas issue at the full rate on gfx950.
+// count 1 in the low 16 bits, the fixed-point grad above it. g * scale is exact in float (scale
+// is a power of two); adding 1.5 * 2^52 to it in double rounds it to an integer with ties to
+// even (as rintf does) and leaves that integer in the low mantissa bits, so the double's bit
+// pattern minus that of 1.5 * 2^52 (low word 0) is q in two's complement for |q| < 2^51. Six
+// instructions where float floor/split conversions took nine; double adds issue at the full
+// rate on gfx950.
 __device__ __forceinline__ unsigned long long grad_addend(float g, float scale) {
-    const double y = __builtin_fma((double)g, (double)scale, 6755399441055744.0);
+    const double y = (double)(g * scale) + 6755399441055744.0;
     const unsigned long long b = (unsigned long long)__double_as_longlong(y);
     const uint32_t lo = (uint32_t)b;                       // q's low word
     const uint32_t hi = (uint32_t)(b >> 32) - 0x43380000u;  // q's high word
