@@ -33,6 +33,9 @@ CASES = [
     # 210 nodes x 40 features x 254 thresholds: max_nodes x wavefront winners >= 32768, so the
     # per-node winners are reduced by one workgroup per node before the decision step
     (9, 40000, 48, 4, 255, 210, 40, 2, 1e-6, 0.5, 0.0, 0.0),
+    # one node x 128 bins x 20 features (config 1's first depth): single-feature tiles of 16
+    # uint8 columns, the widest single-feature launch shape
+    (10, 10000, 20, 10, 128, 1, 20, 20, 1.0, 0.5, 0.0, 0.0),
 ]
 
 
