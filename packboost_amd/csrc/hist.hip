@@ -74,10 +74,11 @@ __device__ __forceinline__ uint32_t mad_bytes(uint32_t x, uint32_t m, uint32_t y
 // Waves per SIMD: six (at most 80 VGPRs) for more loads in flight per CU (measured 6% faster
 // over the depths of a 2.4M-row, 5-bin round than the unconstrained 4-wave build); five for the
 // 16-feature pair tile (measured); four for the 16-feature single-feature tile, which spills at
-// 80 VGPRs and fits 92 without spills (its 128-bin depth measured 7% faster that way).
+// 80 VGPRs and fits 92 without spills (its 128-bin depth measured 7% faster that way), and for
+// the 32-feature pair tile (chosen only when the feature tile is forced), which spills at 96.
 template <int FT, int P>
 constexpr int hist_waves_per_eu() {
-    return (P == 2 && FT >= 16) ? 5 : (P == 1 && FT >= 16) ? 4 : 6;
+    return (P == 2 && FT >= 32) ? 4 : (P == 2 && FT >= 16) ? 5 : (P == 1 && FT >= 16) ? 4 : 6;
 }
 
 template <int FT, int P, bool NIB, int BS>

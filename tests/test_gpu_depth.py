@@ -210,6 +210,32 @@ def test_hist_copies(hip, oracle_mod, monkeypatch, pairs, copies, block):
 
 
 @pytest.mark.parametrize("layout", ["u8", "nibble"])
+@pytest.mark.parametrize("pairs,ftile", [(2, 32), (1, 16)])
+def test_hist_widest_tiles(hip, oracle_mod, monkeypatch, pairs, ftile, layout):
+    """The widest feature tiles (32 features in pairs, 16 single features: the instantiations
+    with the most registers per thread), forced on a 5-bin panel with an odd feature count so
+    the last pair's partner runs past the tile. Counts bit-exact, grads within the per-cell
+    mass bar."""
+    monkeypatch.setenv("PB_HIST_PAIRS", str(pairs))
+    monkeypatch.setenv("PB_HIST_FTILE", str(ftile))
+    print(f"[hist widest tiles] P={pairs} FT={ftile} {layout}", flush=True)
+    K = 33
+    p = make_problem(70 + ftile + pairs, 12000, 40, 6, 5, 2, empty_era=True)
+    feats = np.random.default_rng(ftile + pairs).permutation(40)[:K].astype(np.int32)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, 5, want_planes=True)
+    g = GpuDepth(hip, p, K, msl=3, layout=layout)
+    try:
+        g.hist(feats)
+        cnt, gp = g.planes()
+        np.testing.assert_array_equal(cnt, ref.planes[0])
+        mass = _abs_mass(p, 2)[:, :, None, None]
+        err = np.abs(gp.astype(np.float64) - ref.planes[1].astype(np.float64))
+        assert np.all(err <= 1e-5 * np.maximum(mass, 1.0))
+    finally:
+        g.close()
+
+
+@pytest.mark.parametrize("layout", ["u8", "nibble"])
 @pytest.mark.parametrize("pairs,nb", [(2, 2), (2, 3), (2, 4), (2, 5), (2, 6), (2, 7), (2, 8), (2, 9),
                                       (3, 2), (3, 3), (3, 4), (3, 6)])
 def test_hist_joint_flush_bins(hip, oracle_mod, monkeypatch, pairs, nb, layout):
