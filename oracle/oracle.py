@@ -294,10 +294,12 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
         cut_selection: str = "mass", layer_feature_fraction: float = 1.0, era_alpha: float = 0.0,
         random_state: int | None = None, rng: torch.Generator | None = None,
         stop_after_depths: int | None = None, trace: list | None = None,
-        splitter: str = "restated") -> FitResult:
+        splitter: str = "restated", init_preds: np.ndarray | None = None) -> FitResult:
     """PackBoost.fit on the native CPU path, restated (booster.py:375-599). splitter
     "reference" runs each depth's split finder on the compiled reference frontier
-    (ref_split_batch) instead of the C restatement."""
+    (ref_split_batch) instead of the C restatement. init_preds (float32 [N]) continues a fit
+    from those training predictions (with `rng` left where the earlier rounds took it, a fit
+    split into calls grows the same trees as one call)."""
     split_fn = ref_split_batch if splitter == "reference" else split_batch
     import time
 
@@ -315,7 +317,8 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
             rng.manual_seed(int(random_state))
     k = min(F, max(1, int(round(float(layer_feature_fraction) * F))))
     msl = int(min_samples_leaf)
-    preds = np.zeros(N, dtype=np.float32)
+    preds = np.zeros(N, dtype=np.float32) if init_preds is None else \
+        np.array(init_preds, dtype=np.float32, copy=True)
     rounds, logs, rsec = [], [], []
     split_ms = 0.0
     lr32 = np.float32(learning_rate)
@@ -388,18 +391,37 @@ def fit(bins: np.ndarray, y: np.ndarray, era_codes: np.ndarray | None, *, num_ro
             frontier = nxt
         arrs = {key: np.array([n[key] for n in nodes]) for key in
                 ("feature", "threshold", "left", "right", "value", "is_leaf")}
-        # pack aggregation: B float32 adds of the row's leaf value, then preds += lr * sum
         leaf_val = np.zeros(N, dtype=np.float32)
         for nid, rows in leaf_rows.items():
             if rows.size:
                 leaf_val[rows] = np.float32(nodes[nid]["value"])
-        pack_sum = np.zeros(N, dtype=np.float32)
-        for _t in range(pack_size):
-            pack_sum = (pack_sum + leaf_val).astype(np.float32)
-        preds = (preds + (lr32 * pack_sum).astype(np.float32)).astype(np.float32)
+        preds = pack_update(preds, leaf_val, pack_size, lr32)
         rounds.append(arrs)
         rsec.append(time.perf_counter() - t0)
     return FitResult(rounds=rounds, preds=preds, depth_logs=logs, split_ms=split_ms, round_seconds=rsec)
+
+
+def pack_update(preds: np.ndarray, leaf_val: np.ndarray, pack_size: int, lr32) -> np.ndarray:
+    """End of round (booster.py:581-599): pack_sum = B float32 adds of the row's leaf value (the
+    pack's identical trees, in tree order), then preds += float32(lr) * pack_sum."""
+    pack_sum = np.zeros(leaf_val.shape[0], dtype=np.float32)
+    for _t in range(pack_size):
+        pack_sum = (pack_sum + leaf_val).astype(np.float32)
+    return (preds + (np.float32(lr32) * pack_sum).astype(np.float32)).astype(np.float32)
+
+
+def replay_preds(rounds: list[dict[str, np.ndarray]], bins: np.ndarray, pack_size: int,
+                 learning_rate: float, rows: np.ndarray | None = None) -> np.ndarray:
+    """The training predictions fit() leaves after `rounds`, recomputed from the trees alone: each
+    row's leaf by the partition rule bin <= threshold -> left (leaf_index), then pack_update. With
+    `rows`, only those rows (bins may then hold just them, in that order)."""
+    sub = bins if rows is None else bins[rows]
+    preds = np.zeros(sub.shape[0], dtype=np.float32)
+    lr32 = np.float32(learning_rate)
+    for arrs in rounds:
+        leaf_val = np.asarray(arrs["value"]).astype(np.float32)[leaf_index(arrs, sub)]
+        preds = pack_update(preds, leaf_val, pack_size, lr32)
+    return preds
 
 
 def predict_tree(arrs: dict[str, np.ndarray], bins: np.ndarray) -> np.ndarray:

@@ -198,9 +198,16 @@ class PackBoost:
         self._packed_forest: list[dict[str, torch.Tensor]] = []
         self._num_features: int | None = None
         self._use_native_cuda = self._device.type == "cuda" and native_backends.cuda_available()
-        # per-depth phase times in the depth logs (hist_ms, score_ms, partition_ms): off by
-        # default, since timing every phase runs the rounds one at a time
+        # per-depth phase times in the depth logs (hist_ms, score_ms, partition_ms): every
+        # PACKBOOST_PHASE_EVERY-th round (default 8, round 1 included) is timed phase by phase
+        # with HIP events while the round loop stays pipelined, and the other rounds' logs carry
+        # the last timed round's values (phase_ms_round names it). profile_phases (or
+        # PACKBOOST_PROFILE_PHASES=1) times every round, one round at a time.
         self.profile_phases = os.getenv("PACKBOOST_PROFILE_PHASES", "0") not in ("", "0")
+        try:
+            self.phase_every = max(1, int(os.getenv("PACKBOOST_PHASE_EVERY", "8")))
+        except ValueError:
+            self.phase_every = 8
 
     def _phase_times(self) -> bool:
         return bool(self.profile_phases)
@@ -284,8 +291,10 @@ class PackBoost:
         side = torch.cuda.Stream(device)
         try:
             t0 = perf_counter()
+            last_phase: dict[int, tuple[np.ndarray, int]] = {}  # depth -> (times, timed round)
             for round_idx, (log, preds_after, ready) in enumerate(
-                    fitter.rounds(self._rng, num_rounds, phase_times=self._phase_times())):
+                    fitter.rounds(self._rng, num_rounds, phase_times=self._phase_times(),
+                                  phase_every=self.phase_every)):
                 arrs = tree_arrays_from_log(log, cfg, N)
                 self._rounds.append(arrs)
                 self._trees_cache = None
@@ -294,7 +303,9 @@ class PackBoost:
                 for d in range(int(cfg.max_depth)):
                     if int(log.u_active[d]) <= 0:
                         break
-                    dl = depth_log_from_round(log, d, cfg, k, self._histogram_mode)
+                    if log.phase_ms is not None:
+                        last_phase[d] = (log.phase_ms, round_idx + 1)
+                    dl = depth_log_from_round(log, d, cfg, k, self._histogram_mode, last_phase.get(d))
                     self._depth_logs.append(dl)
                     if self._logger.isEnabledFor(logging.INFO):
                         self._logger.info(json.dumps(dl))

@@ -76,7 +76,8 @@ class RoundLog:
     root_grad: float          # float32 sum of grad over all rows (root value numerator)
     depths_drawn: int         # feature subsets the reference would have drawn
     phase_ms: np.ndarray | None = None  # float64 [4][D] GPU ms of hist / score / decide /
-                                        # partition per depth (rounds(phase_times=True) only)
+                                        # partition per depth (timed rounds only: rounds()
+                                        # with phase_times or phase_every)
 
 
 class _DrawStream:
@@ -393,7 +394,7 @@ class DeviceFit:
         return ms.reshape(4, -1)[:, : self.D], n.reshape(4, -1)[:, : self.D]
 
     def rounds(self, rng: torch.Generator, num_rounds: int, *, profile_every: int = 0,
-               profile_mode: int = 2, phase_times: bool = False):
+               profile_mode: int = 2, phase_times: bool = False, phase_every: int = 0):
         """Runs `num_rounds` rounds with the host one round ahead of the GPU.
 
         profile_every > 0 turns the library's phase timing (pb_profile_enable, mode
@@ -403,6 +404,11 @@ class DeviceFit:
         phase_times: every round timed phase by phase, each read back with its log
         (RoundLog.phase_ms); rounds then run one at a time (no round is enqueued ahead), so
         the times are the round's own.
+
+        phase_every > 1: rounds 0, phase_every, 2 * phase_every, ... are timed phase by phase
+        and their RoundLog.phase_ms filled, while the loop stays one round ahead (the next round
+        is never timed, so reading a timed round's events waits for that round only);
+        phase_every == 1 is phase_times.
 
         Yields (RoundLog, preds_after, ready) per round in order. `preds_after` holds the
         predictions after that round until the consumer resumes the generator (the GPU may
@@ -433,8 +439,12 @@ class DeviceFit:
         draws = _DrawStream(rng, self.F, self.K)
         D = self.D
         p = 0
+        if phase_every == 1:
+            phase_times = True
         if phase_times:
             profile_every, profile_mode = 1, 1
+        elif phase_every > 1:
+            profile_every, profile_mode = phase_every, 1
         set_profile(0)
         self.enqueue_grow_window(draws.window(0, 2 * D), 0, None)
         for r in range(num_rounds):
@@ -449,7 +459,7 @@ class DeviceFit:
                 set_profile(r + 1)
                 self.enqueue_grow_window(draws.window(p, 2 * D), slot ^ 1, slot)
             log = self.read_slot(slot)
-            if phase_times:
+            if phase_times or (phase_every > 1 and r % phase_every == 0):
                 log.phase_ms = self.read_phase_ms()[0]
             p += log.depths_drawn
             draws.release(p)
@@ -559,13 +569,16 @@ def tree_arrays_from_log(log: RoundLog, cfg: PackBoostConfig, num_rows: int) -> 
 
 
 def depth_log_from_round(log: RoundLog, d: int, cfg: PackBoostConfig, k: int,
-                         histogram_mode: str) -> dict:
+                         histogram_mode: str, phase: tuple[np.ndarray, int] | None = None) -> dict:
     """Per-depth instrumentation in the reference's key set (booster.py:220-270, 565-579).
 
-    The *_ms fields are GPU times from the library's phase events when the round was timed
-    (log.phase_ms): hist_ms the histogram kernel, which also forms the prefix scan (so scan_ms
-    stays 0.0), score_ms the DES scorer plus the decision step, partition_ms the partition.
-    Untimed rounds report 0.0, as timing costs the pipelined loop its overlap.
+    The *_ms fields are GPU times from the library's phase events (HIP events on the fit's
+    stream around each launch): hist_ms the histogram kernel, which also forms the prefix scan
+    (scan_ms is therefore 0.0 and `scan_fused` says so), score_ms the DES scorer plus the
+    decision step, partition_ms the partition. `phase` = (phase_ms [4][D], round) gives the
+    times and the 1-based round they were measured on: the round itself when it was timed
+    (log.phase_ms), else the last timed round that reached this depth (`phase_ms_round` names
+    it); None when no timed round has reached the depth, and then the *_ms fields are None.
     One frontier serves the pack's B identical trees: the reference's shard dedup collapses
     B - 1 of every B shards (nodes_collapsed) and processes the rest."""
     ua = int(log.u_active[d])
@@ -573,21 +586,25 @@ def depth_log_from_round(log: RoundLog, d: int, cfg: PackBoostConfig, k: int,
     rows = int(recs["node_count"].astype(np.int64).sum()) if ua else 0
     B = int(cfg.pack_size)
     rebuild = histogram_mode == "rebuild"
-    ph_hist = ph_score = ph_part = 0.0
-    if log.phase_ms is not None and ua:
-        ph_hist = float(log.phase_ms[0, d])
-        ph_score = float(log.phase_ms[1, d] + log.phase_ms[2, d])
-        ph_part = float(log.phase_ms[3, d])
+    ph_hist = ph_score = ph_part = ph_scan = None
+    src = None
+    if phase is not None and ua:
+        ms, src = phase
+        ph_hist = float(ms[0, d])
+        ph_score = float(ms[1, d] + ms[2, d])
+        ph_part = float(ms[3, d])
+        ph_scan = 0.0
     out = {
         "nodes_processed": ua, "nodes_skipped": 0, "rows_total": rows,
         "feature_blocks": 1 if ua else 0, "bincount_calls": 2 if ua else 0,
-        "hist_ms": ph_hist, "scan_ms": 0.0, "score_ms": ph_score, "partition_ms": ph_part,
+        "hist_ms": ph_hist, "scan_ms": ph_scan, "score_ms": ph_score, "partition_ms": ph_part,
         "nodes_subtract_ok": 0 if rebuild else ua, "nodes_rebuild": ua if rebuild else 0,
         "nodes_subtract_fallback": 0, "nodes_collapsed": (B - 1) * ua,
         "feature_block_size": k, "depth": d, "feature_subset_size": k, "pack_size": B,
         "layer_feature_fraction": float(cfg.layer_feature_fraction),
         "histogram_mode": histogram_mode, "seed": cfg.random_state,
         "torch_threads": torch.get_num_threads(),
+        "phase_ms_round": src, "scan_fused": True,
     }
     return out
 

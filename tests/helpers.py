@@ -328,3 +328,112 @@ def assert_near_tie(oracle_mod, bins, got, want, depth_traces, kw):
             print(f"[fit parity] near-tie at node {nid}: {s_dev} vs {best}", flush=True)
             return
     raise AssertionError("trees differ outside the traced depths")
+
+
+# ------------------------------------------------------------------ whole-round fixtures
+class _EraRows:
+    """nodes_era_rows of one traced depth, built on demand (only a near-tie check reads it):
+    per frontier node, its rows per era in ascending order."""
+
+    def __init__(self, node_at_depth: np.ndarray, node_ids, era: np.ndarray, E: int):
+        self.node_at_depth, self.node_ids, self.era, self.E = node_at_depth, node_ids, era, E
+
+    def __getitem__(self, m: int):
+        rows = np.nonzero(self.node_at_depth == int(self.node_ids[m]))[0].astype(np.int64)
+        cuts = np.searchsorted(self.era[rows], np.arange(self.E + 1))
+        return [rows[cuts[e]:cuts[e + 1]] for e in range(self.E)]
+
+
+class _Scores:
+    def __init__(self, score: np.ndarray):
+        self.score = score
+
+
+def node_at_depth(tree: dict, bins: np.ndarray, d: int) -> np.ndarray:
+    """The tree node each row sits in after d levels of the bin <= threshold walk."""
+    node = np.zeros(bins.shape[0], dtype=np.int64)
+    for _ in range(d):
+        inner = np.nonzero(~np.asarray(tree["is_leaf"], bool)[node])[0]
+        if inner.size == 0:
+            break
+        nd = node[inner]
+        go_left = bins[inner, tree["feature"][nd]] <= tree["threshold"][nd]
+        node[inner] = np.where(go_left, tree["left"][nd], tree["right"][nd])
+    return node
+
+
+def fixture_fit_parity(oracle_mod, name: str, fit_rounds) -> int:
+    """A HIP fit against tests/golden/<name>_rounds.npz (tests/golden/make_rounds_golden.py).
+
+    fit_rounds(n) fits the workload's first n rounds on the device and returns the PackBoost
+    model. The oracle's trace is rebuilt from the fixture: the predictions entering each round
+    from its trees (oracle.replay_preds arithmetic, checked against the fixture's prediction
+    sums and samples bit for bit), frontier node ids, subsets and best scores per depth, and
+    each node's era row lists on demand. Then:
+      * compare_fit_rounds: trees identical, or at the first differing node a near-tie (the
+        oracle's score of the device's split on that node's rows within 1e-6 of its best),
+        where the trajectories part; node values within 1e-5;
+      * the depth logs of the matched rounds: frontier size and row count per depth, exact;
+      * training predictions after the matched rounds within 1e-5 (plus the value bars carried
+        through the pack sums) of the oracle's (a second, shorter device fit when the
+        trajectories part early).
+    Returns the number of rounds compared whole (at least 1)."""
+    from pathlib import Path
+
+    from tests.golden.make_rounds_golden import case_data, sample_rows
+
+    path = Path(__file__).resolve().parent / "golden" / f"{name}_rounds.npz"
+    with np.load(path, allow_pickle=False) as z:
+        fx = {k: z[k] for k in z.files}
+    R = int(fx["rounds"][0])
+    keys = ("feature", "threshold", "left", "right", "value", "is_leaf")
+    want = [{k: fx[f"r{r}_{k}"] for k in keys} for r in range(R)]
+    print(f"[{name} fixture] generating the workload ({R} fixture rounds)", flush=True)
+    X, bins, y, era, cfg = case_data(name)
+    E = int(era.max()) + 1
+    samp = sample_rows(bins.shape[0])
+    B, lr = int(cfg["pack_size"]), float(cfg["learning_rate"])
+    trace, after = [], []
+    preds = np.zeros(bins.shape[0], dtype=np.float32)
+    for r in range(R):
+        grad = (preds - y).astype(np.float32)
+        d = 0
+        while f"r{r}_d{d}_nodes" in fx:
+            nodes = fx[f"r{r}_d{d}_nodes"]
+            trace.append({"round": r, "depth": d, "node_ids": nodes, "feats": fx[f"r{r}_d{d}_feats"],
+                          "grad": grad, "result": _Scores(fx[f"r{r}_d{d}_score"]),
+                          "nodes_era_rows": _EraRows(node_at_depth(want[r], bins, d), nodes, era, E)})
+            d += 1
+        leaf_val = want[r]["value"].astype(np.float32)[oracle_mod.leaf_index(want[r], bins)]
+        preds = oracle_mod.pack_update(preds, leaf_val, B, np.float32(lr))
+        assert float(preds.astype(np.float64).sum()) == float(fx[f"r{r}_preds_sum"][0]), f"replay {r}"
+        if f"r{r}_preds_sample" in fx:
+            np.testing.assert_array_equal(preds[samp], fx[f"r{r}_preds_sample"], err_msg=f"replay {r}")
+        after.append(preds)
+    print(f"[{name} fixture] HIP fit", flush=True)
+    model = fit_rounds(R)
+    got = model._rounds
+    assert len(got) == R
+
+    class Ref:
+        rounds = want
+
+    matched, pred_bar = compare_fit_rounds(oracle_mod, got, Ref, trace, bins, dict(cfg))
+    print(f"[{name} fixture] {matched} of {R} rounds identical", flush=True)
+    assert matched >= 1, "the device and the oracle part (at a near-tie) in the first round"
+    logs = iter(model._depth_logs)
+    for t in trace:
+        if t["round"] >= matched:
+            break
+        dl = next(logs)
+        assert (dl["depth"], dl["nodes_processed"]) == (t["depth"], len(t["node_ids"]))
+        assert dl["rows_total"] == int(fx[f"r{t['round']}_d{t['depth']}_rows"].sum())
+    dev_model = model if matched == R else fit_rounds(matched)
+    ref = after[matched - 1].astype(np.float64)
+    bar = np.maximum(1e-5, pred_bar + matched * (B + 1) * 6e-8 * np.abs(ref))
+    dev = dev_model._train_preds.cpu().numpy().astype(np.float64)
+    diff = np.abs(dev - ref)
+    print(f"[{name} fixture] training predictions after {matched} rounds: max diff {diff.max():.3g}, "
+          f"{int(np.sum(diff > 1e-5))} rows beyond 1e-5", flush=True)
+    assert np.all(diff <= bar)
+    return matched

@@ -87,3 +87,51 @@ def test_early_stop_case_stops_early():
     # a round whose leaves all sit above depth D drew fewer than D subsets; later rounds
     # then depend on the rewound generator
     assert any(x < D for x in deepest[:-1]), deepest
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_leaf_index_matches_predict_tree(oracle_mod, name):
+    """oracle.leaf_index (the checker of the device's leaf indices) against the tree walk that
+    the reference goldens pin through predict(): every row lands on a leaf, and that leaf's
+    float32 value is Tree.predict_bins' output (booster.py:131-169)."""
+    d = load_case(name)
+    for r, tree in enumerate(d["trees"]):
+        idx = oracle_mod.leaf_index(tree, d["bins"])
+        assert np.all(tree["is_leaf"][idx]), f"round {r}: a row ends on an internal node"
+        np.testing.assert_array_equal(tree["value"].astype(np.float32)[idx],
+                                      oracle_mod.predict_tree(tree, d["bins"]), err_msg=f"round {r}")
+    # a hand-made tree: node 0 splits feature 1 at 2, node 2 splits feature 0 at 0
+    tree = {"feature": np.array([1, -1, 0, -1, -1]), "threshold": np.array([2, 0, 0, 0, 0]),
+            "left": np.array([1, -1, 3, -1, -1]), "right": np.array([2, -1, 4, -1, -1]),
+            "value": np.array([0.0, 1.0, 0.0, 2.0, 3.0]), "is_leaf": np.array([0, 1, 0, 1, 1], bool)}
+    bins = np.array([[0, 2], [0, 3], [1, 3], [5, 0], [0, 9]], dtype=np.uint8)
+    np.testing.assert_array_equal(oracle_mod.leaf_index(tree, bins), [1, 3, 4, 1, 3])
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_replay_preds_matches_fit(oracle_mod, name):
+    """oracle.replay_preds (training predictions recomputed from trees alone, the checker of
+    the full-size config-3 test) equals the fit loop's own predictions bit for bit, and a fit
+    continued from init_preds with the same generator grows the same trees as one call."""
+    import torch
+
+    d = load_case(name)
+    cfg = dict(d["config"])
+    codes = era_codes(d["era"])
+    res = oracle_mod.fit(d["bins"], d["y"], codes, num_rounds=d["rounds"], **cfg)
+    rep = oracle_mod.replay_preds(res.rounds, d["bins"], cfg["pack_size"], cfg["learning_rate"])
+    np.testing.assert_array_equal(rep, res.preds)
+    rows = np.arange(0, d["bins"].shape[0], 7)
+    np.testing.assert_array_equal(
+        oracle_mod.replay_preds(res.rounds, d["bins"], cfg["pack_size"], cfg["learning_rate"], rows=rows),
+        res.preds[rows])
+    seed = cfg.pop("random_state")
+    rng = torch.Generator().manual_seed(seed)
+    half = d["rounds"] // 2
+    a = oracle_mod.fit(d["bins"], d["y"], codes, num_rounds=half, rng=rng, **cfg)
+    b = oracle_mod.fit(d["bins"], d["y"], codes, num_rounds=d["rounds"] - half, rng=rng,
+                       init_preds=a.preds, **cfg)
+    for r, (got, want) in enumerate(zip(a.rounds + b.rounds, d["trees"])):
+        for key in ("feature", "threshold", "left", "right", "is_leaf", "value"):
+            np.testing.assert_array_equal(np.asarray(got[key]), np.asarray(want[key]), err_msg=f"round {r} {key}")
+    np.testing.assert_array_equal(b.preds, res.preds)

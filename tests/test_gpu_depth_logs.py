@@ -4,8 +4,9 @@ The reference fills a DepthInstrumentation per depth (nodes processed / skipped 
 rows, phase milliseconds, histogram-mode counters) and its tests pin the accounting invariant
 (tests/test_packboost_parity.py:67-87). Here: the same key set, node and row counts equal to
 the oracle's restatement of the reference fit, the invariant in all three histogram modes, and
-phase times that are measured (not placeholders) when phase timing is on, without changing
-the fit.
+phase times that are measured in a default fit (every 8th round timed, the others carrying the
+last timed round's values and naming it) and in every round with phase timing on, without
+changing the fit.
 """
 
 from __future__ import annotations
@@ -22,6 +23,9 @@ REFERENCE_KEYS = {
     "feature_subset_size", "pack_size", "layer_feature_fraction", "histogram_mode", "seed",
     "torch_threads",
 }
+# keys this build adds: the round the *_ms values were measured on, and that the prefix scan is
+# timed inside hist_ms
+EXTRA_KEYS = {"phase_ms_round", "scan_fused"}
 
 
 def _dataset(seed=123, n_rows=320, n_features=12, n_eras=8):
@@ -49,7 +53,7 @@ def test_depth_log_accounting(hip, oracle_mod, hist_mode):
     logs = booster._depth_logs
     assert logs
     for dl in logs:
-        assert set(dl) == REFERENCE_KEYS
+        assert set(dl) == REFERENCE_KEYS | EXTRA_KEYS
         n = dl["nodes_processed"]
         assert dl["nodes_subtract_ok"] + dl["nodes_rebuild"] == n
         if hist_mode == "rebuild":
@@ -58,7 +62,10 @@ def test_depth_log_accounting(hip, oracle_mod, hist_mode):
             assert dl["nodes_subtract_ok"] >= 0
             assert dl["nodes_subtract_fallback"] <= dl["nodes_rebuild"]
         assert dl["histogram_mode"] == hist_mode
-        assert dl["scan_ms"] == 0.0 and dl["hist_ms"] == 0.0  # phase timing off
+        # a default fit times round 1 (then every 8th): both rounds report round 1's times
+        assert dl["phase_ms_round"] == 1
+        assert dl["hist_ms"] > 0.0 and dl["score_ms"] > 0.0 and dl["partition_ms"] > 0.0
+        assert dl["scan_ms"] == 0.0 and dl["scan_fused"]
     bins = preprocess_features(X, 63).bins
     codes = encode_eras(eras, X.shape[0])[0].astype(np.int64)
     ref = oracle_mod.fit(bins, y, codes, num_rounds=2, **kw)
@@ -85,6 +92,16 @@ def test_depth_log_phase_times(hip):
             assert a[key] == b[key]
         assert a["hist_ms"] > 0.0 and a["score_ms"] > 0.0 and a["partition_ms"] > 0.0
         assert a["scan_ms"] == 0.0  # the prefix scan is part of the histogram kernel
+    # every round timed: each log names its own round; the default fit times rounds 1 and 9
+    # here only round 1 (3 rounds), and the later rounds carry its values
+    per_round = {}
+    for a in timed._depth_logs:
+        per_round.setdefault(a["phase_ms_round"], []).append(a)
+    assert sorted(per_round) == [1, 2, 3]
+    first = {b["depth"]: b for b in plain._depth_logs[: len(per_round[1])]}
+    for b in plain._depth_logs:
+        assert b["phase_ms_round"] == 1
+        assert b["hist_ms"] == first[b["depth"]]["hist_ms"]
     for ra, rb in zip(timed._rounds, plain._rounds):
         for key in ("feature", "threshold", "left", "right", "is_leaf"):
             np.testing.assert_array_equal(ra[key], rb[key])
