@@ -504,6 +504,9 @@ def main() -> int:
         "phase_ms_per_round": {k: round(v / n_phase, 4) for k, v in phase_ms.items()},
         "hist_ms_per_depth": [round(float(prof_ms[0, d]) / max(1, int(n_act[d])), 4)
                               for d in range(D)],
+        # score + decide per depth, over the replayed rounds (a depth's launches in rounds that
+        # stopped above it take no time)
+        "score_ms_per_depth": [round(float(phase_raw[1, d]) / n_phase, 4) for d in range(D)],
         "full_depth_rounds": int(sum(1 for log in logs if int(log.u_active[D - 1]) > 0)),
         "cpu_baseline": None,
     }

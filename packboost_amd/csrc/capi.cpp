@@ -53,6 +53,7 @@ struct pb_ctx {
     int32_t hist_block;  // 0: by LDS size, else 128 or 256 threads
     int32_t score_wgs;  // workgroups the producer/consumer scorer aims for
     int32_t score_staged;  // T >= 64 thresholds: LDS-staged scorer instead of the wide one
+    int32_t score_pc_classic;  // unit era weights, T <= 63: the scorer whose consumer forms 1/n
     int32_t num_cus;        // compute units of the device
     int32_t hist_resident;  // histogram: loop work items over a resident grid
     int32_t hist_rounds;
@@ -213,6 +214,7 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
     const int tmax = std::max(1, d.max_bins - 1);
     c->score_wgs = (int32_t)env_int("PB_SCORE_WGS", 768);
     c->score_staged = env_int("PB_SCORE_STAGED", 0) != 0 ? 1 : 0;
+    c->score_pc_classic = (int32_t)std::min<int64_t>(2, std::max<int64_t>(0, env_int("PB_SCORE_PC", 0)));
     c->hist_resident = (int32_t)env_int("PB_HIST_RESIDENT", 0);
     c->hist_rounds = (int32_t)env_int("PB_HIST_ROUNDS", 1);
     c->num_cus = 0;
@@ -581,6 +583,7 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     a.wpt = sh.wpt;
     a.rt = sh.rt;
     a.staged = c->score_staged;
+    a.pc_classic = c->score_pc_classic;
     a.seq = c->seq;
     c->last_w = sh.ntiles * sh.wpt;
     c->last_K = K;

@@ -215,6 +215,9 @@ struct ScoreArgs {
     int32_t wpt;             // wavefront winners per tile (ceil(fts * T / 64))
     int32_t rt;              // size of the 1/n table (equal era weights)
     int32_t staged;          // T >= 64: 1 = LDS-staged two-phase kernel, 0 = wide kernel
+    int32_t pc_classic;      // T <= 63 with unit era weights (PB_SCORE_PC): 0 = des_score_pcu_kernel
+                             // for one pair per producer thread, else des_score_pc_kernel;
+                             // 1 = des_score_pc_kernel always; 2 = des_score_pcu_kernel always
     SeqCands seq;            // every candidate, for the sequential pick
 };
 

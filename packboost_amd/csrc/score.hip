@@ -24,6 +24,7 @@
 #include <algorithm>
 
 #include <type_traits>
+#include <utility>
 
 #include "pb_internal.h"
 
@@ -614,34 +615,36 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
     // always a compile-time constant): this thread's era totals, and per pair the prefix count
     // and grad. Loading two chunks ahead covers the plane loads' latency when three workgroups
     // per CU stream a deep frontier's planes.
+    // Loads without a branch (an element outside the chunk, the last era or this thread's
+    // candidates reads the chunk's first one, always in bounds, and pok[S] marks what is real:
+    // bit 0 the era total, bit 1 + i pair i), so the compiler's wait counts stay exact and the
+    // next chunk's loads stay in flight while this one is made.
     int pct[2] = {0, 0};
     float pGt[2] = {0.0f, 0.0f};
+    uint32_t pok[2] = {0u, 0u};
     int pL[2][kPcPairs];
     float pGL[2][kPcPairs];
     auto prefetch = [&](int chunk, auto set) {
         constexpr int S = decltype(set)::value;
-        const int e0 = chunk * kPcEras;
+        const bool live = chunk < nchunks;
+        const int e0 = live ? chunk * kPcEras : 0;
         const int ne = min(kPcEras, a.E - e0);
         const int64_t eoff = (int64_t)e0 * estride;
-        const bool live = chunk < nchunks;
-        pct[S] = 0;
-        pGt[S] = 0.0f;
-        if (live && slot_el[0] < ne) {  // slot 0 is valid whenever any slot of the thread is
-            const int64_t to = (int64_t)(e0 + my_el) * a.U + u;  // era total
-            pct[S] = a.tot_cnt[to];
-            pGt[S] = a.tot_g[to];
-        }
+        const bool era_ok = live && slot_el[0] < ne;  // slot 0 is valid whenever any slot is
+        const int64_t to = (int64_t)(e0 + (era_ok ? my_el : 0)) * a.U + u;  // era total
+        pct[S] = a.tot_cnt[to];
+        pGt[S] = a.tot_g[to];
+        uint32_t ok = era_ok ? 1u : 0u;
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
             if (i >= np) break;
-            pL[S][i] = 0;
-            pGL[S][i] = 0.0f;
-            if (live && slot_el[i] < ne) {
-                const int64_t off = eoff + slot_off[i];
-                pL[S][i] = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
-                pGL[S][i] = a.g[off];
-            }
+            const bool pair_ok = live && slot_el[i] < ne;
+            const int64_t off = eoff + (pair_ok ? slot_off[i] : 0);
+            pL[S][i] = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
+            pGL[S][i] = a.g[off];
+            ok |= pair_ok ? (2u << i) : 0u;
         }
+        pok[S] = ok;
     };
     // Branch-free per pair (the same float operations as the reference, evaluated for every
     // pair and selected), so the divide sequences of all pairs interleave. The parent term
@@ -649,9 +652,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
     auto produce = [&](int chunk, auto set) {
         constexpr int S = decltype(set)::value;
         float4* buf = ring + (chunk & 1) * kPcEras * kWave;
-        const int ctot = pct[S];
+        const uint32_t ok = pok[S];
+        const int ctot = (ok & 1u) ? pct[S] : 0;
         const bool has = ctot != 0;
-        const float Gt = pGt[S];
+        const float Gt = (ok & 1u) ? pGt[S] : 0.0f;
         const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
         const float pden = (float)ctot + lam;
         const float pq = (0.5f * (Gt * Gt)) / pden;
@@ -659,8 +663,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
             if (i >= np) break;
-            const int Lc = pL[S][i];
-            const float GLc = pGL[S][i];
+            const bool pair_ok = (ok >> (i + 1)) & 1u;
+            const int Lc = pair_ok ? pL[S][i] : 0;
+            const float GLc = pair_ok ? pGL[S][i] : 0.0f;
             const int R = ctot - Lc;
             const float GR = Gt - GLc;
             const float w = (has && Lc > 0 && R > 0) ? wera : 0.0f;
@@ -851,6 +856,327 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
             c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
             if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
         store_seq(a, ((int64_t)u * a.K + k) * T + t, c);
+            if (tile == 0 && tid == 0) {
+                a.ntot[u].count = tc;
+                a.ntot[u].grad = tg;
+            }
+        }
+        const float mine = c.valid ? c.score : -INFINITY;
+#pragma unroll
+        for (int m = 1; m < kWave; m <<= 1) {
+            const Cand o = shfl_xor_cand(c, m);
+            take_if(better(o, c), o, c);
+        }
+        const int band = wave_band_count(c, mine);
+        if (tid == 0) store_winner(a.cand_w + (int64_t)u * a.ntiles + tile, c, band);
+    }
+}
+
+// f(std::integral_constant<int, 0>{}), ..., f(std::integral_constant<int, N - 1>{}), in order
+template <typename F, int... J>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Producer/consumer scorer for unit era weights (era_alpha <= 0) without the direction term,
+// T <= 63: the layout and the producers' gain math of des_score_pc_kernel, with the work that
+// does not depend on the era chain taken off the consumer wave. With unit weights the Welford
+// factor w / wsum is 1 / n, n the candidate's count of valid eras so far: the producers count
+// them (per chunk, one bit per (candidate, era) in an LDS mask, then a popcount below the
+// era's bit plus the count of the earlier chunks) and read the IEEE 1/n (the table of
+// des_score_pc_kernel) into the record, 0 for an era that is not valid; the left counts (an
+// integer sum, order-free) are added up in LDS by the producers. A record is (gain, left
+// grad, factor, weight 1 or 0), and per era the consumer runs
+//     lg = lg + GL;  delta = gain - mean;  mean' = mean + f * delta;
+//     M2 = M2 + (w * delta) * (gain - mean');  mean = mean'
+// which is the reference's recurrence (frontier_cpu.cpp:376-393) bit for bit: for a valid era
+// f = 1/n and w * delta == delta; an invalid era has f = +0 and w = +0 (and gain = +0), so
+// mean + (+-0) == mean and M2 + (+-0) == M2 exactly (mean is never -0: it starts at +0 and an
+// IEEE sum is -0 only when both terms are), which is the reference's `continue`. Eight VALU
+// operations per era and no LDS lookup on the chain, where des_score_pc_kernel takes about
+// fifteen. The producers run two chunks ahead of the consumer (a chunk's masks are complete
+// one barrier after its gains), still one barrier per chunk.
+// NP: the most (candidate, era) pairs a producer thread holds (ceil(candidates / 8)); PF: the
+// chunks whose plane values are in flight in the producers' registers. A workgroup with few
+// candidates (a shallow depth: one feature of four thresholds) has the registers for a deep
+// prefetch, and needs it: each chunk's loads then carry little work to hide their latency.
+template <bool C32, int NP, int PF>
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) void des_score_pcu_kernel(ScoreArgs a) {
+    extern __shared__ unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int u = blockIdx.x / a.ntiles;
+    const int tile = blockIdx.x - u * a.ntiles;
+    const int Ua = a.st->u_active[a.depth];
+    if (u >= Ua) return;
+    const int k0 = tile * a.fts;
+    const int nf = min(a.fts, a.K - k0);
+    if (nf <= 0) return;
+    const int T = a.T;
+    const int nb = a.nb;
+    const int ncand = nf * T;  // <= 63; lane 63 carries the node totals
+    const int RT = a.rt;
+
+    float* recip = reinterpret_cast<float*>(smem);
+    float4* ring = reinterpret_cast<float4*>(recip + ((RT + 3) & ~3));  // [2][kPcEras][64]
+    uint32_t* vmask = reinterpret_cast<uint32_t*>(ring + 2 * kPcEras * kWave);  // [3][64]
+    int32_t* vbase = reinterpret_cast<int32_t*>(vmask + 3 * kWave);            // [2][64]
+    int32_t* ltsum = vbase + 2 * kWave;                                         // [64]
+    static_assert(kPcEras == 3 * 8, "one byte of a 32-bit mask per producer wave");
+
+    for (int i = tid; i < RT; i += kBlock) recip[i] = (i == 0) ? 0.0f : 1.0f / (float)i;
+    for (int i = tid; i < 3 * kWave; i += kBlock) vbase[i] = 0;  // counts, left sums
+
+    const float lam = a.lambda_l2;
+    const int pt = nb - 1;
+    const int64_t ustride = (int64_t)a.K * pt;
+    const int64_t estride = (int64_t)a.U * ustride;
+    const int64_t node_off = (int64_t)u * ustride;
+    const int nchunks = (a.E + kPcEras - 1) / kPcEras;
+    const bool consumer = tid < kWave;
+    const int ptid = tid - kWave;
+
+    // the producer slots of des_score_pc_kernel: thread -> one era of each chunk; slot i holds
+    // candidate c0 + 8 i, and bit i of slot_ok says it is a candidate of this workgroup
+    const int np = min(NP, (ncand + kPcThreadsPerEra - 1) / kPcThreadsPerEra);
+    const int my_el = ptid / kPcThreadsPerEra;
+    const uint32_t below = (1u << (consumer ? 0 : my_el)) - 1u;  // mask bits of earlier eras
+    const int c0 = ptid % kPcThreadsPerEra;
+    uint32_t slot_ok = 0u;
+    int32_t slot_off[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int c = c0 + kPcThreadsPerEra * i;
+        const int cc = min(c, ncand - 1);
+        const int kk = cc / T;
+        const int t = cc - kk * T;
+        const int k = k0 + kk;
+        slot_ok |= (ptid >= 0 && c < ncand) ? (1u << i) : 0u;
+        const int thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
+        slot_off[i] = (int32_t)((int64_t)my_el * estride + node_off + (int64_t)k * pt + thr);
+    }
+
+    // Register set S: the era total and per pair the prefix count and grad of one chunk, read
+    // without a branch (a chunk past the end, an era past the last one or a slot without a
+    // candidate reads the chunk's first elements, always in bounds) so that the compiler's
+    // wait counts stay exact and the loads of later chunks stay in flight; bit 0 of pok[S]
+    // says the era total is real, bit 1 + i that pair i is.
+    int pct[PF];
+    float pGt[PF];
+    uint32_t pok[PF];
+    int pL[PF][NP];
+    float pGL[PF][NP];
+    auto prefetch = [&](int chunk, auto set) {
+        constexpr int S = decltype(set)::value;
+        const bool live = chunk < nchunks;
+        const int e0 = live ? chunk * kPcEras : 0;
+        const int ne = min(kPcEras, a.E - e0);
+        const bool era_ok = live && (slot_ok & 1u) && my_el < ne;
+        const int64_t eoff = (int64_t)e0 * estride;
+        const uint16_t* cb = a.cnt + eoff;
+        const uint32_t* cb32 = a.cnt32 + eoff;
+        const float* gb = a.g + eoff;
+        const int64_t to = (int64_t)(e0 + (era_ok ? my_el : 0)) * a.U + u;
+        pct[S] = a.tot_cnt[to];
+        pGt[S] = a.tot_g[to];
+        uint32_t ok = era_ok ? 1u : 0u;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const bool pair_ok = era_ok && ((slot_ok >> i) & 1u);
+            const uint32_t o = pair_ok ? (uint32_t)slot_off[i] : 0u;
+            pL[S][i] = C32 ? (int)cb32[o] : (int)cb[o];
+            pGL[S][i] = gb[o];
+            ok |= pair_ok ? (2u << i) : 0u;
+        }
+        pok[S] = ok;
+    };
+    // Two producer phases per chunk, one interval apart. Phase 1 (chunk c): gains (the
+    // reference's float operations, branch-free) and left grads kept in registers, and the
+    // validity of every (candidate, era) pair as a mask: a producer wave holds 8 eras of the
+    // chunk (lane = 8 * era + c0), so a ballot over its lanes gathers, per candidate, the byte
+    // of its 8 eras, which the wave's era-0 lanes store as byte (wave - 1) of the candidate's
+    // 24-bit mask in buffer c % 3 (no atomics; every byte of the mask is rewritten each time).
+    // Left counts and the node's rows are summed in registers, into LDS once at the end.
+    // Phase 2 (chunk c, the next interval, when its mask is complete): each valid era's 1/n,
+    // the whole record into ring buffer c % 2, and the count base of chunk c + 1.
+    float hg[NP], hgl[NP];
+    int lt_reg[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) lt_reg[i] = 0;
+    int ct_reg = 0;
+    uint32_t hv = 0u;  // bit i: slot i's era is valid
+    float hgt = 0.0f;  // the era's grad total (the lane-63 record)
+    const int wbyte = (tid / kWave) - 1;  // producer wave 1-3: byte 0-2 of a mask
+    const int lane = tid & (kWave - 1);
+    auto produce1 = [&](int chunk, auto set) {
+        constexpr int S = decltype(set)::value;
+        const uint32_t ok = pok[S];
+        const int ctot = (ok & 1u) ? pct[S] : 0;
+        const bool has = ctot != 0;
+        ct_reg += (c0 == 0 && (slot_ok & 1u)) ? ctot : 0;  // the node's rows, once per era
+        const float Gt = (ok & 1u) ? pGt[S] : 0.0f;
+        const float pden = (float)ctot + lam;
+        const float pq = (0.5f * (Gt * Gt)) / pden;
+        const float parent = (pden > 0.0f) ? pq : 0.0f;
+        uint8_t* mskb = reinterpret_cast<uint8_t*>(vmask + (chunk % 3) * kWave);
+        hv = 0u;
+        hgt = has ? Gt : 0.0f;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            if (i >= np) break;
+            const bool pair_ok = (ok >> (i + 1)) & 1u;
+            const int Lc = pair_ok ? pL[S][i] : 0;
+            const float GLc = pair_ok ? pGL[S][i] : 0.0f;
+            const int R = ctot - Lc;
+            const float GR = Gt - GLc;
+            const bool act = has && Lc > 0 && R > 0;
+            const float dL = (float)Lc + lam;
+            const float dR = (float)R + lam;
+            const float gfull = 0.5f * ((GLc * GLc) / dL + (GR * GR) / dR) - parent;
+            const int c = c0 + kPcThreadsPerEra * i;
+            const bool valid = (slot_ok >> i) & 1u;
+            hg[i] = act ? gfull : 0.0f;
+            hgl[i] = has ? GLc : 0.0f;
+            hv |= act ? (1u << i) : 0u;
+            lt_reg[i] += (valid && has) ? Lc : 0;
+            // bits c0 + 8 k of the ballot: era 8 (wave - 1) + k of candidate c
+            const unsigned long long bal = __ballot(valid && act);
+            const unsigned long long x = (bal >> c0) & 0x0101010101010101ull;
+            if (lane < kPcThreadsPerEra && valid)
+                mskb[c * 4 + wbyte] = (uint8_t)((x * 0x0102040810204080ull) >> 56);
+        }
+    };
+    auto produce2 = [&](int chunk) {
+        float4* buf = ring + (chunk & 1) * kPcEras * kWave;
+        const uint32_t* msk = vmask + (chunk % 3) * kWave;
+        const int32_t* base = vbase + (chunk & 1) * kWave;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            if (i >= np) break;
+            const int c = c0 + kPcThreadsPerEra * i;
+            if ((slot_ok >> i) & 1u) {
+                const uint32_t m = msk[c] & 0x00FFFFFFu;  // bytes 0-2: the three producer waves
+                const int b = base[c];
+                const int n = b + __popc(m & below) + 1;
+                const bool v = (hv >> i) & 1u;
+                buf[my_el * kWave + c] = make_float4(hg[i], hgl[i], v ? recip[n] : 0.0f, v ? 1.0f : 0.0f);
+                // lane 63 pseudo-candidate: its left grad sum becomes the node's float32
+                // era-order grad total
+                if (c == 0) buf[my_el * kWave + (kWave - 1)] = make_float4(0.0f, hgt, 0.0f, 0.0f);
+                if (my_el == 0) vbase[((chunk + 1) & 1) * kWave + c] = b + __popc(m);
+            }
+        }
+    };
+
+    float mean = 0.0f, M2 = 0.0f, lg = 0.0f;
+    const bool owner = tid < ncand;
+    // one chunk's eras in batches of 8 (records of the next batch read while this one runs)
+    auto consume = [&](int chunk) {
+        const float4* buf = ring + (chunk & 1) * kPcEras * kWave;
+        static_assert(kPcEras % 8 == 0, "batches of 8 eras must tile a chunk");
+        constexpr int kBatches = kPcEras / 8;
+        float4 rec[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rec[j] = buf[j * kWave + tid];
+#pragma unroll
+        for (int bi = 0; bi < kBatches; ++bi) {
+            float4 nxt[8];
+            if (bi + 1 < kBatches) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) nxt[j] = buf[((bi + 1) * 8 + j) * kWave + tid];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                lg = lg + rec[j].y;
+                const float gain = rec[j].x;
+                const float delta = gain - mean;
+                const float mean_n = mean + rec[j].z * delta;
+                M2 = M2 + (rec[j].w * delta) * (gain - mean_n);
+                mean = mean_n;
+            }
+            if (bi + 1 < kBatches) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) rec[j] = nxt[j];
+            }
+        }
+    };
+    // One barrier per chunk: in the interval of chunk ch the consumer runs ch while the
+    // producers finish ch + 1 (phase 2), start ch + 2 (phase 1, its plane values from register
+    // set (ch + 2) % PF) and load ch + 2 + PF into that set. Before it: the first PF chunks'
+    // loads, chunk 0's two phases and chunk 1's phase 1 (three barriers both roles pass). The
+    // producers' loop runs a whole multiple of PF intervals with no branch in it (chunks past
+    // the last one load in-bounds elements marked invalid, so their phases add nothing), which
+    // keeps the compiler's load wait counts exact: each chunk waits for its own loads only.
+    const int nint = (nchunks + PF - 1) / PF * PF;
+    if (!consumer) {
+        static_for<PF>([&](auto j) { prefetch(decltype(j)::value, j); });
+        __syncthreads();  // the LDS arrays are initialised
+        produce1(0, std::integral_constant<int, 0>{});
+        prefetch(PF, std::integral_constant<int, 0>{});
+        __syncthreads();  // chunk 0's masks are complete
+        produce2(0);
+        produce1(1, std::integral_constant<int, 1 % PF>{});
+        prefetch(PF + 1, std::integral_constant<int, 1 % PF>{});
+    } else {
+        __syncthreads();
+        __syncthreads();
+    }
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(consumer ? 1 : 0) != 0) {
+        // every lane of the consumer wave runs the chain (lanes past the candidates read
+        // records that were never written and store nothing)
+        for (int ch = 0; ch < nint; ++ch) {
+            if (ch < nchunks) consume(ch);
+            __syncthreads();
+        }
+    } else {
+        for (int ch = 0; ch < nint; ch += PF) {
+            static_for<PF>([&](auto j) {  // interval ch + J; set (J + 2) % PF == (ch + J + 2) % PF
+                constexpr int J = decltype(j)::value;
+                produce2(ch + J + 1);
+                produce1(ch + J + 2, std::integral_constant<int, (J + 2) % PF>{});
+                prefetch(ch + J + 2 + PF, std::integral_constant<int, (J + 2) % PF>{});
+                __syncthreads();
+            });
+        }
+        // left counts of every candidate and the node's rows, exact integer sums
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+            if (i < np && ((slot_ok >> i) & 1u)) atomicAdd(ltsum + c0 + kPcThreadsPerEra * i, lt_reg[i]);
+        if (c0 == 0) atomicAdd(ltsum + (kWave - 1), ct_reg);
+    }
+    __syncthreads();
+
+    if (consumer) {
+        const int lt = ltsum[tid];
+        const int tc = ltsum[kWave - 1];
+        const float tg = __shfl(lg, kWave - 1);
+        const float wsum = (float)vbase[(nchunks & 1) * kWave + (owner ? tid : 0)];  // valid eras
+        Cand c;
+        c.lt = lt;
+        c.lg = lg;
+        c.valid = 0;
+        c.score = 0.0f;
+        c.f = -1;
+        c.thr = -1;
+        if (owner) {
+            const int kk = tid / T;
+            const int t = tid - kk * T;
+            const int k = k0 + kk;
+            c.f = a.feats[k];
+            c.thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
+            const int rt = tc - lt;
+            const float ws = (wsum < 1e-12f) ? 1e-12f : wsum;
+            const float var = M2 / ws;
+            const float sd = sqrtf((0.0f < var) ? var : 0.0f);
+            const float score = mean - a.lambda_dro * sd;
+            c.score = score;
+            c.valid = (tc > 0 && lt >= a.msl && rt >= a.msl && !isnan(score)) ? 1 : 0;
+            if (a.cand_all) store_cand(a.cand_all + ((int64_t)u * a.K + k) * T + t, c);
+            store_seq(a, ((int64_t)u * a.K + k) * T + t, c);
             if (tile == 0 && tid == 0) {
                 a.ntot[u].count = tc;
                 a.ntot[u].grad = tg;
@@ -1572,7 +1898,8 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
         sh.ntiles = (K + sh.fts - 1) / sh.fts;
         sh.wpt = 1;
         sh.ec = kPcEras;
-        sh.lds_bytes = (size_t)((sh.rt + 3) & ~3) * 4 + 2 * (size_t)kPcEras * kWave * 16;
+        // table, record ring, then (unit-weight kernel) the valid-era masks, counts and left sums
+        sh.lds_bytes = (size_t)((sh.rt + 3) & ~3) * 4 + 2 * (size_t)kPcEras * kWave * 16 + 6 * kWave * 4;
         return sh;
     }
     // many thresholds per feature (nb > 65): one feature per workgroup, all threads alternate
@@ -1586,26 +1913,41 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
     return sh;
 }
 
-template <bool C32>
-hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
-    const bool wide = a.T >= kWave && !a.staged;
-    if (wide) lds_bytes = 0;  // the wide scorer computes 1/n (exact_recip) instead of a table
-    const void* fn = (a.T < kWave) ? reinterpret_cast<const void*>(&des_score_pc_kernel<C32>)
-                     : wide        ? reinterpret_cast<const void*>(&des_score_wide_kernel<C32>)
-                                   : reinterpret_cast<const void*>(&des_score_kernel<C32>);
+// Launches kernel `fn` with `lds_bytes` of dynamic LDS (raising the limit past 64 KiB first).
+template <typename K>
+hipError_t launch_lds(K fn, int grid, int block, size_t lds_bytes, hipStream_t s, const ScoreArgs& a) {
     if (lds_bytes > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)lds_bytes);
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
         if (e != hipSuccess) return e;
     }
-    if (a.T < kWave)
-        hipLaunchKernelGGL(des_score_pc_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
-    else if (wide)  // one thread per threshold: whole wavefronts up to T (T <= 254)
-        hipLaunchKernelGGL(des_score_wide_kernel<C32>, dim3(grid), dim3((a.T + kWave - 1) / kWave * kWave),
-                           lds_bytes, s, a);
-    else
-        hipLaunchKernelGGL(des_score_kernel<C32>, dim3(grid), dim3(kBlock), lds_bytes, s, a);
+    hipLaunchKernelGGL(fn, dim3(grid), dim3(block), lds_bytes, s, a);
     return hipGetLastError();
+}
+
+template <bool C32>
+hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+    if (a.T >= kWave) {
+        if (a.staged) return launch_lds(des_score_kernel<C32>, grid, kBlock, lds_bytes, s, a);
+        // the wide scorer computes 1/n (exact_recip) instead of a table; one thread per
+        // threshold, whole wavefronts up to T (T <= 254)
+        return launch_lds(des_score_wide_kernel<C32>, grid, (a.T + kWave - 1) / kWave * kWave, 0, s, a);
+    }
+    // unit era weights, no direction term, the 1/n table covering every era: the
+    // producer/consumer kernel with the factors made by the producers, its prefetch depth by
+    // the pairs per producer thread (ceil(candidates per workgroup / 8))
+    // Measured at the 2.4M x 2376 x 5-bin panel: with one pair per producer thread (4
+    // candidates per workgroup, depths 0-2) it takes 21-23 us per depth against 29-31; from
+    // two pairs on its producers' extra work outweighs the shorter chain (depth 3: 38.6
+    // against 36.8 us, depth 5: 79 against 54). PB_SCORE_PC: 0 that rule, 1 never, 2 always.
+    const bool unit = !(a.era_alpha > 0.0f) && a.dir_w == 0.0f && a.E < a.rt && a.pc_classic != 1;
+    const int np = (a.fts * a.T + kPcThreadsPerEra - 1) / kPcThreadsPerEra;
+    if (!unit || (np > 1 && a.pc_classic != 2))
+        return launch_lds(des_score_pc_kernel<C32>, grid, kBlock, lds_bytes, s, a);
+    if (np <= 1) return launch_lds(des_score_pcu_kernel<C32, 1, 6>, grid, kBlock, lds_bytes, s, a);
+    if (np <= 2) return launch_lds(des_score_pcu_kernel<C32, 2, 4>, grid, kBlock, lds_bytes, s, a);
+    if (np <= 4) return launch_lds(des_score_pcu_kernel<C32, 4, 3>, grid, kBlock, lds_bytes, s, a);
+    return launch_lds(des_score_pcu_kernel<C32, 8, 2>, grid, kBlock, lds_bytes, s, a);
 }
 
 hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {

@@ -7,7 +7,7 @@ workload at its full size, for the GPU tests that compare the HIP fit round by r
            B 8, D 5 (its 100 rounds).
 
 Each workload is a pure function of a NumPy seed (`case_data()`), so the GPU tests regenerate
-it on the box and only the oracle's outputs are committed. The oracle is the restated fit loop
+it on the box and only the oracle's outputs are committed (`load_fixture()` reads them back). The oracle is the restated fit loop
 (oracle.fit, booster.py:375-599) with each depth's split finder run by the reference's own
 compiled frontier (frontier_cpu.cpp:111-515 via oracle/_ref) when it is built here, else by the
 C restatement; the two are bit-identical (tests/test_oracle_reference.py). Per round it records:
@@ -15,7 +15,7 @@ C restatement; the two are bit-identical (tests/test_oracle_reference.py). Per r
   depths  per depth the frontier node ids, the feature subset, and per node the chosen
           (feature, threshold), the split score, the left count and the node's row count;
   preds   the float32 training predictions after the round: their float64 sum over all rows,
-          and their values at SAMPLE_ROWS seeded rows (rounds 0-4, every 10th and the last).
+          and their values at SAMPLE_ROWS seeded rows (rounds 0-4, every 25th and the last).
 
 Run in the build container (config3: about 45 s per round on 8 cores; config2: about 1 s):
 
@@ -40,7 +40,7 @@ CONFIG3 = dict(pack_size=8, max_depth=6, learning_rate=0.01, lambda_l2=1e-6, lam
 CONFIG2 = dict(pack_size=8, max_depth=5, learning_rate=0.1, max_bins=128, min_samples_leaf=20,
                random_state=42)
 ROUNDS = {"config3": 5, "config2": 100}
-SAMPLE_ROWS = 20_000
+SAMPLE_ROWS = {"config3": 20_000, "config2": 4_000}
 SEED = 42
 
 
@@ -86,9 +86,35 @@ def case_data(name: str):
     raise ValueError(name)
 
 
-def sample_rows(n: int) -> np.ndarray:
+def sample_rows(name: str, n: int) -> np.ndarray:
     rng = np.random.default_rng(SEED + 1)
-    return np.sort(rng.choice(n, min(n, SAMPLE_ROWS), replace=False))
+    return np.sort(rng.choice(n, min(n, SAMPLE_ROWS[name]), replace=False))
+
+
+def load_fixture(name: str) -> dict:
+    """tests/golden/<name>_rounds.npz as {"rounds": R, "trees": [per round dict of arrays],
+    "depths": [{"round", "depth", "nodes", "feats", "feature", "threshold", "score",
+    "left_count", "rows"} per traced depth], "preds_sum": [R], "preds_sample": {round: array}}."""
+    with np.load(HERE / f"{name}_rounds.npz", allow_pickle=False) as z:
+        f = {k: z[k] for k in z.files}
+    R = int(f["rounds"][0])
+    trees, t0 = [], 0
+    for r in range(R):
+        n = int(f["t_len"][r])
+        trees.append({k: f[f"t_{k}"][t0:t0 + n] for k in
+                      ("feature", "threshold", "left", "right", "value", "is_leaf")})
+        t0 += n
+    depths, d0 = [], 0
+    for i in range(len(f["d_len"])):
+        n = int(f["d_len"][i])
+        e = {k: f[f"d_{k}"][d0:d0 + n] for k in
+             ("nodes", "feature", "threshold", "score", "left_count", "rows")}
+        e.update(round=int(f["d_round"][i]), depth=int(f["d_depth"][i]), feats=f["d_feats"][i])
+        depths.append(e)
+        d0 += n
+    samples = {r: f[f"r{r}_preds_sample"] for r in range(R) if f"r{r}_preds_sample" in f}
+    return {"rounds": R, "trees": trees, "depths": depths, "preds_sum": f["preds_sum"],
+            "preds_sample": samples}
 
 
 def main() -> int:
@@ -106,8 +132,13 @@ def main() -> int:
     rng = torch.Generator().manual_seed(cfg["random_state"])
     kw = {k: v for k, v in cfg.items() if k != "random_state"}
     out: dict[str, np.ndarray] = {}
-    samp = sample_rows(bins.shape[0])
+    cols: dict[str, list] = {k: [] for k in (
+        "t_feature", "t_threshold", "t_left", "t_right", "t_value", "t_is_leaf", "t_len",
+        "d_round", "d_depth", "d_len", "d_feats", "d_nodes", "d_feature", "d_threshold", "d_score",
+        "d_left_count", "d_rows")}
+    samp = sample_rows(name, bins.shape[0])
     preds = None
+    sums = []
     for r in range(rounds):
         t1 = time.perf_counter()
         trace: list = []
@@ -115,23 +146,38 @@ def main() -> int:
                       init_preds=preds, **kw)
         preds = res.preds
         a = res.rounds[0]
-        for key in ("feature", "threshold", "left", "right", "value", "is_leaf"):
-            out[f"r{r}_{key}"] = np.asarray(a[key])
+        # ids, features and thresholds fit int16 (trees of at most 2^15 nodes, F < 2^15)
+        for key in ("feature", "threshold", "left", "right"):
+            cols[f"t_{key}"].append(np.asarray(a[key]).astype(np.int16))
+        cols["t_value"].append(np.asarray(a["value"], dtype=np.float64))
+        cols["t_is_leaf"].append(np.asarray(a["is_leaf"], dtype=bool))
+        cols["t_len"].append(len(a["feature"]))
         for t in trace:
             d, rr = t["depth"], t["result"]
-            out[f"r{r}_d{d}_nodes"] = np.asarray(t["node_ids"], dtype=np.int32)
-            out[f"r{r}_d{d}_feats"] = np.asarray(t["feats"], dtype=np.int32)
-            out[f"r{r}_d{d}_feature"] = rr.feature.astype(np.int32)
-            out[f"r{r}_d{d}_threshold"] = rr.threshold.astype(np.int32)
-            out[f"r{r}_d{d}_score"] = rr.score.astype(np.float32)
-            out[f"r{r}_d{d}_left_count"] = rr.left_count.astype(np.int64)
-            out[f"r{r}_d{d}_rows"] = np.array([sum(x.size for x in er) for er in t["nodes_era_rows"]],
-                                               dtype=np.int64)
-        if r < 5 or r % 10 == 9 or r == rounds - 1:
+            cols["d_round"].append(r)
+            cols["d_depth"].append(d)
+            cols["d_len"].append(len(t["node_ids"]))
+            cols["d_feats"].append(np.asarray(t["feats"], dtype=np.int16))
+            cols["d_nodes"].append(np.asarray(t["node_ids"], dtype=np.int16))
+            cols["d_feature"].append(rr.feature.astype(np.int16))
+            cols["d_threshold"].append(rr.threshold.astype(np.int16))
+            cols["d_score"].append(rr.score.astype(np.float32))
+            cols["d_left_count"].append(rr.left_count.astype(np.int64))
+            cols["d_rows"].append(np.array([sum(x.size for x in er) for er in t["nodes_era_rows"]],
+                                           dtype=np.int64))
+        if r < 5 or r % 25 == 24 or r == rounds - 1:
             out[f"r{r}_preds_sample"] = preds[samp].astype(np.float32)
-        out[f"r{r}_preds_sum"] = np.array([preds.astype(np.float64).sum()])
+        sums.append(preds.astype(np.float64).sum())
         print(f"round {r}: {len(trace)} depths, tree of {a['feature'].shape[0]} nodes, "
               f"{time.perf_counter() - t1:.1f} s", flush=True)
+    for k, v in cols.items():
+        if k == "d_feats":
+            out[k] = np.stack(v)
+        elif k in ("t_len", "d_round", "d_depth", "d_len"):
+            out[k] = np.asarray(v, dtype=np.int32)
+        else:
+            out[k] = np.concatenate(v)
+    out["preds_sum"] = np.asarray(sums, dtype=np.float64)
     out["rounds"] = np.array([rounds])
     out["splitter"] = np.array([splitter])
     out["config"] = np.array([repr(cfg)])

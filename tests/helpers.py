@@ -378,37 +378,33 @@ def fixture_fit_parity(oracle_mod, name: str, fit_rounds) -> int:
         through the pack sums) of the oracle's (a second, shorter device fit when the
         trajectories part early).
     Returns the number of rounds compared whole (at least 1)."""
-    from pathlib import Path
+    from tests.golden.make_rounds_golden import case_data, load_fixture, sample_rows
 
-    from tests.golden.make_rounds_golden import case_data, sample_rows
-
-    path = Path(__file__).resolve().parent / "golden" / f"{name}_rounds.npz"
-    with np.load(path, allow_pickle=False) as z:
-        fx = {k: z[k] for k in z.files}
-    R = int(fx["rounds"][0])
-    keys = ("feature", "threshold", "left", "right", "value", "is_leaf")
-    want = [{k: fx[f"r{r}_{k}"] for k in keys} for r in range(R)]
+    fx = load_fixture(name)
+    R = fx["rounds"]
+    want = fx["trees"]
     print(f"[{name} fixture] generating the workload ({R} fixture rounds)", flush=True)
     X, bins, y, era, cfg = case_data(name)
     E = int(era.max()) + 1
-    samp = sample_rows(bins.shape[0])
+    samp = sample_rows(name, bins.shape[0])
     B, lr = int(cfg["pack_size"]), float(cfg["learning_rate"])
     trace, after = [], []
     preds = np.zeros(bins.shape[0], dtype=np.float32)
+    by_round: dict = {}
+    for e in fx["depths"]:
+        by_round.setdefault(e["round"], []).append(e)
     for r in range(R):
         grad = (preds - y).astype(np.float32)
-        d = 0
-        while f"r{r}_d{d}_nodes" in fx:
-            nodes = fx[f"r{r}_d{d}_nodes"]
-            trace.append({"round": r, "depth": d, "node_ids": nodes, "feats": fx[f"r{r}_d{d}_feats"],
-                          "grad": grad, "result": _Scores(fx[f"r{r}_d{d}_score"]),
+        for e in by_round.get(r, []):
+            d, nodes = e["depth"], e["nodes"]
+            trace.append({"round": r, "depth": d, "node_ids": nodes, "feats": e["feats"], "grad": grad,
+                          "result": _Scores(e["score"]), "rows": e["rows"],
                           "nodes_era_rows": _EraRows(node_at_depth(want[r], bins, d), nodes, era, E)})
-            d += 1
         leaf_val = want[r]["value"].astype(np.float32)[oracle_mod.leaf_index(want[r], bins)]
         preds = oracle_mod.pack_update(preds, leaf_val, B, np.float32(lr))
-        assert float(preds.astype(np.float64).sum()) == float(fx[f"r{r}_preds_sum"][0]), f"replay {r}"
-        if f"r{r}_preds_sample" in fx:
-            np.testing.assert_array_equal(preds[samp], fx[f"r{r}_preds_sample"], err_msg=f"replay {r}")
+        assert float(preds.astype(np.float64).sum()) == float(fx["preds_sum"][r]), f"replay {r}"
+        if r in fx["preds_sample"]:
+            np.testing.assert_array_equal(preds[samp], fx["preds_sample"][r], err_msg=f"replay {r}")
         after.append(preds)
     print(f"[{name} fixture] HIP fit", flush=True)
     model = fit_rounds(R)
@@ -427,13 +423,51 @@ def fixture_fit_parity(oracle_mod, name: str, fit_rounds) -> int:
             break
         dl = next(logs)
         assert (dl["depth"], dl["nodes_processed"]) == (t["depth"], len(t["node_ids"]))
-        assert dl["rows_total"] == int(fx[f"r{t['round']}_d{t['depth']}_rows"].sum())
+        assert dl["rows_total"] == int(t["rows"].sum())
     dev_model = model if matched == R else fit_rounds(matched)
     ref = after[matched - 1].astype(np.float64)
     bar = np.maximum(1e-5, pred_bar + matched * (B + 1) * 6e-8 * np.abs(ref))
-    dev = dev_model._train_preds.cpu().numpy().astype(np.float64)
+    dev = train_preds_rows(dev_model).astype(np.float64)
     diff = np.abs(dev - ref)
     print(f"[{name} fixture] training predictions after {matched} rounds: max diff {diff.max():.3g}, "
           f"{int(np.sum(diff > 1e-5))} rows beyond 1e-5", flush=True)
     assert np.all(diff <= bar)
     return matched
+
+
+def train_preds_rows(model) -> np.ndarray:
+    """A fitted model's training predictions in the caller's row order (the fit keeps them in
+    its era-major order, model._perm)."""
+    dev = model._train_preds.cpu().numpy()
+    perm = getattr(model, "_perm", None)
+    if perm is None:
+        return dev
+    out = np.empty_like(dev)
+    out[np.asarray(perm)] = dev
+    return out
+
+
+def live_fit_parity(oracle_mod, fit_rounds, bins, y, era_codes, kw, rounds, *, min_matched=None):
+    """A HIP fit against the oracle's fit (run here) on the same data, over `rounds` rounds.
+
+    fit_rounds(n) fits the first n rounds on the device and returns the PackBoost model. Trees
+    must be identical, or part at an asserted near-tie (compare_fit_rounds); node values within
+    1e-5; training predictions and predict() after the matched rounds within 1e-5 of the oracle's
+    (a second, shorter device fit when the trajectories part early); leaf indices of every
+    matched round's tree bit-exact. Requires at least `min_matched` whole rounds (default: all
+    of them, unless they part at an asserted near-tie; then at least one). Returns matched."""
+    model = fit_rounds(rounds)
+    trace: list = []
+    ref = oracle_mod.fit(bins, y, era_codes, num_rounds=rounds, trace=trace, **kw)
+    matched, pred_bar = compare_fit_rounds(oracle_mod, model._rounds, ref, trace, bins, kw)
+    print(f"[fit parity] {matched} of {rounds} rounds identical", flush=True)
+    assert matched >= (1 if min_matched is None else min_matched)
+    B, lr = int(kw.get("pack_size", 8)), float(kw.get("learning_rate", 0.1))
+    dev_model = model if matched == rounds else fit_rounds(matched)
+    ref_train = oracle_mod.replay_preds(ref.rounds[:matched], bins, B, lr).astype(np.float64)
+    if matched == rounds:
+        np.testing.assert_array_equal(ref_train, ref.preds)
+    bar = np.maximum(1e-5, pred_bar + matched * (B + 1) * 6e-8 * np.abs(ref_train))
+    d = np.abs(train_preds_rows(dev_model).astype(np.float64) - ref_train)
+    assert np.all(d <= bar), f"training predictions: max diff {d.max():.3g}"
+    return model, ref, matched, bar

@@ -49,7 +49,20 @@ def test_host_schema_split_finder(hip, oracle_mod, case):
     kw = dict(lambda_l2=1e-3, lambda_dro=dro, direction_weight=dirw, era_alpha=alpha, min_samples_leaf=msl)
     got, stats = backends.find_best_splits_batched(p["bins"].view(np.int8), p["grad"], ner, feats, nb, kc, cut,
                                                    kw["lambda_l2"], dro, dirw, alpha, msl)
-    ref = oracle_mod.split_batch(p["bins"], p["grad"], ner[:-1], feats, nb, kc, cut, want_cands=True, **kw)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], ner[:-1], feats, nb, kc, cut, want_cands=True,
+                                 want_planes=True, **kw)
+
+    def thresholds_of(k: int) -> np.ndarray:
+        """The candidate thresholds of feature slot k (frontier_cpu.cpp:322-338): every one, or
+        the even / mass K-cuts (mass over this call's nodes, from the oracle's planes)."""
+        if not (0 < kc < nb - 1):
+            return np.arange(nb - 1)
+        if cut == "even":
+            return oracle_mod.even_cuts(nb, kc)
+        pref = ref.planes[0][:, :, k, :].astype(np.int64)  # [E, M, nb] prefix counts
+        mass = np.diff(pref, axis=2, prepend=0).sum(axis=(0, 1))
+        return oracle_mod.mass_cuts(mass, nb, kc)
+
     assert isinstance(got, list) and len(got) == M and set(stats) == STAT_KEYS
     assert got[1] is None and got[-1] is None
     assert stats["nodes_processed"] == U and stats["nodes_skipped"] == 2
@@ -68,7 +81,12 @@ def test_host_schema_split_finder(hip, oracle_mod, case):
         assert d is not None, m
         mass = float(np.abs(p["grad"][np.concatenate(eras)]).sum())
         if (d["feature"], d["threshold"]) != (int(ref.feature[m]), int(ref.threshold[m])):
-            assert abs(d["score"] - float(ref.score[m])) <= 1e-6 * max(1.0, abs(float(ref.score[m]))), m
+            # a near-tie: the oracle's own score of the device's pick, not the device's score
+            k = int(np.nonzero(feats == d["feature"])[0][0])
+            t = int(np.nonzero(thresholds_of(k) == d["threshold"])[0][0])
+            alt, best = float(ref.cands[0][m, k, t]), float(ref.score[m])
+            assert ref.cands[3][m, k, t] and abs(alt - best) <= 1e-6 * max(1.0, abs(best)), m
+            print(f"[batched host] near-tie at node {m}: {alt!r} vs {best!r}", flush=True)
             continue
         assert d["left_count"] == int(ref.left_count[m]) and d["right_count"] == int(ref.right_count[m]), m
         assert d["left_hess"] == float(ref.left_hess[m]) and d["right_hess"] == float(ref.right_hess[m]), m

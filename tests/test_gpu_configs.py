@@ -1,11 +1,6 @@
-"""GPU parity at BASELINE configs 2, 4 and 5 at their real workloads.
+"""GPU parity at BASELINE configs 3, 4 and 5 at their real workloads (configs 2 and 3 against
+the oracle's whole rounds: tests/test_gpu_fixture_rounds.py).
 
-- Config 2 (200,000 x 100 float32, 10 columns correlated at 0.6, 50 eras, 128 bins, B 8, D 5):
-  a whole 10-round fit against the oracle's restatement of the reference fit
-  (booster.py:375-599 + frontier_cpu.cpp:111-515). Trees identical (a round whose split
-  differs must be a near-tie: the oracle's score of the device's pick within 1e-6 of its best;
-  the trajectories part there); node values within 1e-5 of the exact float64 value and of the
-  oracle's (widened by the oracle's own float32 summation error); predictions within 1e-5.
 - Config 4 (1,000,000 x 500, 255 bins, 200 eras): one depth-7 step at full size (128 nodes,
   node-tiled histogram), checked through size-independent properties: era totals against
   row counts and float64 sums, monotone prefixes, sampled cells against NumPy bincounts, the
@@ -35,38 +30,6 @@ import pytest
 from tests.helpers import PB_INACTIVE, GpuDepth, compare_fit_rounds, split_params
 
 pytestmark = pytest.mark.gpu
-
-
-# ----------------------------------------------------------------------------- config 2
-def test_config2_fit(hip, oracle_mod):
-    from oracle.calibrate import config2_data
-    from packboost_amd import PackBoost, PackBoostConfig
-    from packboost_amd.data import preprocess_features
-
-    rounds = 10
-    X, y, era = config2_data()
-    kw = dict(pack_size=8, max_depth=5, learning_rate=0.1, max_bins=128, min_samples_leaf=20,
-              random_state=42)
-    print("[config2] HIP fit", flush=True)
-    model = PackBoost(PackBoostConfig(**kw)).fit(X, y, era, num_rounds=rounds)
-    bins = preprocess_features(X, 128).bins
-    print("[config2] oracle fit", flush=True)
-    trace = []
-    ref = oracle_mod.fit(bins, y, era.astype(np.int64), num_rounds=rounds, trace=trace, **kw)
-    matched, pred_bar = compare_fit_rounds(oracle_mod, model._rounds, ref, trace, bins, kw)
-    print(f"[config2] {matched} of {rounds} rounds identical", flush=True)
-    assert matched >= 3
-    if matched == rounds:
-        # predictions within 1e-5, or within what the node value bars allow (lr * B * bar of
-        # the row's leaf per round) plus one float32 rounding per add (B + 1 per round)
-        bar = np.maximum(1e-5, pred_bar + rounds * 9 * 6e-8 * np.abs(ref.preds))
-        d = np.abs(model._train_preds.cpu().numpy().astype(np.float64) - ref.preds)
-        print(f"[config2] training predictions: {int(np.sum(d > 1e-5))} rows beyond 1e-5, "
-              f"max {d.max():.3g}", flush=True)
-        assert np.all(d <= bar)
-        pred = model.predict(X)
-        d = np.abs(pred.astype(np.float64) - oracle_mod.predict(ref.rounds, 8, 0.1, bins))
-        assert np.all(d <= bar)
 
 
 # ----------------------------------------------------------------------------- config 4

@@ -399,3 +399,50 @@ def test_hist_max_nodes_above_frontier_bound(hip, oracle_mod):
         np.testing.assert_array_equal(gp1.view(np.uint32), gp0.view(np.uint32))
     finally:
         g.close()
+
+
+UNIT_CASES = [
+    # seed, N, F, E, nb, U, K: 1, 2, 5 and 8 pairs per producer thread at T = 4 (4, 12, 40
+    # and 60 candidates per workgroup), partial last chunks of eras, an empty era
+    (21, 20_000, 60, 37, 5, 1, 60),
+    (22, 40_000, 240, 50, 5, 8, 240),
+    (23, 60_000, 240, 75, 5, 32, 240),
+    (24, 30_000, 120, 26, 16, 4, 120),
+]
+
+
+@pytest.mark.parametrize("mode", ["0", "1", "2"])
+@pytest.mark.parametrize("case", UNIT_CASES, ids=[f"seed{c[0]}" for c in UNIT_CASES])
+def test_unit_weight_scorers(hip, oracle_mod, monkeypatch, case, mode):
+    """The two producer/consumer scorers for T <= 63 with unit era weights (PB_SCORE_PC: 0 the
+    launch rule, 1 des_score_pc_kernel only, 2 des_score_pcu_kernel only, at every pairs-per-
+    thread instantiation), fed the oracle's planes: every candidate bit-identical to the
+    restated scorer (frontier_cpu.cpp:342-444)."""
+    seed, N, F, E, nb, U, K = case
+    monkeypatch.setenv("PB_SCORE_PC", mode)
+    print(f"[unit scorers] mode={mode} {case}", flush=True)
+    p = make_problem(seed, N, F, E, nb, U, empty_era=True)
+    feats = np.random.default_rng(seed + 100).permutation(F)[:K].astype(np.int32)
+    kw = dict(lambda_l2=1e-6, lambda_dro=0.5, direction_weight=0.0, era_alpha=0.0, min_samples_leaf=5)
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, want_planes=True, **kw)
+    rc, rg = ref.planes
+    rg1 = rg.copy()
+    rg1[..., nb - 1] = rg[:, :, :1, nb - 1]  # one era total per (era, node), as the device planes
+    g = GpuDepth(hip, p, K, msl=5)
+    try:
+        g.load_planes(rc, rg1)
+        params = split_params(hip, lambda_l2=1e-6, lambda_dro=0.5, msl=5)
+        c = g.score(feats, params, nb - 1)
+        sp = oracle_mod.score_planes(rc, rg1, feats, None, **kw)
+        np.testing.assert_array_equal(c["valid"].astype(bool), sp["valid"].astype(bool))
+        v = sp["valid"].astype(bool)
+        assert v.sum() > 0
+        np.testing.assert_array_equal(c["score"][v].view(np.uint32), sp["score"][v].view(np.uint32))
+        np.testing.assert_array_equal(c["left_total"][v], sp["left_total"][v])
+        np.testing.assert_array_equal(c["left_grad"][v].view(np.uint32), sp["left_grad"][v].view(np.uint32))
+        dec = g.decide(params)
+        for u in range(U):
+            if sp["best_feature"][u] >= 0 and v[u].any():
+                assert (dec["feature"][u], dec["threshold"][u]) == (sp["best_feature"][u], sp["best_threshold"][u])
+    finally:
+        g.close()

@@ -97,3 +97,29 @@ def test_segments_many_eras(hip, monkeypatch):
                 np.testing.assert_array_equal(np.asarray(a[key]), np.asarray(b[key]),
                                               err_msg=f"from {from_depth} round {r} {key}")
         np.testing.assert_array_equal(seg._train_preds.cpu().numpy(), planes._train_preds.cpu().numpy())
+
+
+@pytest.mark.parametrize("case", [
+    # seed, N, F, E, nb, D, B, msl, dro, dir, alpha, empty_era, rounds
+    (11, 20000, 16, 10, 255, 6, 4, 20, 0.3, 0.0, 0.0, False, 4),
+    (12, 12000, 12, 7, 64, 5, 2, 30, 0.5, 0.2, 1.5, True, 4),
+], ids=["nb255_d6_dro", "nb64_dir_alpha_dro_empty_era"])
+def test_segments_match_oracle(hip, oracle_mod, monkeypatch, case):
+    """Segment mode fused from depth 0 (every depth's histogram and DES scores from
+    seg_score_kernel) against the oracle's restated reference fit directly: trees identical
+    or parted at an asserted near-tie, values and training predictions within 1e-5
+    (tests.helpers.live_fit_parity)."""
+    from packboost_amd.data import encode_eras, preprocess_features
+    from tests.helpers import live_fit_parity
+
+    seed, N, F, E, nb, D, B, msl, dro, dirw, alpha, empty, rounds = case
+    print(f"[segments vs oracle] {case}", flush=True)
+    X, y, era = _data(seed, N, F, E, empty)
+    kw = dict(pack_size=B, max_depth=D, learning_rate=0.2, min_samples_leaf=msl, max_bins=nb,
+              lambda_dro=dro, direction_weight=dirw, era_alpha=alpha, random_state=seed)
+    bins = preprocess_features(X, nb).bins
+    codes = encode_eras(era, N)[0].astype(np.int64)
+    _, _, matched, _ = live_fit_parity(
+        oracle_mod, lambda n: _fit("segments", monkeypatch, X, y, era, n, 0, **kw), bins, y, codes, kw,
+        rounds)
+    assert matched >= 1
