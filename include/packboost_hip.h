@@ -184,8 +184,9 @@ int pb_set_segment_mode(pb_ctx* ctx, int32_t enable, int32_t from_depth);
 /* Applies the per-node winners of the last pb_des_score: picks each node's split with the
  * reference's sequential scan (features in subset order, thresholds ascending; a candidate wins
  * with a higher score, or within 1e-12 of the best with more left rows, then a larger feature
- * id, then a larger threshold: frontier_cpu.cpp:415-426), reading the feature ids that call was
- * given (keep feats_dev valid until this call's work has run), builds the decisions of this
+ * id, then a larger threshold: frontier_cpu.cpp:415-426), with the feature ids that call was
+ * given (pb_des_score copies them into the context on its stream, so feats_dev may be freed or
+ * rewritten once pb_des_score has returned), builds the decisions of this
  * depth (booster.py:527-563: split -> children ids (len, len+1), child values
  * -G/(H+lambda); no split -> leaf value -G/(H+lambda)), assigns the next frontier
  * (children with >= 2*msl rows, booster.py:516, 794-796) and writes the depth's

@@ -14,6 +14,7 @@ from __future__ import annotations
 import json
 import logging
 import os
+import warnings
 from dataclasses import dataclass, field
 from time import perf_counter
 from typing import Callable, Iterable, List, Sequence, Tuple
@@ -173,8 +174,23 @@ def _require_backend(device: torch.device) -> None:
 class PackBoost:
     """Pack-parallel gradient booster with DES scoring (squared loss)."""
 
-    def __init__(self, config: PackBoostConfig) -> None:
+    NONFINITE_POLICIES = ("raise", "truncate")
+
+    def __init__(self, config: PackBoostConfig, *, nonfinite: str | None = None) -> None:
+        """nonfinite: what fit does at the first round whose gradients (preds - y) are not all
+        finite (y holding NaN/inf, or predictions that overflowed). "raise" (the default, or
+        PACKBOOST_NONFINITE) raises FloatingPointError; "truncate" warns (RuntimeWarning) and
+        ends the fit with the rounds before it, whose trees and training predictions stand.
+        The reference has no such check: its float sums carry NaN into the scores
+        (frontier_cpu.cpp:363-432), a candidate whose era sums hold a NaN never wins, and the
+        failed-split leaf is -NaN/(h + lambda) (booster.py:532-542), so from that round on its
+        trees hold NaN values and its predictions turn NaN. The fixed-point histograms here
+        have no NaN to carry, so neither policy reproduces that; both stop before it."""
         self.config = config
+        policy = (nonfinite or os.getenv("PACKBOOST_NONFINITE") or "raise").lower()
+        if policy not in self.NONFINITE_POLICIES:
+            raise ValueError(f"nonfinite must be one of {self.NONFINITE_POLICIES}, got {policy!r}")
+        self.nonfinite = policy
         self._device = torch.device(config.device)
         self._rng = torch.Generator(device="cpu")
         if config.random_state is not None:
@@ -289,12 +305,24 @@ class PackBoost:
         # metrics and eval predictions run on a side stream so that the next round, already
         # enqueued on the fit's stream, keeps the GPU busy while the host builds trees
         side = torch.cuda.Stream(device)
+        truncated = False
         try:
             t0 = perf_counter()
             last_phase: dict[int, tuple[np.ndarray, int]] = {}  # depth -> (times, timed round)
-            for round_idx, (log, preds_after, ready) in enumerate(
-                    fitter.rounds(self._rng, num_rounds, phase_times=self._phase_times(),
-                                  phase_every=self.phase_every)):
+            round_iter = enumerate(fitter.rounds(self._rng, num_rounds, phase_times=self._phase_times(),
+                                                 phase_every=self.phase_every))
+            while True:
+                try:
+                    round_idx, (log, preds_after, ready) = next(round_iter)
+                except StopIteration:
+                    break
+                except FloatingPointError as exc:
+                    if self.nonfinite != "truncate":
+                        raise
+                    warnings.warn(f"{exc}; nonfinite='truncate' ends the fit after "
+                                  f"{len(self._rounds)} rounds", RuntimeWarning, stacklevel=2)
+                    truncated = True
+                    break
                 arrs = tree_arrays_from_log(log, cfg, N)
                 self._rounds.append(arrs)
                 self._trees_cache = None
@@ -339,7 +367,13 @@ class PackBoost:
             raise
         finally:
             torch.cuda.synchronize(device)
-        self._train_preds = fitter.preds[:N].clone()
+        if truncated:
+            # the device has run the non-finite round (and the one enqueued after it) on
+            # `fitter.preds`: the kept rounds' training predictions come from their trees
+            self._train_preds = (self._predict_device(bins_fm, N, device) if self._rounds
+                                 else torch.zeros(N, dtype=torch.float32, device=device))
+        else:
+            self._train_preds = fitter.preds[:N].clone()
         self._fit_mode = "segments" if fitter.segments else "planes"
         fitter.close()
         self._fitter = None

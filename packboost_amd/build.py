@@ -9,6 +9,7 @@ Every HIP source is compiled with:
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -46,6 +47,27 @@ def compile_flags() -> list[str]:
     ]
 
 
+# Kernels that must not use scratch (register spills): the histogram and the scorers. One build
+# of the single-feature histogram tile that spilled returned wrong plane counts for a code
+# generation it took only with the spills, so a spill here fails the build. (kcuts_kernel keeps
+# per-lane arrays in scratch by design.)
+NO_SCRATCH = re.compile(r"hist_era_kernel|seg_score_kernel|des_score")
+
+
+def spilling_kernels(remarks: str) -> list[str]:
+    """Names of NO_SCRATCH kernels whose kernel-resource-usage remarks report ScratchSize > 0."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name and int(m.group(1)) > 0 and NO_SCRATCH.search(name):
+            out.append(name)
+    return out
+
+
 def build(verbose: bool = False) -> Path:
     """Compiles every source for gfx950 and links the shared library. Always rebuilds."""
     cc = hipcc()
@@ -54,12 +76,19 @@ def build(verbose: bool = False) -> Path:
 
     def one(src: str) -> Path:
         obj = out_dir / (Path(src).stem + ".o")
-        cmd = [cc, *compile_flags(), "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *compile_flags(), "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src),
+               "-o", str(obj)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")
-        if verbose and res.stderr.strip():
-            print(res.stderr, file=sys.stderr)
+        spilled = spilling_kernels(res.stderr)
+        if spilled:
+            raise RuntimeError(f"{src}: register spills (scratch) in {', '.join(spilled)}; the histogram "
+                               "and scorer kernels must fit their registers")
+        if verbose:
+            warn = "\n".join(l for l in res.stderr.splitlines() if "remark:" not in l)
+            if warn.strip():
+                print(warn, file=sys.stderr)
         return obj
 
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:

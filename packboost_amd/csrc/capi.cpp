@@ -45,6 +45,7 @@ struct pb_ctx {
     pb::SeqCands seq;              // every candidate of a depth [umax][max_feats][tmax]
     int32_t last_K, last_T;        // shape, feature ids and threshold table of the last
     const int32_t* last_feats;     // pb_des_score, read by pb_decide
+    int32_t* feats_keep;           // [max_feats] the per-phase pb_des_score's copy of its ids
     const int32_t* last_thr_tab;
     int64_t lds_budget;
     int32_t force_copies;
@@ -141,6 +142,7 @@ void free_ctx(pb_ctx* c) {
     (void)hipFree(c->ids[0]);
     (void)hipFree(c->ids[1]);
     (void)hipFree(c->thr_tab);
+    (void)hipFree(c->feats_keep);
     for (int i = 0; i < 2; ++i) {
         (void)hipFree(c->sb[i].g);
         (void)hipFree(c->sb[i].row);
@@ -299,7 +301,8 @@ int pb_ctx_create(const pb_dims* dims, const int32_t* era_off_host, pb_ctx** out
         (rc = dev_alloc(&c->node_best, c->umax, "alloc node winners")) ||
         (rc = dev_alloc(&c->ids[0], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
         (rc = dev_alloc(&c->ids[1], std::max(c->umax, 2) * 2, "alloc frontier ids")) ||
-        (rc = dev_alloc(&c->thr_tab, (size_t)d.max_feats * tmax, "alloc threshold table"))) {
+        (rc = dev_alloc(&c->thr_tab, (size_t)d.max_feats * tmax, "alloc threshold table")) ||
+        (rc = dev_alloc(&c->feats_keep, (size_t)d.max_feats, "alloc feature ids"))) {
         free_ctx(c);
         return rc;
     }
@@ -520,9 +523,15 @@ int pb_set_bin_layout(pb_ctx* c, int32_t layout) {
     return PB_OK;
 }
 
-int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, const int32_t* feats,
-                 int32_t K, int32_t depth, int32_t max_nodes, const pb_split_params* p,
-                 pb_candidate* cand_all, void* stream) {
+namespace {
+
+// pb_des_score's work. keep_feats: copy the K feature ids into the context (stream-ordered,
+// before pb_decide reads them), so that a caller of the per-phase C ABI may free or rewrite its
+// buffer between pb_des_score and pb_decide; pb_grow_round passes false (the ids it scores
+// stay put for the whole call, and a copy per depth would cost a launch).
+int des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, const int32_t* feats,
+              int32_t K, int32_t depth, int32_t max_nodes, const pb_split_params* p,
+              pb_candidate* cand_all, void* stream, bool keep_feats) {
     if (!c || !hist_cnt || !hist_grad || !feats || !p)
         return fail(PB_ERR_INVALID, "pb_des_score: null argument");
     if (K < 1 || K > c->d.max_feats) return fail(PB_ERR_INVALID, "pb_des_score: K out of range");
@@ -591,7 +600,21 @@ int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, con
     c->last_feats = feats;
     c->last_thr_tab = thr_tab;
     PB_HIP(pb::launch_score(a, (int)grid, sh.lds_bytes, (hipStream_t)stream), "score launch");
+    if (keep_feats) {
+        PB_HIP(hipMemcpyAsync(c->feats_keep, feats, sizeof(int32_t) * K, hipMemcpyDeviceToDevice,
+                              (hipStream_t)stream),
+               "feature id copy");
+        c->last_feats = c->feats_keep;
+    }
     return PB_OK;
+}
+
+}  // namespace
+
+int pb_des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, const int32_t* feats,
+                 int32_t K, int32_t depth, int32_t max_nodes, const pb_split_params* p,
+                 pb_candidate* cand_all, void* stream) {
+    return des_score(c, hist_cnt, hist_grad, feats, K, depth, max_nodes, p, cand_all, stream, true);
 }
 
 int pb_decide(pb_ctx* c, int32_t depth, int32_t max_nodes, const pb_split_params* p,
@@ -819,8 +842,8 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
                                  b->hist_cnt_dev, b->hist_grad_dev, stream)))
                 return rc;
             if ((rc = mark(1))) return rc;
-            if ((rc = pb_des_score(c, b->hist_cnt_dev, b->hist_grad_dev, f, K, d, m, &b->params, nullptr,
-                                   stream)))
+            if ((rc = des_score(c, b->hist_cnt_dev, b->hist_grad_dev, f, K, d, m, &b->params, nullptr,
+                                stream, false)))
                 return rc;
         }
         if ((rc = mark(2))) return rc;

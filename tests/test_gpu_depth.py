@@ -446,3 +446,29 @@ def test_unit_weight_scorers(hip, oracle_mod, monkeypatch, case, mode):
                 assert (dec["feature"][u], dec["threshold"][u]) == (sp["best_feature"][u], sp["best_threshold"][u])
     finally:
         g.close()
+
+
+def test_decide_keeps_scored_feature_ids(hip, oracle_mod):
+    """pb_decide uses the feature ids pb_des_score was given even when the caller rewrites its
+    buffer between the two calls (pb_des_score keeps a copy on its stream)."""
+    seed, N, F, E, nb, U, K = 31, 8000, 30, 7, 5, 3, 20
+    p = make_problem(seed, N, F, E, nb, U)
+    feats = np.random.default_rng(seed).permutation(F)[:K].astype(np.int32)
+    params = split_params(hip, lambda_dro=0.5, msl=5)
+    decs = []
+    for clobber in (False, True):
+        g = GpuDepth(hip, p, K, msl=5)
+        try:
+            g.hist(feats)
+            g.score(feats, params, nb - 1)
+            if clobber:
+                g.feats.fill_(F + 7)  # the caller reuses its buffer before pb_decide
+            decs.append(g.decide(params))
+        finally:
+            g.close()
+    ref = oracle_mod.split_batch(p["bins"], p["grad"], node_era_rows(p), feats, nb, lambda_dro=0.5,
+                                 min_samples_leaf=5)
+    for key in ("split", "feature", "threshold", "left_count"):
+        np.testing.assert_array_equal(decs[1][key], decs[0][key])
+    assert set(decs[1]["feature"][decs[1]["split"] == 1]) <= set(feats.tolist())
+    assert decs[1]["split"].sum() == int((ref.feature >= 0).sum())

@@ -215,9 +215,30 @@ def test_nonfinite_gradients_stop_the_fit(hip, case):
         cfg, rounds = PackBoostConfig(pack_size=2, learning_rate=0.1, **{**kw, "min_samples_leaf": 2000}), 2
     print(f"[nonfinite] {case}", flush=True)
     model = PackBoost(cfg)
+    assert model.nonfinite == "raise"
     with pytest.raises(FloatingPointError, match="not finite"):
         model.fit(X, y, era, num_rounds=rounds)
     assert model._fitter is None
+    kept = len(model._rounds)  # the rounds before the non-finite one
+    assert kept < rounds
+
+    # nonfinite="truncate": a warning, and the fit ends with the same finite rounds
+    print(f"[nonfinite] {case} truncate ({kept} finite rounds)", flush=True)
+    trunc = PackBoost(cfg, nonfinite="truncate")
+    with pytest.warns(RuntimeWarning, match="not finite"):
+        trunc.fit(X, y, era, num_rounds=rounds)
+    assert trunc._fitter is None and len(trunc._rounds) == kept
+    for a, b in zip(model._rounds, trunc._rounds):
+        for key in a:
+            np.testing.assert_array_equal(a[key], b[key], err_msg=key)
+    p = trunc.predict(X)
+    assert np.all(np.isfinite(p))
+    # the training predictions are the kept trees' (era-major row order)
+    order = np.argsort(era, kind="stable")
+    np.testing.assert_allclose(trunc._train_preds.cpu().numpy(), p[order], rtol=1e-6,
+                               atol=1e-6 * max(1.0, float(np.abs(p).max())))
+    if case != "overflowing_predictions":
+        assert kept == 0 and np.all(p == 0.0)
     # the same model object fits again on finite data
     y_ok = np.nan_to_num(y, nan=0.0, posinf=0.0)
     model2 = PackBoost(PackBoostConfig(pack_size=2, learning_rate=0.1, **kw)).fit(X, y_ok, era, num_rounds=2)
