@@ -59,7 +59,14 @@ typedef struct {
  * (frontier_cpu.cpp:116-123) as C++ float after pybind's double->float cast, while
  * leaf values use the Python double (booster.py:545-546). They are carried here as
  * double; the scorer rounds each to float exactly as that cast does.
- * cut_selection: 0 = "even", 1 = "mass". */
+ * cut_selection: 0 = "even", 1 = "mass".
+ * skip_last_bin: 1 when the histogram planes were built with one bin more than the
+ * reference's num_bins (the context's max_bins = num_bins + 1), that last bin holding the rows
+ * whose bin is >= num_bins. The reference leaves such rows out of a feature's histogram
+ * (frontier_cpu.cpp:278-281, frontier_cuda.cu:451) while they still count in the node's row
+ * total and go right in the partition (:464-470). pb_des_score then sweeps thresholds
+ * 0..num_bins-2 only, takes each era's totals for a feature over its bins < num_bins, and the
+ * era weights and the node's row count over all rows. 0: every row's bin is < max_bins. */
 typedef struct {
     double lambda_l2;
     double lambda_dro;
@@ -68,7 +75,7 @@ typedef struct {
     int32_t min_samples_leaf;
     int32_t k_cuts;
     int32_t cut_selection;
-    int32_t reserved;
+    int32_t skip_last_bin;
 } pb_split_params;
 
 /* One entry per active frontier node and depth: the reference's SplitDecision

@@ -149,8 +149,12 @@ typedef struct {
 
 /* Score every threshold of one (node, feature) and update the node's running best,
  * visiting thresholds in list order (frontier_cpu.cpp:353-433). The per-era inputs are the
- * node's prefix/total planes for this feature: pc/pg [E][nb] with index nb-1 = total. */
-static void score_feature(const int64_t* pc, const float* pg, int E, int nb, const int32_t* thr_list,
+ * node's prefix/total planes for this feature: pc/pg [E][nb] with index nb-1 = total. The
+ * era weights count all of the node's rows in the era (NodeContext::era_weights,
+ * frontier_cpu.cpp:196-204): es [E+1], the node's era splits, or NULL when the feature's
+ * totals hold every row (no bin >= nb). */
+static void score_feature(const int64_t* pc, const float* pg, const int64_t* es, int E, int nb,
+                          const int32_t* thr_list,
                           int n_thr, int32_t feature, int64_t node_count, float lambda_l2,
                           float lambda_dro, float dir_w, float era_alpha, int msl, float* best_score,
                           int32_t* best_feat, int32_t* best_thr, int64_t* best_left, float* best_lg,
@@ -176,7 +180,8 @@ static void score_feature(const int64_t* pc, const float* pg, int E, int nb, con
 #if ORACLE_MUTANT == 2
             const float era_w = 1.0f;
 #else
-            const float era_w = (era_alpha > 0.0f) ? ((float)total_e + era_alpha) : 1.0f;
+            const int64_t rows_e = es ? es[e + 1] - es[e] : total_e;
+            const float era_w = (era_alpha > 0.0f) ? ((float)rows_e + era_alpha) : 1.0f;
 #endif
             const float weight = (left_e > 0 && right_e > 0) ? era_w : 0.0f;
             left_total += left_e;
@@ -400,7 +405,8 @@ int oracle_split_batch(const uint8_t* bins, int64_t n_rows, int64_t n_feat, cons
             if (!ctx[m].valid) continue;
             const size_t base = (size_t)m * E * nb;
             const size_t co = ((size_t)m * n_sub + fi) * T;
-            score_feature(pcnt + base, pgrd + base, E, nb, thr_list, n_thr, f, ctx[m].count,
+            score_feature(pcnt + base, pgrd + base, era_splits + (int64_t)m * (E + 1), E, nb,
+                          thr_list, n_thr, f, ctx[m].count,
                           lambda_l2, lambda_dro, dir_w, era_alpha, msl, &best_score[m], &best_feat[m],
                           &best_thr[m], &best_left[m], &best_lg[m], cand_score ? cand_score + co : NULL,
                           cand_lt ? cand_lt + co : NULL, cand_lg ? cand_lg + co : NULL,
@@ -489,7 +495,7 @@ int oracle_score_planes(const int32_t* plane_cnt, const float* plane_g, int32_t 
                 }
                 continue;
             }
-            score_feature(pc, pg, E, nb, thr_list, T, feats[fi], count, lambda_l2, lambda_dro, dir_w,
+            score_feature(pc, pg, NULL, E, nb, thr_list, T, feats[fi], count, lambda_l2, lambda_dro, dir_w,
                           era_alpha, msl, &bs, &bf, &bt, &bl, &blg, cand_score + co, cand_lt + co,
                           cand_lg + co, cand_valid + co);
         }

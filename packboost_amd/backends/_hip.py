@@ -57,7 +57,7 @@ class PbSplitParams(ctypes.Structure):
         ("lambda_l2", ctypes.c_double), ("lambda_dro", ctypes.c_double),
         ("direction_weight", ctypes.c_double), ("era_alpha", ctypes.c_double),
         ("min_samples_leaf", ctypes.c_int32), ("k_cuts", ctypes.c_int32),
-        ("cut_selection", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("cut_selection", ctypes.c_int32), ("skip_last_bin", ctypes.c_int32),
     ]
 
 

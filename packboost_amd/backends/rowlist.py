@@ -105,6 +105,24 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
     vals = grad.to(device=dev, dtype=torch.float32).contiguous()
     R = int(rows.numel())
     T = k_cuts if 0 < int(k_cuts) < nb - 1 else nb - 1
+    # bins >= max_bins: the reference leaves those rows out of the histogram and sends them
+    # right (frontier_cuda.cu:451, frontier_cpu.cpp:278-281, 464-470); here the subset's columns
+    # are copied with such bins set to max_bins, one extra plane bin that the scorer skips
+    fid_gather, skip = fid, 0
+    sel = None
+    if K and N:
+        # ids out of range are left to the gather kernel's own check (it raises "feature id");
+        # index_select would read out of bounds with them
+        lo, hi = (int(v) for v in torch.aminmax(fid))
+        if 0 <= lo and hi < F:
+            sel = b_fm.index_select(0, fid.long())
+    if sel is not None and int(sel.max()) >= nb:
+        if nb + 1 > 255:
+            raise ValueError("bins >= max_bins need max_bins <= 254 on the HIP backend")
+        b_fm = torch.clamp(sel, max=nb).contiguous()
+        F, ld_in = K, int(b_fm.stride(0))
+        fid_gather, skip = torch.arange(K, dtype=torch.int32, device=dev), 1
+    del sel
     out_s = torch.full((M, K), float("-inf"), dtype=torch.float32, device=dev)
     out_t = torch.full((M, K), -1, dtype=torch.int32, device=dev)
     out_g = torch.zeros((M, K), dtype=torch.float32, device=dev)
@@ -116,7 +134,7 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
     p = _hip.PbSplitParams(lambda_l2=float(lambda_l2), lambda_dro=float(lambda_dro),
                            direction_weight=float(direction_weight), era_alpha=alpha,
                            min_samples_leaf=int(min_samples_leaf), k_cuts=int(k_cuts),
-                           cut_selection=1 if str(cut_selection) == "mass" else 0, reserved=0)
+                           cut_selection=1 if str(cut_selection) == "mass" else 0, skip_last_bin=skip)
     t0 = time.perf_counter()
 
     def consume(m0, U, mx, cand, cnt, gp):
@@ -125,8 +143,8 @@ def find_best_splits_batched_rowlist(bins, grad, hess, rows_index, node_row_spli
                                           out_h[m0].data_ptr(), out_c[m0].data_ptr(), _hip.stream_ptr()),
                    "pb_best_thresholds")
 
-    _score_node_chunks(lib, b_fm, F, N, ld_in, fid, fid, K, vals, rows, R, nrs, nes, M, E, nb, T, p,
-                       _NODE_CHUNK, consume, "find_best_splits_batched_cuda")
+    _score_node_chunks(lib, b_fm, F, N, ld_in, fid_gather, fid, K, vals, rows, R, nrs, nes, M, E, nb + skip,
+                       T, p, _NODE_CHUNK, consume, "find_best_splits_batched_cuda")
     kernel_ms = (time.perf_counter() - t0) * 1e3
     return {"scores": out_s, "thresholds": out_t, "left_grad": out_g, "left_hess": out_h,
             "left_count": out_c, "kernel_ms": kernel_ms}
@@ -266,8 +284,8 @@ def find_best_splits_batched_host(bins, grad, nodes_era_rows, feature_subset, ma
     pb_des_score, pb_pick_sequential, pb_rowlist_partition). Differences from the reference:
     a node's left/right sums come from exact fixed-point histograms rounded once to float32
     (the reference adds float32 in row order); every node must list the same number of eras;
-    bins >= max_bins raise ValueError (the reference skips such rows in the histogram); mass
-    K-cuts are taken over the whole call up to 32768 nodes."""
+    bins >= max_bins are skipped in the histogram and sent right, as the reference does, for
+    max_bins up to 254; mass K-cuts are taken over the whole call up to 32768 nodes."""
     lib = _hip.load()
     bins_np = np.asarray(bins)
     grad_np = np.asarray(grad, dtype=np.float32)
@@ -326,8 +344,17 @@ def find_best_splits_batched_host(bins, grad, nodes_era_rows, feature_subset, ma
     if not 2 <= nb <= 255:
         raise ValueError("max_bins must lie in [2, 255]")
     sub = np.ascontiguousarray(bins_np[:, feats]).astype(np.int8, copy=False).view(np.uint8)  # [N, K]
+    # bins >= max_bins (int8 bins read unsigned, as the reference's cast does): the reference
+    # leaves those rows out of the feature's histogram and sends them right (frontier_cpu.cpp:
+    # 278-281, 464-470). They go to one extra plane bin, max_bins, that the scorer skips
+    # (pb_split_params.skip_last_bin); the partition's bin <= threshold sends them right.
+    skip = 0
     if int(sub.max()) >= nb:
-        raise ValueError("bins >= max_bins are not supported by the HIP backend")
+        if nb + 1 > 255:
+            raise ValueError("bins >= max_bins need max_bins <= 254 on the HIP backend")
+        sub = np.minimum(sub, np.uint8(nb))
+        skip = 1
+    nbp = nb + skip  # bins of the histogram planes
     dev = torch.device("cuda")
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]  # around the partition
     b_fm = torch.from_numpy(sub).to(dev).t().contiguous()  # [K, N] feature-major
@@ -351,7 +378,7 @@ def find_best_splits_batched_host(bins, grad, nodes_era_rows, feature_subset, ma
     p = _hip.PbSplitParams(lambda_l2=float(lambda_l2), lambda_dro=float(lambda_dro),
                            direction_weight=float(direction_weight), era_alpha=max(0.0, float(era_alpha)),
                            min_samples_leaf=int(min_samples_leaf), k_cuts=int(k_cuts),
-                           cut_selection=1 if str(cut_selection) == "mass" else 0, reserved=0)
+                           cut_selection=1 if str(cut_selection) == "mass" else 0, skip_last_bin=skip)
     win = torch.zeros(M * _hip.CANDIDATE_DTYPE.itemsize, dtype=torch.uint8, device=dev)  # valid = 0
     tot_g = np.zeros((M, E), dtype=np.float32)
     sc_ms = [0.0]
@@ -365,13 +392,13 @@ def find_best_splits_batched_host(bins, grad, nodes_era_rows, feature_subset, ma
                                           _hip.stream_ptr()), "pb_pick_sequential")
         e1.record()
         # era totals [E][mx] after the prefix planes (pb_hist_build's layout)
-        off = (E * mx * K * (nb - 1) + 63) // 64 * 64
+        off = (E * mx * K * (nbp - 1) + 63) // 64 * 64
         tot_g[m0:m0 + U] = gp[off:off + E * mx].view(E, mx)[:, :U].t().cpu().numpy()
         sc_ms[0] += e0.elapsed_time(e1)
 
     times = {}
-    _score_node_chunks(lib, b_fm, K, N, int(b_fm.stride(0)), local, fid, K, vals, rows, R, nrs, nes, M, E, nb, T,
-                       p, _HOST_CHUNK, consume, "find_best_splits_batched", times)
+    _score_node_chunks(lib, b_fm, K, N, int(b_fm.stride(0)), local, fid, K, vals, rows, R, nrs, nes, M, E, nbp,
+                       T, p, _HOST_CHUNK, consume, "find_best_splits_batched", times)
     w = np.frombuffer(win.cpu().numpy().tobytes(), dtype=_hip.CANDIDATE_DTYPE)
     split = w["valid"] != 0
     # partition every node (nodes without a split go all left and are not read)

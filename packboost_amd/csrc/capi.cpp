@@ -111,7 +111,7 @@ int32_t max_nodes_at(const pb_ctx* c, int32_t depth) {
 }
 
 int32_t thresholds_per_feature(const pb_ctx* c, const pb_split_params* p) {
-    const int full = std::max(1, c->d.max_bins - 1);
+    const int full = std::max(1, c->d.max_bins - 1 - (p->skip_last_bin ? 1 : 0));
     if (p->k_cuts > 0 && p->k_cuts < full) return std::max(1, std::min(p->k_cuts, full));
     return full;
 }
@@ -538,22 +538,26 @@ int des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, const 
     if (depth < 0 || depth >= c->d.max_depth) return fail(PB_ERR_RANGE, "pb_des_score: depth out of range");
     if (max_nodes < max_nodes_at(c, depth))
         return fail(PB_ERR_INVALID, "pb_des_score: max_nodes below the frontier bound of this depth");
-    const int nb = c->d.max_bins;
+    const int nb = c->d.max_bins;  // bins of the planes
+    const int skip = p->skip_last_bin ? 1 : 0;
+    if (skip && nb < 3)
+        return fail(PB_ERR_INVALID, "pb_des_score: skip_last_bin needs a context of max_bins >= 3");
     const int T = thresholds_per_feature(c, p);
-    const int full = std::max(1, nb - 1);
+    const int full = std::max(1, nb - skip - 1);
     const int32_t* thr_tab = nullptr;
     if (p->k_cuts > 0 && p->k_cuts < full) {
         PB_HIP(pb::launch_kcuts(reinterpret_cast<const uint16_t*>(hist_cnt),
                                 c->cnt32 ? reinterpret_cast<const uint32_t*>(hist_cnt) : nullptr,
                                 hist_cnt + pb::plane_tot_off(c->d.num_eras, max_nodes, K, nb),
-                                c->d.num_eras, max_nodes, K, nb, p->k_cuts,
+                                c->d.num_eras, max_nodes, K, nb - skip, skip, p->k_cuts,
                                 p->cut_selection == 1 ? 1 : 0, c->st, depth, c->thr_tab,
                                 (hipStream_t)stream),
                "kcuts launch");
         thr_tab = c->thr_tab;
     }
-    const pb::ScoreShape sh = pb::score_shape(K, T, c->d.num_eras, max_nodes_at(c, depth),
-                                                    c->score_wgs);
+    const pb::ScoreShape sh = skip ? pb::score_shape_classic(K, T, c->d.num_eras)
+                                   : pb::score_shape(K, T, c->d.num_eras, max_nodes_at(c, depth),
+                                                     c->score_wgs);
     const int64_t grid = (int64_t)sh.ntiles * max_nodes_at(c, depth);
     if (grid > INT32_MAX) return fail(PB_ERR_UNSUPPORTED, "pb_des_score: grid too large");
     if (sh.ntiles * sh.wpt > c->wmax) return fail(PB_ERR_INVALID, "pb_des_score: candidate buffer too small");
@@ -594,6 +598,7 @@ int des_score(pb_ctx* c, const int32_t* hist_cnt, const float* hist_grad, const 
     a.staged = c->score_staged;
     a.pc_classic = c->score_pc_classic;
     a.seq = c->seq;
+    a.skip_last = skip;
     c->last_w = sh.ntiles * sh.wpt;
     c->last_K = K;
     c->last_T = T;
@@ -793,6 +798,8 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
         return fail(PB_ERR_INVALID, "pb_grow_round: the nibble bin layout needs max_bins <= 16");
     if (nib && (reinterpret_cast<uintptr_t>(b->bins4_dev) & 15))
         return fail(PB_ERR_INVALID, "pb_grow_round: bins4 must be 16-byte aligned");
+    if (b->params.skip_last_bin)
+        return fail(PB_ERR_UNSUPPORTED, "pb_grow_round: bins must lie below max_bins (skip_last_bin 0)");
     const bool seg = c->seg_mode;
     if (seg) {
         const int32_t full = std::max(1, c->d.max_bins - 1);

@@ -219,6 +219,8 @@ struct ScoreArgs {
                              // for one pair per producer thread, else des_score_pc_kernel;
                              // 1 = des_score_pc_kernel always; 2 = des_score_pcu_kernel always
     SeqCands seq;            // every candidate, for the sequential pick
+    int32_t skip_last;       // 1: nb = the reference's num_bins + 1, the last bin its skipped
+                             // rows (pb_split_params.skip_last_bin); des_score_kernel only
 };
 
 // Launch shape of the scorer for K features and T thresholds (shared by the context's
@@ -228,15 +230,14 @@ struct ScoreShape {
     size_t lds_bytes;
 };
 ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t target_wgs);
+ScoreShape score_shape_classic(int32_t K, int32_t T, int32_t E);
 
 // Launchers (defined in the .hip files; all return hipError_t of the launch).
 hipError_t launch_hist(const HistArgs& a, int pairs, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s);
 hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt, int32_t E,
-                        int32_t U, int32_t K,
-                        int32_t nb,
-                        int32_t k, int32_t mass, const Frontier* st, int32_t depth,
-                        int32_t* thr_tab, hipStream_t s);
+                        int32_t U, int32_t K, int32_t nb, int32_t skip, int32_t k, int32_t mass,
+                        const Frontier* st, int32_t depth, int32_t* thr_tab, hipStream_t s);
 // The candidates of the depth the decision step picks from: the scorer's wavefront winners
 // (cand_w [U][W]) and every candidate in visiting order (seq, K features x T thresholds of the
 // ids feats / thresholds thr_tab, or 0..T-1 when thr_tab is null).

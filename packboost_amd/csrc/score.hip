@@ -142,8 +142,12 @@ struct PairIn {
     float Gt, GL;
 };
 
-// C32: the planes carry 32-bit counts (an era above 65535 rows)
-template <bool C32>
+// C32: the planes carry 32-bit counts (an era above 65535 rows). SKIP: the planes hold one bin
+// more than the reference's num_bins, the rows whose bin is >= num_bins (ScoreArgs.skip_last):
+// an era's totals for a feature are then its prefix through bin num_bins - 1 (the last plane
+// cell) while the era weight and the node's row and gradient totals stay those of all rows
+// (frontier_cpu.cpp:174-206, 278-281, 296-314).
+template <bool C32, bool SKIP>
 __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     extern __shared__ unsigned char smem[];
     const int tid = threadIdx.x;
@@ -178,6 +182,8 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
     const int nchunks = (a.E + EC - 1) / EC;
 
     PairIn pin[kPairs];
+    int cful[SKIP ? kPairs : 1];    // SKIP: the era's rows (all bins) and their gradient sum
+    float gful[SKIP ? kPairs : 1];
     auto prefetch = [&](int chunk) {
         const int e0 = chunk * EC;
         const int ne = min(EC, a.E - e0);
@@ -188,6 +194,10 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
             pin[i].L = 0;
             pin[i].Gt = 0.0f;
             pin[i].GL = 0.0f;
+            if (SKIP) {
+                cful[SKIP ? i : 0] = 0;
+                gful[SKIP ? i : 0] = 0.0f;
+            }
             if (pidx < ne * ncand) {
                 const int el = pidx / ncand;
                 const int c = pidx - el * ncand;
@@ -197,8 +207,15 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                 const int thr = a.thr_tab ? a.thr_tab[k * T + t] : t;
                 const int64_t off = (int64_t)(e0 + el) * estride + node_off + (int64_t)k * pt;
                 const int64_t to = (int64_t)(e0 + el) * a.U + u;
-                pin[i].ctot = a.tot_cnt[to];
-                pin[i].Gt = a.tot_g[to];
+                if (SKIP) {
+                    pin[i].ctot = C32 ? (int)a.cnt32[off + pt - 1] : (int)a.cnt[off + pt - 1];
+                    pin[i].Gt = a.g[off + pt - 1];
+                    cful[SKIP ? i : 0] = a.tot_cnt[to];
+                    gful[SKIP ? i : 0] = a.tot_g[to];
+                } else {
+                    pin[i].ctot = a.tot_cnt[to];
+                    pin[i].Gt = a.tot_g[to];
+                }
                 pin[i].L = C32 ? (int)a.cnt32[off + thr] : (int)a.cnt[off + thr];
                 pin[i].GL = a.g[off + thr];
             }
@@ -235,7 +252,7 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                     GL = pin[i].GL;
                     const int R = ctot - L;
                     const float GR = Gt - GL;
-                    const float wera = (alpha > 0.0f) ? ((float)ctot + alpha) : 1.0f;
+                    const float wera = (alpha > 0.0f) ? ((float)(SKIP ? cful[SKIP ? i : 0] : ctot) + alpha) : 1.0f;
                     const float w = (L > 0 && R > 0) ? wera : 0.0f;
                     if (w > 0.0f) {
                         const float dL = (float)L + lam;
@@ -256,9 +273,9 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                 sGL[el * cstride + c] = GL;
                 sL[el * cstride + c] = L;
                 sWD[el * cstride + c] = wd;
-                if (c == 0) {
-                    sCt[el] = ctot;
-                    sGt[el] = pin[i].Gt;
+                if (c == 0) {  // the node's totals over all of the era's rows
+                    sCt[el] = SKIP ? cful[SKIP ? i : 0] : ctot;
+                    sGt[el] = SKIP ? gful[SKIP ? i : 0] : pin[i].Gt;
                 }
             }
         }
@@ -1218,8 +1235,11 @@ __device__ void even_cuts(int nb, int k, int32_t* out) {
     while (m < kk) { out[m] = out[m - 1]; ++m; }
 }
 
+// skip: the planes hold nb + 1 bins, the last one the rows the reference leaves out of the
+// histogram (frontier_cpu.cpp:278-281); the mass then counts bins < nb only, the last of them
+// from the final plane cell instead of the (all-bins) era total.
 __global__ void kcuts_kernel(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt,
-                             int32_t E, int32_t U, int32_t K, int32_t nb,
+                             int32_t E, int32_t U, int32_t K, int32_t nb, int32_t skip,
                              int32_t k, int32_t mass, const Frontier* st, int32_t depth,
                              int32_t* thr_tab) {
     const int kf = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1238,11 +1258,13 @@ __global__ void kcuts_kernel(const uint16_t* cnt, const uint32_t* cnt32, const i
     // bin nb-1's running sum is the era total)
     long long cdf[256];
     for (int b = 0; b < nb; ++b) cdf[b] = 0;
+    const int pt = nb - 1 + (skip ? 1 : 0);  // plane cells per (era, node, feature)
     for (int e = 0; e < E; ++e)
         for (int u = 0; u < Ua; ++u) {
-            const int64_t base = (((int64_t)e * U + u) * K + kf) * (nb - 1);
+            const int64_t base = (((int64_t)e * U + u) * K + kf) * pt;
             for (int b = 0; b < nb - 1; ++b) cdf[b] += cnt32 ? cnt32[base + b] : cnt[base + b];
-            cdf[nb - 1] += tot_cnt[(int64_t)e * U + u];
+            cdf[nb - 1] += skip ? (cnt32 ? cnt32[base + nb - 1] : cnt[base + nb - 1])
+                                : tot_cnt[(int64_t)e * U + u];
         }
     const long long total = cdf[nb - 1];
     if (total <= 0) {
@@ -1913,6 +1935,20 @@ ScoreShape score_shape(int32_t K, int32_t T, int32_t E, int32_t nodes, int32_t t
     return sh;
 }
 
+// Launch shape of des_score_kernel for any T: one feature per workgroup, its T candidates on
+// the first T threads, eras staged in chunks of `ec` (about kPairs (candidate, era) pairs per
+// thread).
+ScoreShape score_shape_classic(int32_t K, int32_t T, int32_t E) {
+    ScoreShape sh;
+    sh.rt = std::max(2, std::min<int32_t>(E + 1, 4096));
+    sh.fts = 1;
+    sh.ntiles = K;
+    sh.wpt = (T + kWave - 1) / kWave;
+    sh.ec = std::max(1, (kPairs * kBlock) / std::max(1, T));
+    sh.lds_bytes = (size_t)sh.rt * 4 + 2 * ((size_t)sh.ec * T * 16 + (size_t)sh.ec * 8);
+    return sh;
+}
+
 // Launches kernel `fn` with `lds_bytes` of dynamic LDS (raising the limit past 64 KiB first).
 template <typename K>
 hipError_t launch_lds(K fn, int grid, int block, size_t lds_bytes, hipStream_t s, const ScoreArgs& a) {
@@ -1927,8 +1963,10 @@ hipError_t launch_lds(K fn, int grid, int block, size_t lds_bytes, hipStream_t s
 
 template <bool C32>
 hipError_t launch_score_c(const ScoreArgs& a, int grid, size_t lds_bytes, hipStream_t s) {
+    // rows past the reference's bins (score_shape_classic's launch shape)
+    if (a.skip_last) return launch_lds(des_score_kernel<C32, true>, grid, kBlock, lds_bytes, s, a);
     if (a.T >= kWave) {
-        if (a.staged) return launch_lds(des_score_kernel<C32>, grid, kBlock, lds_bytes, s, a);
+        if (a.staged) return launch_lds(des_score_kernel<C32, false>, grid, kBlock, lds_bytes, s, a);
         // the wide scorer computes 1/n (exact_recip) instead of a table; one thread per
         // threshold, whole wavefronts up to T (T <= 254)
         return launch_lds(des_score_wide_kernel<C32>, grid, (a.T + kWave - 1) / kWave * kWave, 0, s, a);
@@ -1955,12 +1993,12 @@ hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStrea
 }
 
 hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt, int32_t E,
-                        int32_t U, int32_t K, int32_t nb, int32_t k, int32_t mass, const Frontier* st,
-                        int32_t depth, int32_t* thr_tab, hipStream_t s) {
+                        int32_t U, int32_t K, int32_t nb, int32_t skip, int32_t k, int32_t mass,
+                        const Frontier* st, int32_t depth, int32_t* thr_tab, hipStream_t s) {
     const int threads = 64;
     const int grid = (K + threads - 1) / threads;
     hipLaunchKernelGGL(kcuts_kernel, dim3(grid), dim3(threads), 0, s, cnt, cnt32, tot_cnt, E, U, K,
-                       nb, k, mass, st, depth, thr_tab);
+                       nb, skip, k, mass, st, depth, thr_tab);
     return hipGetLastError();
 }
 

@@ -48,7 +48,7 @@ def split_params(cfg: PackBoostConfig) -> _hip.PbSplitParams:
     p.min_samples_leaf = int(cfg.min_samples_leaf)
     p.k_cuts = int(cfg.k_cuts)
     p.cut_selection = 1 if str(cfg.cut_selection) == "mass" else 0
-    p.reserved = 0
+    p.skip_last_bin = 0
     return p
 
 

@@ -35,6 +35,19 @@ def make_problem(seed: int, N: int, F: int, E: int, nb: int, U: int, *, inactive
             "era_off": offs.astype(np.int32), "N": N, "F": F, "E": E, "nb": nb, "U": U}
 
 
+def with_skipped_bins(p: dict, seed: int, frac: float = 0.08) -> dict:
+    """Sets a seeded `frac` of the bins to values >= nb (nb, nb + 3 and 255, the last being -1 as
+    the reference's int8), and every bin of feature 0 in era 1 to nb, so that the era has rows
+    but none in that feature's histogram."""
+    rng = np.random.default_rng(seed + 1000)
+    bins = p["bins"].copy()
+    nb = p["nb"]
+    hit = rng.random(bins.shape) < frac
+    bins[hit] = rng.choice(np.array([nb, min(255, nb + 3), 255], dtype=np.uint8), size=int(hit.sum()))
+    bins[p["era_off"][1]:p["era_off"][2], 0] = nb
+    return {**p, "bins": bins}
+
+
 def node_era_rows(p: dict) -> list[list[np.ndarray]]:
     nid, era = p["nid"].astype(np.int64), p["era"]
     out = []

@@ -76,7 +76,7 @@ def _c_layout() -> dict[str, int]:
 int main(void) {
   S(pb_dims) O(pb_dims, ld) O(pb_dims, num_features) O(pb_dims, min_samples_leaf)
   S(pb_split_params) O(pb_split_params, era_alpha) O(pb_split_params, min_samples_leaf)
-  O(pb_split_params, cut_selection)
+  O(pb_split_params, cut_selection) O(pb_split_params, skip_last_bin)
   S(pb_decision) O(pb_decision, score) O(pb_decision, left_count) O(pb_decision, node_grad)
   O(pb_decision, node_count)
   S(pb_candidate) O(pb_candidate, left_total) O(pb_candidate, valid)
@@ -106,7 +106,7 @@ def test_struct_layouts_match_header():
     for f in ("ld", "num_features", "min_samples_leaf"):
         assert c[f"pb_dims.{f}"] == getattr(_hip.PbDims, f).offset
     assert c["pb_split_params"] == ctypes.sizeof(_hip.PbSplitParams)
-    for f in ("era_alpha", "min_samples_leaf", "cut_selection"):
+    for f in ("era_alpha", "min_samples_leaf", "cut_selection", "skip_last_bin"):
         assert c[f"pb_split_params.{f}"] == getattr(_hip.PbSplitParams, f).offset
     assert c["pb_fit_buffers"] == ctypes.sizeof(_hip.PbFitBuffers)
     for f in ("values_dev", "pack_size", "learning_rate", "params"):

@@ -32,14 +32,24 @@ STAT_KEYS = {"nodes_processed", "nodes_skipped", "rows_total", "feature_blocks",
     (3, 7000, 12, 5, 128, 4, 9, 6, "even", 20, 0.0, 0.0, 0.0),
     (4, 5000, 8, 4, 255, 3, 8, 0, "mass", 3, 0.7, 0.2, 0.5),
     (5, 3000, 6, 3, 16, 40, 6, 0, "mass", 40, 0.0, 0.0, 0.3),
-], ids=["nb5", "nb32_kcuts_alpha_dir", "nb128_even_cuts", "nb255_alpha_dir", "40_nodes_msl40"])
+    # bins >= max_bins (skipped in the histogram, sent right: frontier_cpu.cpp:278-281, 464-470)
+    (6, 6000, 14, 6, 5, 6, 10, 0, "mass", 10, 0.0, 0.0, 0.4, True),
+    (7, 8000, 20, 9, 32, 5, 12, 4, "mass", 5, 1.5, 0.1, 0.4, True),
+    (8, 5000, 8, 4, 64, 3, 8, 0, "mass", 3, 0.7, 0.2, 0.5, True),
+    (9, 7000, 12, 5, 128, 4, 9, 6, "even", 20, 0.0, 0.0, 0.0, True),
+], ids=["nb5", "nb32_kcuts_alpha_dir", "nb128_even_cuts", "nb255_alpha_dir", "40_nodes_msl40",
+        "skipped_nb5", "skipped_nb32_kcuts_alpha_dir", "skipped_nb64_alpha_dir", "skipped_nb128_even_cuts"])
 def test_host_schema_split_finder(hip, oracle_mod, case):
     from packboost_amd import backends
+    from tests.helpers import with_skipped_bins
 
-    seed, N, F, E, nb, U, K, kc, cut, msl, alpha, dirw, dro = case
+    seed, N, F, E, nb, U, K, kc, cut, msl, alpha, dirw, dro = case[:13]
+    skipped = len(case) > 13 and case[13]
     print(f"[batched host] {case}", flush=True)
     assert backends.cpu_available()
     p = make_problem(seed, N, F, E, nb, U, empty_era=True)
+    if skipped:
+        p = with_skipped_bins(p, seed)
     ner = node_era_rows(p)
     ner.insert(1, [np.empty(0, np.int64) for _ in range(E)])  # a node without rows
     ner.append([])  # a node without eras
@@ -102,6 +112,18 @@ def test_host_schema_split_finder(hip, oracle_mod, case):
             np.testing.assert_array_equal(d["left_rows"][e], r[gl])
             np.testing.assert_array_equal(d["right_rows"][e], r[~gl])
             assert d["left_rows"][e].dtype == np.int64
+
+
+def test_host_schema_bins_past_254_bins(hip):
+    """With max_bins 255 a bin of 255 has no spare plane bin to go to: ValueError."""
+    from packboost_amd import backends
+
+    bins = np.zeros((10, 2), np.uint8)
+    bins[3, 1] = 255
+    ner = [[np.arange(10, dtype=np.int64)]]
+    with pytest.raises(ValueError, match="max_bins <= 254"):
+        backends.find_best_splits_batched(bins.view(np.int8), np.ones(10, np.float32), ner,
+                                          np.arange(2, dtype=np.int32), 255, 0, "mass", 1e-6, 0.0, 0.0, 0.0, 1)
 
 
 def test_host_schema_no_nodes_and_no_features(hip):

@@ -61,15 +61,23 @@ def _oracle_per_feature(cands):
     (2, 8000, 20, 9, 32, 5, 12, 5, 1.5, 0.1),
     (3, 6000, 10, 4, 128, 2, 10, 20, 0.0, 0.0),
     (4, 60000, 6, 3, 5, 4200, 3, 2, 0.0, 0.0),
-], ids=["nb5", "nb32_alpha_dir", "nb128", "4200_nodes_two_chunks"])
+    # bins >= max_bins: left out of the histogram (frontier_cuda.cu:451, frontier_cpu.cpp:278-281)
+    (5, 5000, 12, 6, 5, 3, 8, 10, 0.0, 0.0, True),
+    (6, 8000, 20, 9, 32, 5, 12, 5, 1.5, 0.1, True),
+    (7, 6000, 10, 4, 128, 2, 10, 20, 0.0, 0.0, True),
+], ids=["nb5", "nb32_alpha_dir", "nb128", "4200_nodes_two_chunks", "skipped_nb5",
+        "skipped_nb32_alpha_dir", "skipped_nb128"])
 def test_split_finder_rowlist(hip, oracle_mod, case):
     import torch
 
     from packboost_amd import backends
+    from tests.helpers import with_skipped_bins
 
-    seed, N, F, E, nb, U, K, msl, alpha, dirw = case
+    seed, N, F, E, nb, U, K, msl, alpha, dirw = case[:10]
     print(f"[rowlist split] {case}", flush=True)
     p = make_problem(seed, N, F, E, nb, U)
+    if len(case) > 10 and case[10]:
+        p = with_skipped_bins(p, seed)
     ner = node_era_rows(p)
     feats = np.random.default_rng(seed).permutation(F)[:K].astype(np.int32)
     ref = oracle_mod.split_batch(p["bins"], p["grad"], ner, feats, nb, lambda_l2=1e-3, lambda_dro=0.4,

@@ -40,11 +40,36 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES, ids=[f"case{c[0]}" for c in CASES])
 def test_oracle_matches_reference_cpu(oracle_mod, case):
-    ref = _load_ref()
-    from tests.helpers import make_problem, node_era_rows
+    from tests.helpers import make_problem
 
     seed, N, F, E, nb, U, K, kc, cut, msl, lam, dro, dw, alpha = case
     p = make_problem(seed, N, F, E, nb, U, empty_era=(seed % 2 == 0))
+    _compare(oracle_mod, p, case)
+
+
+SKIP_CASES = [
+    # bins >= max_bins: skipped in the histogram, sent right (frontier_cpu.cpp:278-281, 464-470)
+    (11, 3000, 8, 5, 5, 2, 8, 0, "mass", 10, 1e-6, 0.5, 0.0, 0.0),
+    (12, 4000, 10, 7, 32, 3, 10, 6, "mass", 5, 1e-3, 0.1, 0.0, 0.0),
+    (13, 4000, 10, 7, 16, 3, 10, 0, "mass", 5, 1e-3, 0.1, 0.2, 1.5),
+]
+
+
+@pytest.mark.parametrize("case", SKIP_CASES, ids=[f"case{c[0]}" for c in SKIP_CASES])
+def test_oracle_matches_reference_with_skipped_bins(oracle_mod, case):
+    from tests.helpers import make_problem, with_skipped_bins
+
+    seed, N, F, E, nb, U, K, kc, cut, msl, lam, dro, dw, alpha = case
+    p = with_skipped_bins(make_problem(seed, N, F, E, nb, U, empty_era=True), seed)
+    assert int(p["bins"].max()) >= nb
+    _compare(oracle_mod, p, case)
+
+
+def _compare(oracle_mod, p, case):
+    ref = _load_ref()
+    from tests.helpers import node_era_rows
+
+    seed, N, F, E, nb, U, K, kc, cut, msl, lam, dro, dw, alpha = case
     feats = np.random.default_rng(seed).permutation(F)[:K].astype(np.int32)
     ner = node_era_rows(p)
     got = oracle_mod.split_batch(p["bins"], p["grad"], ner, feats, nb, kc, cut, lam, dro, dw, alpha, msl)
