@@ -13,9 +13,10 @@ bytes this build's layouts move per launch (bin codes at half a byte per row in 
 layout, grad f32 and a 2-byte node id per row, the compact planes written) over the average
 launch time from HIP events on the fit's stream; beside it the same time priced in the
 reference's formats (one byte per bin code, 8 bytes of row state, 8 bytes per histogram cell),
-and the HBM traffic rocprofv3 measured. The CPU baseline is the reference's own compiled
-frontier (frontier_cpu.cpp, oracle/_ref) under the oracle's restated fit loop, timed on a
-bounded row sample on the host cores (the C restatement when oracle/_ref is absent).
+and the HBM traffic rocprofv3 measured. The CPU baseline is the oracle's C restatement of the
+reference's CPU split finder (frontier_cpu.cpp) under its restated fit loop, on the host cores,
+at two bounded row samples extrapolated to the full rows (--cpu-full: rounds 1-3 at full size),
+with the build container's reference/restatement timing ratio (oracle/calibration.json).
 """
 
 from __future__ import annotations
@@ -112,41 +113,82 @@ def host_cpu() -> dict:
     }
 
 
-def cpu_baseline(c: dict, budget_s: float = 12.0, sample_rows: int | None = None) -> dict:
-    """The reference CPU path on a bounded row sample: the oracle's restated fit loop with each
-    depth's split finder run by the reference's own compiled frontier (frontier_cpu.cpp, OpenMP
-    over nodes, built into oracle/_ref), or by the C restatement when that is not built."""
+def _calibration() -> list | None:
+    """oracle/calibration.json: the build container's timing of the reference's own splitter
+    against the restatement under the same fit loop (oracle/calibrate.py --write)."""
+    path = ROOT / "oracle" / "calibration.json"
+    try:
+        return json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(c: dict, budget_s: float = 12.0, full: bool = False) -> dict:
+    """The reference's CPU path as it runs on the GPU box: the oracle's C restatement of its split
+    finder (frontier_cpu.cpp:111-515: row-major int8 bins, serial over the sampled features,
+    OpenMP over nodes) under the restated fit loop (booster.py:375-599), steady-state seconds
+    per round (rounds 2.., the span of round_seconds, booster.py:495, 654). The reference itself
+    is not run here; the container-measured ratio of the two (oracle/calibration.json) rides in
+    the line.
+
+    Default: rounds at two row samples n1 = N/40 and n2 = N/20 (E * 25 / E * 50 rows at least),
+    extrapolated linearly in rows to N. A round's histogram and partition work grow with the
+    rows; its scan and scoring (nodes x eras x features x thresholds) do not, so scaling one
+    sample by N / n would overstate a full round. full=True times rounds 1-3 at N rows."""
     from oracle import oracle as ref
 
     N, F, E, nb = c["rows"], c["features"], c["eras"], c["bins"]
-    n_s = sample_rows or max(E * 50, N // 20)
-    rng = np.random.default_rng(0)
-    bins = rng.integers(0, nb, size=(n_s, F), dtype=np.uint8)
-    y = (rng.integers(0, 5, size=n_s) / 4.0).astype(np.float32)
-    codes = np.repeat(np.arange(E), np.diff(era_offsets(n_s, E)))
-    splitter = "reference" if ref.ref_module() is not None else "restated"
-    gen = __import__("torch").Generator().manual_seed(42)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 6 and (len(times) < 2 or time.perf_counter() - t_start < budget_s):
-        r = ref.fit(bins, y, codes, num_rounds=1, pack_size=c["pack_size"], max_depth=c["max_depth"],
-                    learning_rate=c["lr"], lambda_l2=c["lambda_l2"], lambda_dro=c["lambda_dro"],
-                    min_samples_leaf=c["msl"], max_bins=nb, layer_feature_fraction=c["frac"], rng=gen,
-                    splitter=splitter)
-        times.append(r.round_seconds[0])
-    steady = times[1:] if len(times) > 1 else times
-    sec = float(np.mean(steady))
-    return {
-        "value": (n_s / N) / sec,
+    threads = int(ref.lib().oracle_num_threads())
+
+    def steady_at(n: int, max_rounds: int, budget: float) -> tuple[float, int]:
+        rng = np.random.default_rng(0)
+        bins = rng.integers(0, nb, size=(n, F), dtype=np.uint8)
+        y = (rng.integers(0, 5, size=n) / 4.0).astype(np.float32)
+        codes = np.repeat(np.arange(E), np.diff(era_offsets(n, E)))
+        gen = __import__("torch").Generator().manual_seed(42)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < max_rounds and (len(times) < 3 or time.perf_counter() - t_start < budget):
+            r = ref.fit(bins, y, codes, num_rounds=1, pack_size=c["pack_size"], max_depth=c["max_depth"],
+                        learning_rate=c["lr"], lambda_l2=c["lambda_l2"], lambda_dro=c["lambda_dro"],
+                        min_samples_leaf=c["msl"], max_bins=nb, layer_feature_fraction=c["frac"], rng=gen,
+                        splitter="restated")
+            times.append(r.round_seconds[0])
+        return float(np.mean(times[1:])), len(times) - 1
+
+    if full:
+        sec, k = steady_at(N, 3, 0.0)
+        sample = (f"full size: {N} rows x {F} features (row-major int8), {E} eras, rounds 1-3, "
+                  f"steady rounds 2-3 mean {sec:.2f} s")
+    else:
+        n1, n2 = max(E * 25, N // 40), max(E * 50, N // 20)
+        s1, k1 = steady_at(n1, 5, budget_s / 3)
+        s2, k2 = steady_at(n2, 5, 2 * budget_s / 3)
+        slope = (s2 - s1) / (n2 - n1)
+        sec = s2 + slope * (N - n2) if slope > 0 else s2 * N / n2
+        sample = (f"{n1} and {n2} rows x {F} features (row-major int8), {E} eras, full "
+                  f"{c['max_depth']}-depth rounds: steady {s1:.3f} s ({k1} rounds) and {s2:.3f} s "
+                  f"({k2} rounds), extrapolated linearly in rows to {N}: {sec:.2f} s per round")
+    out = {
+        "value": 1.0 / sec,
         "unit": "rounds/s",
-        "cores": int(ref.lib().oracle_num_threads()),
-        "kind": "reference" if splitter == "reference" else "port",
-        "sample": (f"{n_s} rows x {F} features (row-major int8), {E} eras, full {c['max_depth']}-depth "
-                   f"rounds; {'reference frontier_cpu.cpp' if splitter == 'reference' else 'C restatement'}"
-                   f" under the restated fit loop; mean of {len(steady)} rounds = {sec:.3f} s, "
-                   f"scaled by rows {n_s}/{N}"),
+        "cores": threads,
+        "kind": "port",
+        "sample": sample + "; C restatement of frontier_cpu.cpp under the restated fit loop",
         "host": host_cpu(),
     }
+    cal = _calibration()
+    if cal:
+        ratios = {r["workload"]: r["reference_over_restated"] for r in cal}
+        out["calibration"] = {
+            "reference_over_restated_s_per_round": ratios,
+            "identical_trees": all(r.get("identical_trees") for r in cal),
+            "measured": f"oracle/calibrate.py in the build container ({cal[0].get('cpu')}, "
+                        f"{cal[0].get('omp_threads')} threads)",
+        }
+        if "config3_slice" in ratios:
+            out["calibration"]["reference_estimate_value"] = out["value"] / ratios["config3_slice"]
+    return out
 
 
 def profiled_traffic(config: int, rows: int, summary: str = "hist_score") -> float | None:
@@ -311,6 +353,8 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=0, help="override row count (quick runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="CPU baseline from rounds 1-3 at the full size (minutes) instead of two samples")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (counter calibration)")
     args = ap.parse_args()
@@ -514,8 +558,8 @@ def main() -> int:
     del bins
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline and args.config == 3:
-        print("[bench] timing the reference CPU frontier on a row sample", file=sys.stderr, flush=True)
-        out["cpu_baseline"] = cpu_baseline(c, args.cpu_budget)
+        print("[bench] timing the CPU restatement of the reference frontier", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(c, args.cpu_budget, full=args.cpu_full)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -91,11 +91,15 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--rounds", type=int, default=3)
     ap.add_argument("--workloads", default="config2,config3_slice")
+    ap.add_argument("--write", action="store_true",
+                    help="also write the records to oracle/calibration.json (read by bench.py's "
+                         "cpu_baseline leg on the GPU box, where the reference is not run)")
     args = ap.parse_args()
     if om.ref_module() is None:
         print("oracle/_ref is not built: run `make -C oracle ref`", file=sys.stderr)
         return 2
     threads = int(om.lib().oracle_num_threads())
+    records = []
     for name in args.workloads.split(","):
         bins, y, era, kw = config2() if name == "config2" else config3_slice()
         res = {}
@@ -106,13 +110,19 @@ def main() -> int:
                   file=sys.stderr, flush=True)
         (ra, sa), (rb, sb) = res["restated"], res["reference"]
         same = all(np.array_equal(a[k], b[k]) for a, b in zip(ra.rounds, rb.rounds) for k in a)
-        print(json.dumps({
+        rec = {
             "workload": name, "rows": int(bins.shape[0]), "features": int(bins.shape[1]),
             "rounds": args.rounds, "omp_threads": threads, "torch_threads": torch.get_num_threads(),
             "restated_s_per_round": round(sa, 4), "reference_s_per_round": round(sb, 4),
             "reference_over_restated": round(sb / sa, 3), "identical_trees": bool(same),
             "cpu": os.popen("lscpu | grep 'Model name'").read().split(":", 1)[-1].strip(),
-        }), flush=True)
+        }
+        records.append(rec)
+        print(json.dumps(rec), flush=True)
+    if args.write:
+        path = ROOT / "oracle" / "calibration.json"
+        path.write_text(json.dumps(records, indent=1) + "\n")
+        print(f"wrote {path}", file=sys.stderr)
     return 0
 
 
