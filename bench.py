@@ -154,6 +154,7 @@ def cpu_baseline(c: dict, budget_s: float = 12.0, full: bool = False) -> dict:
                         min_samples_leaf=c["msl"], max_bins=nb, layer_feature_fraction=c["frac"], rng=gen,
                         splitter="restated")
             times.append(r.round_seconds[0])
+            print(f"[bench] cpu round {len(times)} at {n} rows: {times[-1]:.2f} s", file=sys.stderr, flush=True)
         return float(np.mean(times[1:])), len(times) - 1
 
     if full:
