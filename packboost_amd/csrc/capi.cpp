@@ -64,6 +64,7 @@ struct pb_ctx {
     bool seg_mode;
     int32_t seg_from;           // first depth scored by the fused kernel
     int32_t seg_ft;             // cap on the fused kernel's features per workgroup (0: rule)
+    int32_t seg_major_nodes;    // frontier bound from which the fused kernel runs tile-major
     int32_t seg_cur;            // buffer set holding the current depth's rows
     pb::SegBuffers sb[2];
     int32_t* seg[2];            // [E][segw] segment starts of the rows in sb[i]
@@ -696,6 +697,7 @@ int seg_score(pb_ctx* c, const uint8_t* bins, const int32_t* feats, int32_t K, i
     a.seq = c->seq;
     a.ntot = c->ntot;
     a.rt = std::max(2, std::min<int32_t>(a.E + 1, 4096));
+    a.tile_major = max_nodes >= c->seg_major_nodes ? 1 : 0;
     if (a.ntiles * a.wpt > c->wmax) return fail(PB_ERR_INVALID, "segment scorer: candidate buffer too small");
     c->last_w = a.ntiles * a.wpt;
     c->last_K = K;
@@ -778,6 +780,8 @@ int pb_set_segment_mode(pb_ctx* c, int32_t enable, int32_t from_depth) {
     c->ss.rules = c->rules;
     c->seg_from = std::min<int32_t>(from, c->d.max_depth);
     c->seg_ft = (int32_t)env_int("PB_SEG_FT", 0);
+    // tile-major block order from this many frontier nodes on (PB_SEG_MAJOR)
+    c->seg_major_nodes = (int32_t)std::max<long long>(1, env_int("PB_SEG_MAJOR", 32));
     if (c->seg_ft != 0 && c->seg_ft != 1 && c->seg_ft != 2 && c->seg_ft != 4)
         return fail(PB_ERR_INVALID, "pb_set_segment_mode: PB_SEG_FT must be 1, 2 or 4");
     c->seg_mode = true;

@@ -281,6 +281,8 @@ struct SegScoreArgs {
     SeqCands seq;
     NodeTotal* ntot;
     int32_t rt;            // size of the 1/n table (equal era weights)
+    int32_t mu;            // node slots per tile in the grid (the launch's max_nodes)
+    int32_t tile_major;    // 1: XCD-aware tile-major block order (nodes fastest), 0: node-major
 };
 constexpr int kSegMaxFt = 4;  // 8 measured slower: 123 VGPRs hold it to 4 waves per SIMD (FT 4: 6)
 // The sorted rows of segment mode: per row its gradient, original row id and tree node id.

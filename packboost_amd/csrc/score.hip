@@ -1681,10 +1681,24 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(seg_wave
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1);
     const int wave = tid / kWave;
-    const int u = blockIdx.x / a.ntiles;
-    const int tile = blockIdx.x - u * a.ntiles;
+    // blockIdx -> (node, feature tile). tile_major (many nodes): XCD-aware, the 8 XCDs take
+    // blocks round-robin and XCD x walks tiles x, x + 8, ... with the node fastest. The
+    // workgroups resident on one XCD at a time are then mostly all the nodes of one tile: they
+    // gather the same columns' lines era by era (a deep node holds one row in tens of a line's),
+    // so the XCD's L2 serves each line to every node instead of each node fetching it.
+    // Otherwise node-major: a node's tiles are consecutive blocks.
+    int u, tile;
+    if (a.tile_major) {
+        const int i = (int)(blockIdx.x >> 3);
+        const int jt = i / a.mu;
+        u = i - jt * a.mu;
+        tile = (int)(blockIdx.x & 7) + 8 * jt;
+    } else {
+        u = (int)blockIdx.x / a.ntiles;
+        tile = (int)blockIdx.x - u * a.ntiles;
+    }
     const int Ua = a.st->u_active[a.depth];
-    if (u >= Ua) return;
+    if (u >= Ua || tile >= a.ntiles) return;
     const int k0 = tile * FT;
     const int nf = min(FT, a.K - k0);
     if (nf <= 0) return;
@@ -2042,8 +2056,13 @@ size_t seg_score_lds_bytes(int32_t fts, int32_t rt) {
     return (size_t)fts * 256 * (8 + 4 + 4) + 4 * 4 + (size_t)rt * 4;
 }
 
-hipError_t launch_seg_score(const SegScoreArgs& a, int32_t max_nodes, hipStream_t s) {
-    const int64_t grid = (int64_t)max_nodes * a.ntiles;
+hipError_t launch_seg_score(const SegScoreArgs& args, int32_t max_nodes, hipStream_t s) {
+    SegScoreArgs a = args;
+    a.mu = max_nodes;
+    // tile_major: every XCD gets ceil(ntiles / 8) tiles x max_nodes blocks (past the last tile
+    // they exit)
+    const int64_t grid = a.tile_major ? 8 * (int64_t)((a.ntiles + 7) / 8) * max_nodes
+                                      : (int64_t)max_nodes * a.ntiles;
     if (grid <= 0) return hipSuccess;
     if (grid > INT32_MAX || a.T > 254 || a.T != a.nb - 1) return hipErrorInvalidValue;
     const size_t lds = seg_score_lds_bytes(a.fts, a.rt);
