@@ -47,11 +47,10 @@ def compile_flags() -> list[str]:
     ]
 
 
-# Kernels that must not use scratch (register spills): the histogram and the scorers. One build
-# of the single-feature histogram tile that spilled returned wrong plane counts for a code
-# generation it took only with the spills, so a spill here fails the build. (kcuts_kernel keeps
-# per-lane arrays in scratch by design.)
-NO_SCRATCH = re.compile(r"hist_era_kernel|seg_score_kernel|des_score")
+# Kernels that must not use scratch (register spills): the histogram, the scorers and the K-cut
+# selection. One build of the single-feature histogram tile that spilled returned wrong plane
+# counts for a code generation it took only with the spills, so a spill here fails the build.
+NO_SCRATCH = re.compile(r"hist_era_kernel|seg_score_kernel|des_score|kcuts_kernel")
 
 
 def spilling_kernels(remarks: str) -> list[str]:

@@ -1235,78 +1235,110 @@ __device__ void even_cuts(int nb, int k, int32_t* out) {
     while (m < kk) { out[m] = out[m - 1]; ++m; }
 }
 
+// K-cut thresholds per feature (frontier_cpu.cpp:36-101, 322-330): even cuts, or mass cuts
+// from the feature's count distribution over the depth's nodes and eras. One workgroup per
+// feature (kKcutsBlock threads):
+//   (1) cdf[b] = sum over (era, node) of the plane's prefix count of bin b (the planes hold
+//       running sums over the bins, so these are the cumulative counts; bin nb-1's is the era
+//       total). Thread t sums bin t % nb over every (1024 / nb)-th (era, node) pair in a
+//       register, then adds it into the LDS cdf once.
+//   (2) thread i < kk takes the lower bound of target i over cdf;
+//   (3) thread 0 de-duplicates and tops up with even cuts (at most 2 x 254 values).
 // skip: the planes hold nb + 1 bins, the last one the rows the reference leaves out of the
 // histogram (frontier_cpu.cpp:278-281); the mass then counts bins < nb only, the last of them
 // from the final plane cell instead of the (all-bins) era total.
-__global__ void kcuts_kernel(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt,
-                             int32_t E, int32_t U, int32_t K, int32_t nb, int32_t skip,
-                             int32_t k, int32_t mass, const Frontier* st, int32_t depth,
-                             int32_t* thr_tab) {
-    const int kf = blockIdx.x * blockDim.x + threadIdx.x;
+constexpr int kKcutsBlock = 1024;
+
+__global__ __launch_bounds__(kKcutsBlock) void kcuts_kernel(const uint16_t* cnt, const uint32_t* cnt32,
+                                                           const int32_t* tot_cnt, int32_t E, int32_t U,
+                                                           int32_t K, int32_t nb, int32_t skip, int32_t k,
+                                                           int32_t mass, const Frontier* st, int32_t depth,
+                                                           int32_t* thr_tab) {
+    const int kf = blockIdx.x;
     if (kf >= K) return;
+    const int tid = threadIdx.x;
     const int max_thr = max(1, nb - 1);
     const int kk = max(1, min(k, max_thr));
     int32_t* out = thr_tab + (int64_t)kf * kk;
-    int32_t buf[512];
+    __shared__ unsigned long long cdf[256];
+    __shared__ int32_t buf[512];
+    __shared__ int32_t ev[256];
     if (!mass) {
-        even_cuts(nb, k, buf);
-        for (int i = 0; i < kk; ++i) out[i] = buf[i];
+        if (tid == 0) {
+            even_cuts(nb, k, buf);
+            for (int i = 0; i < kk; ++i) out[i] = buf[i];
+        }
         return;
     }
+    for (int b = tid; b < 256; b += kKcutsBlock) cdf[b] = 0ull;
+    __syncthreads();
     const int Ua = st->u_active[depth];
-    // cdf[b] = sum over nodes, eras of count of bin b (planes hold running sums over bins;
-    // bin nb-1's running sum is the era total)
-    long long cdf[256];
-    for (int b = 0; b < nb; ++b) cdf[b] = 0;
     const int pt = nb - 1 + (skip ? 1 : 0);  // plane cells per (era, node, feature)
-    for (int e = 0; e < E; ++e)
-        for (int u = 0; u < Ua; ++u) {
-            const int64_t base = (((int64_t)e * U + u) * K + kf) * pt;
-            for (int b = 0; b < nb - 1; ++b) cdf[b] += cnt32 ? cnt32[base + b] : cnt[base + b];
-            cdf[nb - 1] += skip ? (cnt32 ? cnt32[base + nb - 1] : cnt[base + nb - 1])
-                                : tot_cnt[(int64_t)e * U + u];
+    const int G = kKcutsBlock / nb;          // pairs summed side by side per bin (nb <= 255)
+    if (tid < G * nb) {
+        const int b = tid % nb;
+        const int g = tid / nb;
+        unsigned long long acc = 0ull;
+        const int P = E * Ua;
+        // four pairs per step, their loads issued together
+        for (int p0 = g; p0 < P; p0 += 4 * G) {
+            unsigned long long v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int pi = p0 + q * G;
+                v[q] = 0ull;
+                if (pi < P) {
+                    const int e = pi / Ua;
+                    const int u = pi - e * Ua;
+                    const int64_t base = (((int64_t)e * U + u) * K + kf) * pt;
+                    if (b < nb - 1)
+                        v[q] = cnt32 ? cnt32[base + b] : cnt[base + b];
+                    else
+                        v[q] = skip ? (cnt32 ? cnt32[base + nb - 1] : cnt[base + nb - 1])
+                                    : (unsigned long long)tot_cnt[(int64_t)e * U + u];
+                }
+            }
+            acc += (v[0] + v[1]) + (v[2] + v[3]);
         }
-    const long long total = cdf[nb - 1];
-    if (total <= 0) {
-        even_cuts(nb, k, buf);
-        for (int i = 0; i < kk; ++i) out[i] = buf[i];
+        atomicAdd(&cdf[b], acc);
+    }
+    __syncthreads();
+    const long long total = (long long)cdf[nb - 1];
+    if (total <= 0) {  // uniform: every thread reads the same cdf
+        if (tid == 0) {
+            even_cuts(nb, k, buf);
+            for (int i = 0; i < kk; ++i) out[i] = buf[i];
+        }
         return;
     }
     const double upper = (double)total * (1.0 - 1e-12);
-    int n = 0;
-    for (int i = 0; i < kk; ++i) {
+    for (int i = tid; i < kk; i += kKcutsBlock) {
         const double alpha = (kk == 1) ? 0.0 : (double)i / (double)(kk - 1);
         const double target = upper * alpha;
         int idx = nb - 1;  // lower_bound over cdf; end() -> last index
         for (int b = 0; b < nb; ++b)
-            if (!((double)cdf[b] < target)) { idx = b; break; }
-        buf[n++] = max(0, min(idx - 1, max_thr - 1));
+            if (!((double)(long long)cdf[b] < target)) { idx = b; break; }
+        buf[i] = max(0, min(idx - 1, max_thr - 1));
     }
-    // sort (insertion; kk <= 254) + unique
-    for (int i = 1; i < n; ++i) {
-        const int v = buf[i];
-        int q = i - 1;
-        while (q >= 0 && buf[q] > v) { buf[q + 1] = buf[q]; --q; }
-        buf[q + 1] = v;
-    }
+    __syncthreads();
+    if (tid != 0) return;
+    // buf[0..kk) ascends with the targets (the reference sorts it, which keeps it); unique, then
+    // top up with the even cuts: the sorted, de-duplicated union (frontier_cpu.cpp:86-101),
+    // formed by one merge of the two ascending lists
     int m = 0;
-    for (int i = 0; i < n; ++i)
+    for (int i = 0; i < kk; ++i)
         if (m == 0 || buf[m - 1] != buf[i]) buf[m++] = buf[i];
-    // top up with even cuts, re-sorting and de-duplicating (frontier_cpu.cpp:93-101)
-    int32_t ev[256];
     if (m < kk) {
         even_cuts(nb, kk, ev);
-        for (int i = 0; i < kk; ++i) buf[m + i] = ev[i];
-        n = m + kk;
-        for (int i = 1; i < n; ++i) {
-            const int v = buf[i];
-            int q = i - 1;
-            while (q >= 0 && buf[q] > v) { buf[q + 1] = buf[q]; --q; }
-            buf[q + 1] = v;
+        int32_t* mg = buf + 256;  // the merge's output, after buf's m values
+        int ia = 0, ib = 0, n = 0;
+        while (ia < m || ib < kk) {
+            const bool take_a = ib >= kk || (ia < m && buf[ia] <= ev[ib]);
+            const int v = take_a ? buf[ia++] : ev[ib++];
+            if (n == 0 || mg[n - 1] != v) mg[n++] = v;
         }
-        m = 0;
-        for (int i = 0; i < n; ++i)
-            if (m == 0 || buf[m - 1] != buf[i]) buf[m++] = buf[i];
+        for (int i = 0; i < n; ++i) buf[i] = mg[i];
+        m = n;
     }
     for (int i = 0; i < kk; ++i) {
         const int v = (i < m) ? buf[i] : buf[m - 1];
@@ -2009,9 +2041,8 @@ hipError_t launch_score(const ScoreArgs& a, int grid, size_t lds_bytes, hipStrea
 hipError_t launch_kcuts(const uint16_t* cnt, const uint32_t* cnt32, const int32_t* tot_cnt, int32_t E,
                         int32_t U, int32_t K, int32_t nb, int32_t skip, int32_t k, int32_t mass,
                         const Frontier* st, int32_t depth, int32_t* thr_tab, hipStream_t s) {
-    const int threads = 64;
-    const int grid = (K + threads - 1) / threads;
-    hipLaunchKernelGGL(kcuts_kernel, dim3(grid), dim3(threads), 0, s, cnt, cnt32, tot_cnt, E, U, K,
+    if (K <= 0) return hipSuccess;
+    hipLaunchKernelGGL(kcuts_kernel, dim3(K), dim3(kKcutsBlock), 0, s, cnt, cnt32, tot_cnt, E, U, K,
                        nb, skip, k, mass, st, depth, thr_tab);
     return hipGetLastError();
 }

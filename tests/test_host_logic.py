@@ -154,16 +154,18 @@ def test_draw_window_matches_sequential_draws():
 
 
 def test_build_rejects_spilling_hot_kernels():
-    """packboost_amd.build fails a build in which a histogram or scorer kernel spills registers
-    (hipcc's kernel-resource-usage remarks report its scratch), and lets other kernels keep
-    scratch arrays."""
+    """packboost_amd.build fails a build in which a histogram, scorer or K-cut kernel spills
+    registers (hipcc's kernel-resource-usage remarks report its scratch), and lets other kernels
+    keep scratch arrays."""
     from packboost_amd.build import spilling_kernels
 
     r = "\n".join([
         "a.hip:1:1: remark: Function Name: _ZN2pb12_GLOBAL__N_115hist_era_kernelILi16ELi1ELb0ELi256EEEvNS_8HistArgsE",
         "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 20 [-Rpass-analysis=kernel-resource-usage]",
-        "a.hip:2:1: remark: Function Name: _ZN2pb12_GLOBAL__N_112kcuts_kernelEPKt",
+        "a.hip:2:1: remark: Function Name: _ZN2pb12_GLOBAL__N_117forest_tile_kernelEv",
         "a.hip:2:1: remark:     ScratchSize [bytes/lane]: 5136 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:5:1: remark: Function Name: _ZN2pb12_GLOBAL__N_112kcuts_kernelEPKt",
+        "a.hip:5:1: remark:     ScratchSize [bytes/lane]: 16 [-Rpass-analysis=kernel-resource-usage]",
         "a.hip:3:1: remark: Function Name: _ZN2pb12_GLOBAL__N_116seg_score_kernelILi4ELb0ELb1EEEvNS_12SegScoreArgsE",
         "a.hip:3:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
         "a.hip:4:1: remark: Function Name: _ZN2pb12_GLOBAL__N_120des_score_pcu_kernelILb0ELi8ELi2EEEvNS_9ScoreArgsE",
@@ -171,5 +173,6 @@ def test_build_rejects_spilling_hot_kernels():
     ])
     assert spilling_kernels(r) == [
         "_ZN2pb12_GLOBAL__N_115hist_era_kernelILi16ELi1ELb0ELi256EEEvNS_8HistArgsE",
+        "_ZN2pb12_GLOBAL__N_112kcuts_kernelEPKt",
         "_ZN2pb12_GLOBAL__N_120des_score_pcu_kernelILb0ELi8ELi2EEEvNS_9ScoreArgsE",
     ]
