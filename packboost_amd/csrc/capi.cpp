@@ -378,15 +378,19 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     // first, then as many histogram copies as fit in half of that.
     int P = (nb <= 16 && K >= 2) ? 2 : 1;
     // feature triples while their joint histogram stays small (at most 512 cells per copy:
-    // depths 0-2 at 5 bins), where a third fewer atomics beat the larger flush
-    if (nb <= 6 && K >= 3 && (int64_t)max_nodes * nb * nb * nb <= 512) P = 3;
+    // depths 0-2 at 5 bins), where a third fewer atomics beat the larger flush; at 5-6 bins up
+    // to 1000 cells (8 nodes at 5 bins) with 12-feature tiles in a 40 KB budget (config 3's
+    // depth 3: 121 against 135 us for 16-feature pair tiles; 16 nodes measured slower)
+    const int64_t tri_cells = (int64_t)max_nodes * nb * nb * nb;
+    if (nb <= 6 && K >= 3 && (tri_cells <= 512 || (nb >= 5 && tri_cells <= 1000))) P = 3;
     if (c->force_pairs == 1 || (c->force_pairs == 2 && nb <= 16) ||
         (c->force_pairs == 3 && nb <= 6 && K >= 3))
         P = c->force_pairs;
     const int64_t cells_node = (P == 3 ? nb * nb * nb : P == 2 ? nb * nb : nb);
     // budget: 20 KB for narrow frontiers (2-wave workgroups), 26 KB from 16 nodes on, where
     // 16-feature pair tiles and 4-wave workgroups measured faster (config 3 depths 4-5)
-    const int64_t budget = c->lds_budget > 0 ? c->lds_budget : (max_nodes >= 16 ? 26 * 1024 : 20000);
+    int64_t budget = c->lds_budget > 0 ? c->lds_budget : (max_nodes >= 16 ? 26 * 1024 : 20000);
+    if (c->lds_budget <= 0 && P == 3 && tri_cells > 512) budget = 40000;
     int64_t cap = std::max<int64_t>(budget, 4 * 1024);
     // node tiles when one feature's node x bin histogram does not fit: single features, up
     // to 32 KiB of LDS, as many nodes per tile as fit (swept at 1M rows x 500 features x 255
