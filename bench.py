@@ -324,6 +324,17 @@ def bench_predict(args, c: dict) -> int:
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / args.steps
+    # the same shape as a fitted model holds it: each pack repeats one tree pack_size times
+    # (booster.py:503-519), so the compiled forest walks 250 trees, each counted 8 times
+    packed = CompiledForest(pack_forest(rounds[: c["packs"]], c["pack_size"], torch.device("cuda")))
+    packed.predict(bins, N, 1.0)
+    e0.record()
+    for _ in range(args.steps):
+        packed.predict(bins, N, 1.0)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_packed = e0.elapsed_time(e1) / args.steps
+    packed.close()
     bytes_compulsory = float(N) * F + N * 4
     achieved = bytes_compulsory / (ms * 1e-3) / 1e9
     print(json.dumps({
@@ -334,6 +345,9 @@ def bench_predict(args, c: dict) -> int:
         "data": "synthetic (bins and forest generated in HBM / seeded)",
         "config": {"workload": f"config5: {N} rows x {F} features, {T} trees of depth {D}"},
         "kernel_ms": round(ms, 3),
+        "fitted_packs": {"kernel_ms": round(ms_packed, 3), "rows_per_s": round(N / (ms_packed * 1e-3), 1),
+                         "forest": f"{c['packs']} packs x {c['pack_size']} identical depth-{D} trees, "
+                                   "as a fitted model holds them (each pack walked once)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(5, N, "predict"),

@@ -1075,6 +1075,8 @@ struct pb_forest {
     uint32_t* heap_blocks = nullptr;  // tile.blocks x kForestBlockWords: per block of trees, the
                                       // packed records (pb::forest_tile_record), then leaf values
     int32_t* heap_id = nullptr;       // [T][2^depth] leaf node indices (absolute)
+    int32_t* heap_first = nullptr;    // [heap_trees] first forest tree each heap tree stands for
+    int32_t heap_trees = 0;           // distinct runs of consecutive identical trees
 };
 
 namespace {
@@ -1085,6 +1087,7 @@ void free_forest(pb_forest* fo) {
     (void)hipFree(fo->roots);
     (void)hipFree(fo->heap_blocks);
     (void)hipFree(fo->heap_id);
+    (void)hipFree(fo->heap_first);
     delete fo;
 }
 
@@ -1201,29 +1204,67 @@ int pb_forest_create(const int32_t* feature, const int32_t* threshold, const int
     for (int t = 0; t < T; ++t)
         for (int n = off[t]; n < off[t + 1]; ++n)
             if (!lf[n] && depth[n] >= 0) max_thr = std::max(max_thr, th[n]);
-    if (D <= pb::kForestTileMaxDepth) fo->tile = pb::forest_tile_shape(fo->max_feature + 1, max_thr, D, T);
+    // Runs of consecutive identical trees (a fitted pack repeats one tree B times): the tiled
+    // walk holds each run once, with its length, and counts its value that many times.
+    auto same_tree = [&](int ta, int tb) {
+        const int na = off[ta + 1] - off[ta];
+        if (na != off[tb + 1] - off[tb]) return false;
+        for (int k = 0; k < na; ++k) {
+            const int x = off[ta] + k, y = off[tb] + k;
+            if (lf[x] != lf[y] || __builtin_bit_cast(uint32_t, v[x]) != __builtin_bit_cast(uint32_t, v[y]))
+                return false;
+            if (!lf[x] && (f[x] != f[y] || th[x] != th[y] || l[x] - off[ta] != l[y] - off[tb] ||
+                           r[x] - off[ta] != r[y] - off[tb]))
+                return false;
+        }
+        return true;
+    };
+    std::vector<int32_t> first;  // first tree of each run
+    std::vector<int32_t> count;  // its length
+    for (int t = 0; t < T; ++t) {
+        if (!first.empty() && same_tree(first.back(), t)) {
+            ++count.back();
+        } else {
+            first.push_back(t);
+            count.push_back(1);
+        }
+    }
+    const int Td = (int)first.size();
+    if (D <= pb::kForestTileMaxDepth) fo->tile = pb::forest_tile_shape(fo->max_feature + 1, max_thr, D, Td);
     if (T > 0 && D <= pb::kForestTileMaxDepth && pb::forest_tile_lds_bytes(fo->tile) <= pb::kForestTileMaxLds) {
         const size_t NL = (size_t)1 << D, TB = (size_t)fo->tile.tree_block;
         const size_t BW = pb::kForestBlockWords;
-        // tree k of block b at dwords b*BW + k*2NL: node i (from 1) at dword i, leaves from NL;
-        // padding trees: always-left records and zero leaf values
+        // run k of block b at dwords b*BW + k*2NL: its length at dword 0 (a float), node i (from
+        // 1) at dword i, leaves from NL; padding trees: length 0, always-left records and zero
+        // leaf values
         std::vector<uint32_t> blk((size_t)fo->tile.blocks * BW, 0u);
         for (size_t x = 0; x < blk.size(); x += 2 * NL)
             std::fill(blk.begin() + x + 1, blk.begin() + x + NL, 255u << 24);
         std::vector<float> val(NL);
+        std::vector<uint32_t> scratch(NL);
         std::vector<int32_t> hi((size_t)T * NL, -1);
-        for (int t = 0; t < T; ++t) {
-            uint32_t* tree = blk.data() + (size_t)(t / TB) * BW + (size_t)(t % TB) * 2 * NL;
-            heap_tree(fo->tile, off[t], D, f, th, l, r, v, lf, tree + 1, val.data(), hi.data() + (size_t)t * NL);
-            std::memcpy(tree + NL, val.data(), sizeof(float) * NL);
+        for (int k = 0; k < Td; ++k) {
+            uint32_t* tree = blk.data() + (size_t)(k / TB) * BW + (size_t)(k % TB) * 2 * NL;
+            tree[0] = __builtin_bit_cast(uint32_t, (float)count[k]);
+            for (int c = 0; c < count[k]; ++c) {  // leaf node ids of every tree of the run
+                const int t = first[k] + c;
+                uint32_t* dst = c == 0 ? tree + 1 : scratch.data();
+                heap_tree(fo->tile, off[t], D, f, th, l, r, v, lf, dst, val.data(), hi.data() + (size_t)t * NL);
+                if (c == 0) std::memcpy(tree + NL, val.data(), sizeof(float) * NL);
+            }
         }
         if (hipMalloc(&fo->heap_blocks, sizeof(uint32_t) * blk.size()) != hipSuccess ||
-            hipMalloc(&fo->heap_id, sizeof(int32_t) * hi.size()) != hipSuccess) {
+            hipMalloc(&fo->heap_id, sizeof(int32_t) * hi.size()) != hipSuccess ||
+            hipMalloc(&fo->heap_first, sizeof(int32_t) * first.size()) != hipSuccess) {
             free_forest(fo);
             return fail(PB_ERR_NOMEM, "pb_forest_create: device allocation failed");
         }
+        fo->heap_trees = Td;
+        fo->tile.runs = Td < T ? 1 : 0;
         hipError_t e3 = hipMemcpy(fo->heap_blocks, blk.data(), sizeof(uint32_t) * blk.size(), hipMemcpyHostToDevice);
         if (e3 == hipSuccess) e3 = hipMemcpy(fo->heap_id, hi.data(), sizeof(int32_t) * hi.size(), hipMemcpyHostToDevice);
+        if (e3 == hipSuccess)
+            e3 = hipMemcpy(fo->heap_first, first.data(), sizeof(int32_t) * first.size(), hipMemcpyHostToDevice);
         if (e3 != hipSuccess) {
             free_forest(fo);
             return hip_fail(e3, "forest upload");
@@ -1248,8 +1289,8 @@ int pb_forest_predict(const pb_forest* fo, const uint8_t* bins, int64_t N, int64
     // the tiled walk reads a tile's rows four at a time: row stride and columns 4-byte aligned
     if (fo->heap_blocks && ld % 4 == 0 && reinterpret_cast<uintptr_t>(bins) % 4 == 0 &&
         env_int("PB_FOREST_TILE", 1) != 0) {
-        PB_HIP(pb::launch_forest_tile(bins, N, ld, fo->tile, fo->heap_blocks, fo->heap_id, fo->T, fo->depth,
-                                      tree_weight, out, leaf, (hipStream_t)stream),
+        PB_HIP(pb::launch_forest_tile(bins, N, ld, fo->tile, fo->heap_blocks, fo->heap_id, fo->heap_first,
+                                      fo->heap_trees, fo->depth, tree_weight, out, leaf, (hipStream_t)stream),
                "forest tile launch");
         return PB_OK;
     }

@@ -398,13 +398,14 @@ struct ForestTile {
     int32_t tree_block;  // trees per block (forest_tree_block of the depth)
     int32_t blocks;      // tree blocks (the last one padded with trees that add 0)
     int32_t threads;     // threads per workgroup (256, 512 or 1024)
+    int32_t runs;        // 1: some heap tree stands for a run of identical trees (dword 0 counts)
 };
 ForestTile forest_tile_shape(int32_t features, int32_t max_threshold, int32_t depth, int32_t trees);
 size_t forest_tile_lds_bytes(const ForestTile& ft);
 uint32_t forest_tile_record(const ForestTile& ft, int32_t feature, int32_t threshold);
 hipError_t launch_forest_tile(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft,
-                              const uint32_t* blocks, const int32_t* lid, int32_t T, int32_t depth,
-                              float tree_weight, float* out, int32_t* leaf, hipStream_t s);
+                              const uint32_t* blocks, const int32_t* lid, const int32_t* tfirst, int32_t T,
+                              int32_t depth, float tree_weight, float* out, int32_t* leaf, hipStream_t s);
 hipError_t launch_predict_pack(const uint8_t* bins, int64_t N, int64_t ld, int32_t F,
                                const int32_t* feature, const int32_t* threshold,
                                const int32_t* left_abs, const int32_t* right_abs,

@@ -13,6 +13,7 @@
 // One lane per row: a wavefront reads 64 consecutive rows of the same column while its rows
 // sit in the same node, and the forest arrays are small enough to stay in L2.
 #include <algorithm>
+#include <type_traits>
 
 #include "pb_internal.h"
 
@@ -132,7 +133,9 @@ __global__ __launch_bounds__(kBlock) void forest_kernel(
 // leaf), grouped in blocks of TB = forest_tree_block(D) trees of kForestBlockWords dwords:
 // tree k of a block takes dwords k * 2^(D+1) .. (k + 1) * 2^(D+1) - 1, node i (counted from 1,
 // children 2i and 2i + 1) at dword i: the records of its internal nodes (i < 2^D) and the
-// values of its leaves (i >= 2^D); dword 0 is unused. A record packs the bit position of its feature in its word of a row
+// values of its leaves (i >= 2^D); dword 0 holds, as a float, how many consecutive trees of the
+// forest the tree stands for (a fitted pack repeats one tree B times: it is walked once and its
+// value counted B times; padding trees hold 0). A record packs the bit position of its feature in its word of a row
 // tile (bits 0-4), the byte offset of that word row in the tile (bits 5-23; a multiple of
 // 4 * rows) and the threshold (bits 24-31). Trees past the forest's last one pad the last
 // block with always-left records and zero leaf values.
@@ -145,8 +148,8 @@ __global__ __launch_bounds__(kBlock) void forest_kernel(
 // walked), and NT / R tree streams (a lane per row) walk them, G trees per lane at once: every
 // load of the walk is an LDS load. Per level a lane reads the bin word of its node, compares,
 // and reads the chosen child's record (five VALU instructions per node). Each stream adds
-// float32(weight * leaf value) of its trees in double; the streams' sums are added in a fixed
-// order and rounded once to float32.
+// count * float32(weight * leaf value) of its trees in double (one fma: the product is exact);
+// the streams' sums are added in a fixed order and rounded once to float32.
 
 typedef __attribute__((address_space(3))) uint32_t lds_word;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte copies of tree blocks
@@ -194,11 +197,11 @@ __device__ __forceinline__ void stage_tile(const uint8_t* __restrict__ bins, int
 
 // LDS holds the kernel at two workgroups per CU (NT / 128 waves per SIMD), which sets the
 // register budget of a lane: all of it goes to the trees a lane walks at once.
-template <int D, int R, int NT, bool LEAF>
+template <int D, int R, int NT, bool LEAF, bool RUNS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT / 128, NT / 128))) void forest_tile_kernel(
     const uint8_t* __restrict__ bins, int64_t N, int64_t ld, ForestTile ft, const u32x4* __restrict__ blocks,
-    const int32_t* __restrict__ lid, int32_t T, float tree_weight, float* __restrict__ out,
-    int32_t* __restrict__ leaf) {
+    const int32_t* __restrict__ lid, const int32_t* __restrict__ tfirst, int32_t T, float tree_weight,
+    float* __restrict__ out, int32_t* __restrict__ leaf) {
     extern __shared__ uint32_t lds[];
     constexpr int NL = 1 << D;
     constexpr int S = NT / R;                     // tree streams
@@ -283,10 +286,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT / 128, NT
             }
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                acc += (double)(tree_weight * __uint_as_float(lds_at(base[g] + 4u * i[g])));
+                // dword 0: how many consecutive trees of the forest this one stands for (RUNS:
+                // some tree stands for more than one; a branch on it per tree cost 7%)
+                const float lv = tree_weight * __uint_as_float(lds_at(base[g] + 4u * i[g]));
+                const float m = RUNS ? __uint_as_float(lds_at(base[g])) : 1.0f;
+                if (RUNS)
+                    acc = __builtin_fma((double)lv, (double)m, acc);
+                else
+                    acc += (double)lv;
                 if (LEAF) {
                     const int t = b * TB + k0 + g * S;
-                    if (t < T && r < N) leaf[(int64_t)t * N + r] = lid[(int64_t)t * NL + (int)i[g] - NL];
+                    if (t < T && r < N) {
+                        const int t0 = tfirst[t];
+                        for (int j = 0; j < (int)m; ++j)
+                            leaf[(int64_t)(t0 + j) * N + r] = lid[(int64_t)(t0 + j) * NL + (int)i[g] - NL];
+                    }
                 }
             }
         }
@@ -305,7 +319,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(NT / 128, NT
 
 template <int D>
 hipError_t launch_tile_d(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft, const uint32_t* blocks,
-                         const int32_t* lid, int32_t T, float w, float* out, int32_t* leaf, hipStream_t s) {
+                         const int32_t* lid, const int32_t* tfirst, int32_t T, float w, float* out, int32_t* leaf,
+                         hipStream_t s) {
     const size_t lds = forest_tile_lds_bytes(ft);
     const int64_t tiles = (N + ft.rows - 1) / ft.rows;
     if (tiles > INT32_MAX || ft.tree_block != forest_tree_block(D) || (ft.rows != 32 && ft.rows != 64) ||
@@ -318,19 +333,23 @@ hipError_t launch_tile_d(const uint8_t* bins, int64_t N, int64_t ld, const Fores
             if (e != hipSuccess) return e;
         }
         hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(ft.threads), lds, s, bins, N, ld, ft,
-                           reinterpret_cast<const u32x4*>(blocks), lid, T, w, out, leaf);
+                           reinterpret_cast<const u32x4*>(blocks), lid, tfirst, T, w, out, leaf);
         return hipGetLastError();
     };
-    if (ft.threads == 1024) {
-        if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 1024, true>) : go(forest_tile_kernel<D, 32, 1024, true>);
-        return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 1024, false>) : go(forest_tile_kernel<D, 32, 1024, false>);
-    }
-    if (ft.threads == 512) {
-        if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 512, true>) : go(forest_tile_kernel<D, 32, 512, true>);
-        return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 512, false>) : go(forest_tile_kernel<D, 32, 512, false>);
-    }
-    if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 256, true>) : go(forest_tile_kernel<D, 32, 256, true>);
-    return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 256, false>) : go(forest_tile_kernel<D, 32, 256, false>);
+    auto pick = [&](auto runs) -> hipError_t {
+        constexpr bool RU = decltype(runs)::value;
+        if (ft.threads == 1024) {
+            if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 1024, true, RU>) : go(forest_tile_kernel<D, 32, 1024, true, RU>);
+            return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 1024, false, RU>) : go(forest_tile_kernel<D, 32, 1024, false, RU>);
+        }
+        if (ft.threads == 512) {
+            if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 512, true, RU>) : go(forest_tile_kernel<D, 32, 512, true, RU>);
+            return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 512, false, RU>) : go(forest_tile_kernel<D, 32, 512, false, RU>);
+        }
+        if (leaf) return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 256, true, RU>) : go(forest_tile_kernel<D, 32, 256, true, RU>);
+        return ft.rows == 64 ? go(forest_tile_kernel<D, 64, 256, false, RU>) : go(forest_tile_kernel<D, 32, 256, false, RU>);
+    };
+    return ft.runs ? pick(std::true_type{}) : pick(std::false_type{});
 }
 
 int grid_rows(int64_t N) {
@@ -413,19 +432,19 @@ uint32_t forest_tile_record(const ForestTile& ft, int32_t feature, int32_t thres
 }
 
 hipError_t launch_forest_tile(const uint8_t* bins, int64_t N, int64_t ld, const ForestTile& ft,
-                              const uint32_t* blocks, const int32_t* lid, int32_t T, int32_t depth,
-                              float tree_weight, float* out, int32_t* leaf, hipStream_t s) {
+                              const uint32_t* blocks, const int32_t* lid, const int32_t* tfirst, int32_t T,
+                              int32_t depth, float tree_weight, float* out, int32_t* leaf, hipStream_t s) {
     if (ld % 4 != 0 || reinterpret_cast<uintptr_t>(bins) % 4 != 0 || ft.blocks < 1) return hipErrorInvalidValue;
     switch (depth) {
-        case 0: return launch_tile_d<0>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 1: return launch_tile_d<1>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 2: return launch_tile_d<2>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 3: return launch_tile_d<3>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 4: return launch_tile_d<4>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 5: return launch_tile_d<5>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 6: return launch_tile_d<6>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 7: return launch_tile_d<7>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
-        case 8: return launch_tile_d<8>(bins, N, ld, ft, blocks, lid, T, tree_weight, out, leaf, s);
+        case 0: return launch_tile_d<0>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 1: return launch_tile_d<1>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 2: return launch_tile_d<2>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 3: return launch_tile_d<3>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 4: return launch_tile_d<4>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 5: return launch_tile_d<5>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 6: return launch_tile_d<6>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 7: return launch_tile_d<7>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
+        case 8: return launch_tile_d<8>(bins, N, ld, ft, blocks, lid, tfirst, T, tree_weight, out, leaf, s);
         default: return hipErrorInvalidValue;
     }
 }

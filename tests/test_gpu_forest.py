@@ -33,20 +33,22 @@ def _forest(seed, packs, B, D, F, ragged=False, max_thr=3):
     return rounds
 
 
+@pytest.mark.parametrize("B", [8, 1], ids=["packs", "distinct"])
 @pytest.mark.parametrize("tile", [1, 0], ids=["tiled", "per-row"])
 @pytest.mark.parametrize("ragged", [False, True])
-def test_compiled_forest(hip, oracle_mod, monkeypatch, ragged, tile):
+def test_compiled_forest(hip, oracle_mod, monkeypatch, ragged, tile, B):
     """tile 1: the tiled walk (double sums rounded once; the tree-order float32 sum of
     pb_predict_forest carries up to T float32 roundings, so the two agree to 1e-5); tile 0: the
-    per-row walk, bit-identical to pb_predict_forest."""
+    per-row walk, bit-identical to pb_predict_forest. B 8: each pack repeats one tree 8 times,
+    which the tiled walk holds once with its count; B 1: every tree distinct (no counts)."""
     import torch
 
     monkeypatch.setenv("PB_FOREST_TILE", str(tile))
     from packboost_amd.booster import pack_forest
     from packboost_amd.predictor import CompiledForest
 
-    N, F, B, D = 20011, 300, 8, 6
-    print(f"[forest] ragged={ragged}", flush=True)
+    N, F, D = 20011, 300, 6
+    print(f"[forest] ragged={ragged} tile={tile} B={B}", flush=True)
     rounds = _forest(3, 25, B, D, F, ragged)
     rng = np.random.default_rng(4)
     bins = rng.integers(0, 5, size=(N, F), dtype=np.uint8)
