@@ -1395,52 +1395,100 @@ __device__ void sequential_pick(const DecideCands& dc, int u, Cand& best) {
     const int64_t n = (int64_t)dc.K * dc.T;
     const float* sc = dc.seq.score + (int64_t)u * n;
     const double M = (double)best.score;
+    // the band's width w = 2^k * 1e-12 (widened as kTieBand0): the first k from 6 whose band
+    // holds fewer than 2^k candidates (or 2^k > n); eight widths counted per pass over the scores
     double w = 0.0;
-    int64_t count = 0;
-    for (int k = 6;; ++k) {
-        w = ldexp(kTieBand0, k - 6);  // 2^k * 1e-12, widened as kTieBand0
-        int64_t c = 0;
-        for (int64_t i = lane; i < n; i += kWave) c += ((double)sc[i] >= M - w) ? 1 : 0;
+    for (int k0 = 6;; k0 += 8) {
+        int c[8];
 #pragma unroll
-        for (int m = 1; m < kWave; m <<= 1) c += __shfl_xor(c, m);
-        count = c;
-        if (count < (int64_t(1) << k) || (int64_t(1) << k) > n) break;
+        for (int q = 0; q < 8; ++q) c[q] = 0;
+        for (int64_t i = lane; i < n; i += kWave) {
+            const double d = M - (double)sc[i];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) c[q] += (d <= ldexp(kTieBand0, k0 + q - 6)) ? 1 : 0;
+        }
+        int k_hit = -1;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            int64_t cq = c[q];
+#pragma unroll
+            for (int m = 1; m < kWave; m <<= 1) cq += __shfl_xor(cq, m);
+            const int k = k0 + q;
+            if (k_hit < 0 && (cq < (int64_t(1) << k) || (int64_t(1) << k) > n)) k_hit = k;
+        }
+        if (k_hit >= 0) {  // uniform
+            w = ldexp(kTieBand0, k_hit - 6);
+            break;
+        }
     }
     int32_t* band = dc.seq.band + (int64_t)u * n;
     int64_t pos = 0;
     for (int64_t b0 = 0; b0 < n; b0 += kWave) {
         const int64_t i = b0 + lane;
-        const bool in = i < n && (double)sc[i] >= M - w;
+        const bool in = i < n && M - (double)sc[i] <= w;
         const unsigned long long m = __ballot(in);
         if (in) band[pos + __popcll(m & ((1ull << lane) - 1ull))] = (int32_t)i;
         pos += __popcll(m);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    if (lane == 0) {
-        Cand cur = best;
-        bool started = false;
-        for (int64_t j = 0; j < pos; ++j) {
+    // The scan over the band in visiting order, 64 candidates per window: every lane loads
+    // one candidate and tests it against the best so far. A window where no lane would replace
+    // it is passed over; otherwise the scan runs through the window from the first lane that
+    // would, on values read from the lanes' registers (uniform across the wavefront), so a band
+    // where nearly every candidate replaces the last one costs register steps, not a chain of
+    // dependent loads.
+    float c_s = 0.0f, c_lg = 0.0f;
+    int c_lt = 0, c_f = -1, c_thr = -1;
+    float b_s = best.score, b_lg = best.lg;
+    int b_lt = best.lt, b_f = best.f, b_thr = best.thr;
+    bool started = false;
+    for (int64_t j0 = 0; j0 < pos; j0 += kWave) {  // wave-uniform
+        const int64_t j = j0 + lane;
+        bool take = false;
+        if (j < pos) {
             const int32_t i = band[j];
-            const float sv = sc[i];
             const int kk = i / dc.T;
             const int t = i - kk * dc.T;
-            Cand c;
-            c.score = sv;
-            c.lt = dc.seq.lt[(int64_t)u * n + i];
-            c.lg = dc.seq.lg[(int64_t)u * n + i];
-            c.f = dc.feats[kk];
-            c.thr = dc.thr_tab ? dc.thr_tab[kk * dc.T + t] : t;
-            c.valid = 1;
-            const bool first = !started && ((double)sv == M);
-            const bool s_gt = sv > cur.score;
-            const bool near = fabsf(sv - cur.score) <= 1e-12f;
-            const bool tie_win = (c.lt > cur.lt) | ((c.lt == cur.lt) & ((c.f > cur.f) | ((c.f == cur.f) & (c.thr > cur.thr))));
-            const bool take = first | (started & (s_gt | (near & tie_win)));
-            take_if(take, c, cur);
-            started = started | first;
+            c_s = sc[i];
+            c_lt = dc.seq.lt[(int64_t)u * n + i];
+            c_lg = dc.seq.lg[(int64_t)u * n + i];
+            c_f = dc.feats[kk];
+            c_thr = dc.thr_tab ? dc.thr_tab[kk * dc.T + t] : t;
+            const bool first = !started && ((double)c_s == M);
+            const bool s_gt = c_s > b_s;
+            const bool near = fabsf(c_s - b_s) <= 1e-12f;
+            const bool tie_win = (c_lt > b_lt) | ((c_lt == b_lt) & ((c_f > b_f) | ((c_f == b_f) & (c_thr > b_thr))));
+            take = first | (started & (s_gt | (near & tie_win)));
         }
-        best = cur;
+        const unsigned long long m = __ballot(take);
+        if (m == 0ull) continue;
+        const int l0 = __ffsll((long long)m) - 1;
+        const int l1 = (int)min<int64_t>((int64_t)kWave, pos - j0);
+        for (int l = l0; l < l1; ++l) {  // uniform: the same steps on every lane
+            const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c_s), l));
+            const int lt = __builtin_amdgcn_readlane(c_lt, l);
+            const int f = __builtin_amdgcn_readlane(c_f, l);
+            const int thr = __builtin_amdgcn_readlane(c_thr, l);
+            const bool first = !started && ((double)sv == M);
+            const bool s_gt = sv > b_s;
+            const bool near = fabsf(sv - b_s) <= 1e-12f;
+            const bool tie_win = (lt > b_lt) | ((lt == b_lt) & ((f > b_f) | ((f == b_f) & (thr > b_thr))));
+            if (first | (started & (s_gt | (near & tie_win)))) {
+                b_s = sv;
+                b_lt = lt;
+                b_lg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c_lg), l));
+                b_f = f;
+                b_thr = thr;
+                started = true;
+            }
+        }
     }
+    best.score = b_s;
+    best.lt = b_lt;
+    best.lg = b_lg;
+    best.f = b_f;
+    best.thr = b_thr;
+    best.valid = 1;
 }
 
 // Candidates of the node scoring below its best score M but within kTieBand0 of it, as far

@@ -69,6 +69,13 @@ def test_depth_parity(hip, oracle_mod, case, layout):
         g.hist(feats)
         cnt, gp = g.planes()
         rc, rg = ref.planes
+        # every (era, node) total is that node's rows in the era, counted from the row ids
+        # (independent of the oracle: a build that miscounts fails here first)
+        nid = p["nid"].astype(np.int64)
+        act = nid < U
+        rows_en = np.zeros((E, U), dtype=np.int64)
+        np.add.at(rows_en, (p["era"][act], nid[act]), 1)
+        np.testing.assert_array_equal(cnt[:, :, :, nb - 1], np.repeat(rows_en[:, :, None], K, axis=2))
         np.testing.assert_array_equal(cnt, rc)
         mass = _abs_mass(p, U)[:, :, None, None]
         err = np.abs(gp.astype(np.float64) - rg.astype(np.float64))
