@@ -37,8 +37,10 @@ STAT_KEYS = {"nodes_processed", "nodes_skipped", "rows_total", "feature_blocks",
     (7, 8000, 20, 9, 32, 5, 12, 4, "mass", 5, 1.5, 0.1, 0.4, True),
     (8, 5000, 8, 4, 64, 3, 8, 0, "mass", 3, 0.7, 0.2, 0.5, True),
     (9, 7000, 12, 5, 128, 4, 9, 6, "even", 20, 0.0, 0.0, 0.0, True),
+    (10, 150000, 5, 2, 16, 2, 5, 4, "mass", 20, 0.5, 0.0, 0.3, True),  # eras above 65535 rows
 ], ids=["nb5", "nb32_kcuts_alpha_dir", "nb128_even_cuts", "nb255_alpha_dir", "40_nodes_msl40",
-        "skipped_nb5", "skipped_nb32_kcuts_alpha_dir", "skipped_nb64_alpha_dir", "skipped_nb128_even_cuts"])
+        "skipped_nb5", "skipped_nb32_kcuts_alpha_dir", "skipped_nb64_alpha_dir", "skipped_nb128_even_cuts",
+        "skipped_32bit_counts_kcuts_alpha"])
 def test_host_schema_split_finder(hip, oracle_mod, case):
     from packboost_amd import backends
     from tests.helpers import with_skipped_bins
