@@ -189,13 +189,20 @@ def test_255_bins_fit(hip, oracle_mod):
     np.testing.assert_allclose(model.predict(X), oracle_mod.predict(ref.rounds, 2, 0.1, bins), atol=1e-5)
 
 
-@pytest.mark.parametrize("case", ["nan_target", "overflowing_predictions", "root_too_small"])
-def test_nonfinite_gradients_stop_the_fit(hip, case):
+@pytest.mark.parametrize("case", ["nan_target", "overflowing_predictions", "root_too_small",
+                                  "overflowing_segments"])
+def test_nonfinite_gradients_stop_the_fit(hip, monkeypatch, case):
     """Gradients that are not finite have no fixed-point value: the round is flagged on the
     device (pb_round_header.reserved[0]; the per-phase path checks the gradients) and the fit
-    raises FloatingPointError instead of growing trees from meaningless histograms. The
-    reference's float sums would carry the NaN into its scores instead; this build stops."""
+    raises FloatingPointError instead of growing trees from meaningless histograms (nonfinite
+    "raise"), or keeps the finite rounds before it (nonfinite "truncate"). The reference's float
+    sums would carry the NaN into its scores instead (tests/test_oracle_nonfinite.py pins what it
+    produces). "overflowing_segments" runs the fused segment-mode scorer from depth 0."""
     from packboost_amd import PackBoost, PackBoostConfig
+
+    if case == "overflowing_segments":
+        monkeypatch.setenv("PB_FIT_MODE", "segments")
+        monkeypatch.setenv("PB_SEG_FROM_DEPTH", "0")
 
     rng = np.random.default_rng(11)
     N, F = 3000, 6
@@ -206,7 +213,7 @@ def test_nonfinite_gradients_stop_the_fit(hip, case):
     if case == "nan_target":
         y[17] = np.nan
         cfg, rounds = PackBoostConfig(pack_size=2, learning_rate=0.1, **kw), 2
-    elif case == "overflowing_predictions":
+    elif case in ("overflowing_predictions", "overflowing_segments"):
         # learning_rate x pack_size = 128: the residuals grow ~127x per round and the
         # predictions pass float32's range within about 20 rounds
         cfg, rounds = PackBoostConfig(pack_size=64, learning_rate=2.0, **kw), 60
@@ -237,7 +244,7 @@ def test_nonfinite_gradients_stop_the_fit(hip, case):
     order = np.argsort(era, kind="stable")
     np.testing.assert_allclose(trunc._train_preds.cpu().numpy(), p[order], rtol=1e-6,
                                atol=1e-6 * max(1.0, float(np.abs(p).max())))
-    if case != "overflowing_predictions":
+    if not case.startswith("overflowing"):
         assert kept == 0 and np.all(p == 0.0)
     # the same model object fits again on finite data
     y_ok = np.nan_to_num(y, nan=0.0, posinf=0.0)
