@@ -359,11 +359,16 @@ int pb_predict_forest(const uint8_t* bins_dev, int64_t N, int64_t ld, int32_t F,
  * the packed SoA forest (same arrays and layout as pb_predict_forest, offsets int32 [T+1],
  * device pointers), checks every tree (children inside the tree, no node reached twice,
  * 0 <= feature < 2^24 - 1, 0 <= threshold <= 255) and stores one 16-byte record per node
- * in device memory the handle owns. pb_forest_predict gives the same result as
- * pb_predict_forest: out[r] = sum over trees in order of float32(tree_weight * leaf value),
- * one float32 rounding per product and per add (booster.py:709-712). A lane walks 8 trees
- * at once. leaf_dev (optional): int32 [T][N] absolute leaf index per tree. PB_ERR_RANGE if a
- * split feature is >= F. */
+ * in device memory the handle owns, plus, for forests up to depth 8 whose row tile fits the
+ * LDS, every tree as a complete heap for the tiled walk; runs of consecutive identical trees
+ * (a fitted pack's B copies) are stored there once with their length.
+ * pb_forest_predict: out[r] = sum over trees of float32(tree_weight * leaf value)
+ * (booster.py:709-712). The tiled walk (used when the row stride and bins are 4-byte
+ * aligned) adds the products in double, a run's length times its product in one exact fma,
+ * and rounds once, so it agrees with pb_predict_forest's tree-order float32 sum within that
+ * sum's roundings; otherwise one lane per row walks the trees in order with pb_predict_forest's
+ * float32 adds, bit for bit. leaf_dev (optional): int32 [T][N] absolute leaf index per tree
+ * (every tree of a run). PB_ERR_RANGE if a split feature is >= F. */
 typedef struct pb_forest pb_forest;
 int pb_forest_create(const int32_t* feature_dev, const int32_t* threshold_dev,
                      const int32_t* left_abs_dev, const int32_t* right_abs_dev,
