@@ -656,14 +656,24 @@ int pb_partition(pb_ctx* c, const uint8_t* bins, int32_t depth, uint16_t* nid, u
     return partition(c, bins, nib ? c->d.ld / 2 : c->d.ld, nib, depth, nid, tnode, stream);
 }
 
-int pb_round_end(pb_ctx* c, const uint16_t* tnode, const float* values, int32_t pack_size,
-                 float lr, float* preds, void* stream) {
+namespace {
+
+// pb_round_end's work; with `header`, the kernel also writes the round header
+int round_end(pb_ctx* c, const uint16_t* tnode, const float* values, int32_t pack_size, float lr,
+              float* preds, pb_round_header* header, void* stream) {
     if (!c || !tnode || !values || !preds) return fail(PB_ERR_INVALID, "pb_round_end: null argument");
     if (pack_size < 1) return fail(PB_ERR_INVALID, "pb_round_end: pack_size must be >= 1");
-    PB_HIP(pb::launch_round_end(tnode, values, pack_size, lr, preds, c->d.num_rows,
+    PB_HIP(pb::launch_round_end(tnode, values, pack_size, lr, preds, c->d.num_rows, c->st, header,
                                 (hipStream_t)stream),
            "round_end launch");
     return PB_OK;
+}
+
+}  // namespace
+
+int pb_round_end(pb_ctx* c, const uint16_t* tnode, const float* values, int32_t pack_size,
+                 float lr, float* preds, void* stream) {
+    return round_end(c, tnode, values, pack_size, lr, preds, nullptr, stream);
 }
 
 namespace {
@@ -879,15 +889,15 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
             return rc;
         if ((rc = mark(4))) return rc;
     }
-    PB_HIP(pb::launch_round_header(c->st, header, (hipStream_t)stream), "round header launch");
+    // the round-end kernel also writes the round's header (its first workgroup)
     if (seg) {
         const pb::SegBuffers& cur = c->sb[c->seg_cur];
         PB_HIP(pb::launch_seg_round_end(cur.tnode, cur.row, b->values_dev, b->pack_size, b->learning_rate,
-                                        b->preds_dev, c->d.num_rows, (hipStream_t)stream),
+                                        b->preds_dev, c->d.num_rows, c->st, header, (hipStream_t)stream),
                "segment round end launch");
         return PB_OK;
     }
-    return pb_round_end(c, b->tnode_dev, b->values_dev, b->pack_size, b->learning_rate, b->preds_dev,
+    return round_end(c, b->tnode_dev, b->values_dev, b->pack_size, b->learning_rate, b->preds_dev, header,
                         stream);
 }
 

@@ -228,7 +228,9 @@ template <bool VEC>
 __global__ __launch_bounds__(kBlock) void round_end_kernel(const uint16_t* __restrict__ tnode,
                                                        const float* __restrict__ values,
                                                        int32_t B, float lr,
-                                                       float* __restrict__ preds, int64_t N) {
+                                                       float* __restrict__ preds, int64_t N,
+                                                       const Frontier* st, pb_round_header* header) {
+    if (header && blockIdx.x == 0) write_round_header(st, header);  // the round's last kernel
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     const int64_t t0 = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (VEC) {
@@ -246,13 +248,6 @@ __global__ __launch_bounds__(kBlock) void round_end_kernel(const uint16_t* __res
     } else {
         for (int64_t r = t0; r < N; r += stride) preds[r] = pack_step(preds[r], values[tnode[r]], B, lr);
     }
-}
-
-__global__ void round_header_kernel(const Frontier* st, pb_round_header* h) {
-    const int i = threadIdx.x;
-    if (i <= PB_MAX_DEPTH) h->u_active[i] = st->u_active[i];
-    if (i == 0) h->tree_size = st->tree_size;
-    if (i < 6) h->reserved[i] = i == 0 ? st->reserved[kNonFinite] : 0;
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -301,21 +296,17 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
     return hipGetLastError();
 }
 
-hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s) {
-    hipLaunchKernelGGL(round_header_kernel, dim3(1), dim3(64), 0, s, st, h);
-    return hipGetLastError();
-}
-
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
-                            float lr, float* preds, int64_t N, hipStream_t s) {
+                            float lr, float* preds, int64_t N, const Frontier* st, pb_round_header* header,
+                            hipStream_t s) {
     if (aligned(tnode, 8) && aligned(preds, 16)) {
         const int grid = grid_for(std::max<int64_t>(1, N / 4), kBlock, 8192);
         hipLaunchKernelGGL(round_end_kernel<true>, dim3(grid), dim3(kBlock), 0, s, tnode, values, pack_size,
-                           lr, preds, N);
+                           lr, preds, N, st, header);
     } else {
         const int grid = grid_for(N, kBlock, 8192);
         hipLaunchKernelGGL(round_end_kernel<false>, dim3(grid), dim3(kBlock), 0, s, tnode, values, pack_size,
-                           lr, preds, N);
+                           lr, preds, N, st, header);
     }
     return hipGetLastError();
 }

@@ -24,6 +24,15 @@ struct Frontier {
 };
 constexpr int kNonFinite = 0;
 
+// The round's header (pb_round_header) from the frontier state, written by the first
+// workgroup's threads of a kernel that runs after the round's last decision step.
+__device__ __forceinline__ void write_round_header(const Frontier* st, pb_round_header* h) {
+    const int i = (int)threadIdx.x;
+    if (i <= PB_MAX_DEPTH) h->u_active[i] = st->u_active[i];
+    if (i == 0) h->tree_size = st->tree_size;
+    if (i < 6) h->reserved[i] = i == 0 ? st->reserved[kNonFinite] : 0;
+}
+
 // Fixed-point gradient scale of one era: rows add q = round(g * 2^sh) into the 48-bit grad field
 // of a histogram word. round_begin sums |g| over windows of kGradWinRows consecutive rows, and
 // era_scale_kernel bounds the era's sum of |g| by the sum of the windows that overlap it
@@ -313,7 +322,8 @@ hipError_t launch_seg_partition(const SegState& st, const int32_t* seg, int32_t*
                                 const SegBuffers& dst, const uint8_t* bins, int32_t depth, bool last,
                                 hipStream_t s);
 hipError_t launch_seg_round_end(const uint16_t* stn, const int32_t* srow, const float* values, int32_t B,
-                                float lr, float* preds, int64_t N, hipStream_t s);
+                                float lr, float* preds, int64_t N, const Frontier* st, pb_round_header* header,
+                                hipStream_t s);
 // Features per workgroup for `nodes` active slots and K features: enough workgroups to fill
 // the device (about 1024), at most kSegMaxFt.
 int32_t seg_score_fts(int32_t nodes, int32_t K);
@@ -335,9 +345,9 @@ hipError_t launch_round_begin(const float* preds, const float* y, float* grad, u
                               uint16_t* tnode, int64_t N, int64_t rows_padded, int32_t root_active,
                               const int32_t* era_off, int32_t E, float* win_sum, int32_t* sh_era,
                               Frontier* st, int32_t* cur_ids, hipStream_t s);
-hipError_t launch_round_header(const Frontier* st, pb_round_header* h, hipStream_t s);
 hipError_t launch_round_end(const uint16_t* tnode, const float* values, int32_t pack_size,
-                            float lr, float* preds, int64_t N, hipStream_t s);
+                            float lr, float* preds, int64_t N, const Frontier* st, pb_round_header* header,
+                            hipStream_t s);
 hipError_t launch_pack_bins4(const uint8_t* bins, int64_t n, int64_t ld, int32_t F, uint8_t* out,
                              hipStream_t s);
 // Row-list kernels (rowlist.hip). Workspace: rowlist_work_elems(segments) int32, whose first

@@ -340,7 +340,9 @@ __global__ __launch_bounds__(kBlock) void seg_final_kernel(SegState s, const int
 __global__ __launch_bounds__(kBlock) void seg_round_end_kernel(const uint16_t* __restrict__ stn,
                                                          const int32_t* __restrict__ srow,
                                                          const float* __restrict__ values, int32_t B,
-                                                         float lr, float* __restrict__ preds, int64_t N) {
+                                                         float lr, float* __restrict__ preds, int64_t N,
+                                                         const Frontier* st, pb_round_header* header) {
+    if (header && blockIdx.x == 0) write_round_header(st, header);  // the round's last kernel
     const int64_t stride = (int64_t)gridDim.x * kBlock;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < N; i += stride) {
         const float v = values[stn[i]];
@@ -386,9 +388,10 @@ hipError_t launch_seg_partition(const SegState& st, const int32_t* seg, int32_t*
 }
 
 hipError_t launch_seg_round_end(const uint16_t* stn, const int32_t* srow, const float* values, int32_t B,
-                                float lr, float* preds, int64_t N, hipStream_t s) {
+                                float lr, float* preds, int64_t N, const Frontier* st, pb_round_header* header,
+                                hipStream_t s) {
     hipLaunchKernelGGL(seg_round_end_kernel, dim3(grid_of_rows(N)), dim3(kBlock), 0, s, stn, srow, values, B, lr,
-                       preds, N);
+                       preds, N, st, header);
     return hipGetLastError();
 }
 
