@@ -157,6 +157,34 @@ def test_deep_tree_fit(hip, oracle_mod, nb):
     assert max(int(np.count_nonzero(~np.asarray(r["is_leaf"]))) for r in ref.rounds) > 128
 
 
+def test_deepest_tree_fit(hip, oracle_mod):
+    """max_depth 15, the library's limit, on 24k rows with min_samples_leaf 2: frontiers of
+    thousands of nodes (node tiles of single features), tree node ids into the tens of
+    thousands (uint16 ids), and the last depths' tiny nodes. The tree matches the oracle's
+    node for node, or up to its first differing node, which must be a near-tie
+    (compare_fit_rounds); depth 16 is refused."""
+    from packboost_amd import PackBoost, PackBoostConfig
+    from tests.helpers import compare_fit_rounds
+
+    print("[deepest] D=15", flush=True)
+    rng = np.random.default_rng(15)
+    N, F, nb = 24000, 6, 8
+    bins = rng.integers(0, nb, size=(N, F)).astype(np.int8)
+    y = (_target(rng, bins, k=4) + 0.5 * rng.standard_normal(N).astype(np.float32)).astype(np.float32)
+    era = np.repeat(np.arange(4), N // 4).astype(np.int16)
+    kw = dict(pack_size=1, max_depth=15, learning_rate=0.1, lambda_l2=0.5, lambda_dro=0.0,
+              min_samples_leaf=2, max_bins=nb, random_state=15)
+    model = PackBoost(PackBoostConfig(**kw, prebinned=True)).fit(bins, y, era, num_rounds=1)
+    trace: list = []
+    ref = oracle_mod.fit(bins, y, era.astype(np.int64), num_rounds=1, trace=trace, **kw)
+    sizes = (len(model._rounds[0]["feature"]), len(ref.rounds[0]["feature"]))
+    matched, _ = compare_fit_rounds(oracle_mod, model._rounds, ref, trace, bins, kw)
+    print(f"[deepest] tree nodes {sizes}, {matched} of 1 rounds identical", flush=True)
+    assert min(sizes) > 4000 and max(t["depth"] for t in trace) == 14, sizes
+    with pytest.raises(Exception, match="max_depth"):
+        PackBoost(PackBoostConfig(max_depth=16, max_bins=nb, prebinned=True)).fit(bins, y, era, num_rounds=1)
+
+
 def test_fit_without_eras_large(hip, oracle_mod):
     """era=None puts all 150k rows in one era: built in segments, 32-bit counts."""
     print("[no eras, 150k rows]", flush=True)
