@@ -24,6 +24,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -357,6 +358,40 @@ def bench_predict(args, c: dict) -> int:
     return 0
 
 
+def other_configs(configs=(2, 4, 5), timeout_s: float = 300.0) -> dict:
+    """BASELINE.json's other single-GPU configs, measured by the same run: `bench.py --config N
+    --no-cpu-baseline` in a child process each (its own GPU context, after config 3's buffers are
+    freed), their progress on this process's stderr. Each entry keeps the child's rate and the
+    figures that locate it; a child that fails or passes `timeout_s` leaves its error instead."""
+    res = {}
+    for n in configs:
+        print(f"[bench] config {n} in a child process", file=sys.stderr, flush=True)
+        t0 = time.perf_counter()
+        try:
+            p = subprocess.run([sys.executable, "-u", str(Path(__file__).resolve()), "--config", str(n),
+                                "--no-cpu-baseline"], stdout=subprocess.PIPE, text=True, timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            res[f"config{n}"] = {"error": f"no result within {timeout_s:.0f} s"}
+            continue
+        lines = [ln for ln in p.stdout.splitlines() if ln.startswith("{")]
+        if p.returncode != 0 or not lines:
+            res[f"config{n}"] = {"error": f"exit status {p.returncode}"}
+            continue
+        j = json.loads(lines[-1])
+        keep = {k: j[k] for k in ("metric", "value", "unit", "steps", "warmup", "ms_per_step") if k in j}
+        keep["workload"] = j.get("config", {}).get("workload")
+        for k in ("kernel_ms", "fitted_packs", "phase_ms_per_round", "hist_ms_per_depth", "full_depth_rounds"):
+            if k in j:
+                keep[k] = j[k]
+        if "fit_mode" in j.get("config", {}):
+            keep["fit_mode"] = j["config"]["fit_mode"]
+        r = j.get("roofline") or {}
+        keep["roofline"] = {k: r.get(k) for k in ("kernel", "bound", "achieved", "unit", "frac")}
+        keep["child_wall_s"] = round(time.perf_counter() - t0, 1)
+        res[f"config{n}"] = keep
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -372,6 +407,8 @@ def main() -> int:
                     help="CPU baseline from rounds 1-3 at the full size (minutes) instead of two samples")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (counter calibration)")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="config 3 only (by default its line also carries configs 2, 4 and 5)")
     args = ap.parse_args()
     if args.copy_probe:
         return copy_probe(args.copy_probe)
@@ -572,6 +609,8 @@ def main() -> int:
     fit.close()
     del bins
     torch.cuda.empty_cache()
+    if args.config == 3 and not args.rows and not args.no_other_configs:
+        out["other_configs"] = other_configs()
     if not args.no_cpu_baseline and args.config == 3:
         print("[bench] timing the CPU restatement of the reference frontier", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(c, args.cpu_budget, full=args.cpu_full)
