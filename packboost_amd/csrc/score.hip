@@ -633,9 +633,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
     // and grad. Loading two chunks ahead covers the plane loads' latency when three workgroups
     // per CU stream a deep frontier's planes.
     // Loads without a branch (an element outside the chunk, the last era or this thread's
-    // candidates reads the chunk's first one, always in bounds, and pok[S] marks what is real:
-    // bit 0 the era total, bit 1 + i pair i), so the compiler's wait counts stay exact and the
-    // next chunk's loads stay in flight while this one is made.
+    // candidates reads the chunk's first one, always in bounds, and bit 0 of pok[S] says the
+    // era is real, and with it the thread's pairs), so the compiler's wait counts stay exact and
+    // the next chunk's loads stay in flight while this one is made.
     int pct[2] = {0, 0};
     float pGt[2] = {0.0f, 0.0f};
     uint32_t pok[2] = {0u, 0u};
@@ -659,7 +659,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
             const int64_t off = eoff + (pair_ok ? slot_off[i] : 0);
             pL[S][i] = C32 ? (int)a.cnt32[off] : (int)a.cnt[off];
             pGL[S][i] = a.g[off];
-            ok |= pair_ok ? (2u << i) : 0u;
         }
         pok[S] = ok;
     };
@@ -680,9 +679,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
 #pragma unroll
         for (int i = 0; i < kPcPairs; ++i) {
             if (i >= np) break;
-            const bool pair_ok = (ok >> (i + 1)) & 1u;
-            const int Lc = pair_ok ? pL[S][i] : 0;
-            const float GLc = pair_ok ? pGL[S][i] : 0.0f;
+            // a pair's values are real whenever its era is (ok bit 0; a thread's pairs share one
+            // era), and every output below is masked by `has` (false unless the era is real), so
+            // the values of a pair outside the chunk reach no output and are not masked here
+            const int Lc = pL[S][i];
+            const float GLc = pGL[S][i];
             const int R = ctot - Lc;
             const float GR = Gt - GLc;
             const float w = (has && Lc > 0 && R > 0) ? wera : 0.0f;
@@ -980,7 +981,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
     // without a branch (a chunk past the end, an era past the last one or a slot without a
     // candidate reads the chunk's first elements, always in bounds) so that the compiler's
     // wait counts stay exact and the loads of later chunks stay in flight; bit 0 of pok[S]
-    // says the era total is real, bit 1 + i that pair i is.
+    // says the era is real, and with it the pairs of the thread's candidate slots.
     int pct[PF];
     float pGt[PF];
     uint32_t pok[PF];
@@ -1006,7 +1007,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
             const uint32_t o = pair_ok ? (uint32_t)slot_off[i] : 0u;
             pL[S][i] = C32 ? (int)cb32[o] : (int)cb[o];
             pGL[S][i] = gb[o];
-            ok |= pair_ok ? (2u << i) : 0u;
         }
         pok[S] = ok;
     };
@@ -1044,9 +1044,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
 #pragma unroll
         for (int i = 0; i < NP; ++i) {
             if (i >= np) break;
-            const bool pair_ok = (ok >> (i + 1)) & 1u;
-            const int Lc = pair_ok ? pL[S][i] : 0;
-            const float GLc = pair_ok ? pGL[S][i] : 0.0f;
+            // as in des_score_pc_kernel: every output is masked by `has` (or by the slot's
+            // validity), so a pair outside the chunk needs no mask of its own
+            const int Lc = pL[S][i];
+            const float GLc = pGL[S][i];
             const int R = ctot - Lc;
             const float GR = Gt - GLc;
             const bool act = has && Lc > 0 && R > 0;
