@@ -686,7 +686,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
             const float GLc = pGL[S][i];
             const int R = ctot - Lc;
             const float GR = Gt - GLc;
-            const float w = (has && Lc > 0 && R > 0) ? wera : 0.0f;
+            const bool act = has && Lc > 0 && R > 0;
+            const float w = act ? wera : 0.0f;  // wera >= 1 for an era with rows
             const float dL = (float)Lc + lam;
             const float dR = (float)R + lam;
             const float gfull = 0.5f * ((GLc * GLc) / dL + (GR * GR) / dR) - parent;
@@ -696,9 +697,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
                 const float rv = -GR / dR;
                 pos = lv > rv;
             }
-            const bool act = w > 0.0f;
             const float gain = act ? gfull : 0.0f;
-            const float wd = act ? (pos ? w : -w) : 0.0f;
+            const float wd = pos ? w : -w;  // +-0 when inactive: the consumer reads |wd| first
             // An era without rows of the node contributes L = 0, GL = +0 and weight 0, which
             // leaves every consumer sum bit-unchanged: the reference skips such eras
             // (frontier_cpu.cpp:367-369), and x + (+0) == x for every x the sums can hold
@@ -708,7 +708,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
             const int el = slot_el[i];
             const int c = slot_c[i];
             // eras past the end of the last chunk get neutral records (no rows, zero
-            // weight: the prefetched values are zero there), so the consumer reads whole
+            // weight: their era total is masked to zero), so the consumer reads whole
             // batches unconditionally
             if (el < kPcEras) {
                 buf[el * kWave + c] = make_float4(gain, GL, __int_as_float(L), wd);
@@ -733,8 +733,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
     // the factor w / wsum is 1/n, read from the table of IEEE 1/n (bit-identical), and
     // w * delta == delta; otherwise it is the IEEE division. The lookups are issued off the
     // mean/M2 chain (computing 1/n with exact_recip instead measured slower here: more VALU on
-    // the consumer wave). Inactive eras get factor 0 and keep mean/M2 by selection. TABLE and
-    // DIR are compile-time, so the loop has no branches.
+    // the consumer wave). Inactive eras get factor 0 and weight 0, which keep mean/M2 exactly.
+    // TABLE and DIR are compile-time, so the loop has no branches.
     const bool table = unit_w && a.E < RT;
     auto consume = [&](int chunk, auto table_flag, auto dir_flag) {
         constexpr bool TABLE = decltype(table_flag)::value;
@@ -778,12 +778,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
                 lg = lg + rec[j].y;
                 const float gain = rec[j].x;
                 const bool act = actv[j];
+                // An inactive era has factor 0 and weight 0 (gain +0): mean + 0 * delta and
+                // M2 + (+-0) leave both sums bit-unchanged (neither is ever -0: they start at +0
+                // and an IEEE sum is -0 only when both terms are), the reference's `continue`,
+                // with no select on the mean's chain.
                 const float delta = gain - mean;
                 const float mean_n = mean + fac[j] * delta;
-                const float wdelta = TABLE ? delta : wv[j] * delta;
-                const float M2_n = M2 + wdelta * (gain - mean_n);
-                mean = act ? mean_n : mean;
-                M2 = act ? M2_n : M2;
+                const float wdelta = TABLE ? (act ? delta : 0.0f) : wv[j] * delta;
+                M2 = M2 + wdelta * (gain - mean_n);
+                mean = mean_n;
                 if (DIR) {
                     const float w = wv[j];
                     agn = act ? agn + w * ((rec[j].w > 0.0f) ? 1.0f : -1.0f) : agn;
