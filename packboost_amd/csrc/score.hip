@@ -301,7 +301,6 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                     gtb[j] = sGt[el];
                 }
                 float facb[kRecBatch], wb[kRecBatch];
-                bool actb[kRecBatch];
 #pragma unroll
                 for (int j = 0; j < kRecBatch; ++j) {
                     const float w = (b0 + j < ne) ? fabsf(wdb[j]) : 0.0f;
@@ -309,9 +308,8 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                     const float wn = wsum + w;
                     const int wi = (int)wn;
                     facb[j] = (unit_w && wi < RT) ? (act ? exact_recip(wn) : 0.0f) : w / (act ? wn : 1.0f);
-                    wsum = act ? wn : wsum;
+                    wsum = wn;  // + (+0) when inactive
                     wb[j] = w;
-                    actb[j] = act;
                 }
 #pragma unroll
                 for (int j = 0; j < kRecBatch; ++j) {
@@ -323,16 +321,16 @@ __global__ __launch_bounds__(kBlock) void des_score_kernel(ScoreArgs a) {
                     tc += ctb[j];
                     tg = (ctb[j] != 0) ? tg + gtb[j] : tg;
                     const float w = wb[j];
-                    const bool act = actb[j];
                     const float gain = gb[j];
+                    // an inactive era (w = +0, gain = +0, factor 0) adds +-0 to every sum, which
+                    // keeps its bits (no sum is ever -0): the reference's `continue`
                     const float delta = gain - mean;
                     const float mean_n = mean + facb[j] * delta;
-                    const float M2_n = M2 + (w * delta) * (gain - mean_n);
-                    mean = act ? mean_n : mean;
-                    M2 = act ? M2_n : M2;
+                    M2 = M2 + (w * delta) * (gain - mean_n);
+                    mean = mean_n;
                     if (use_dir) {
-                        agn = act ? agn + w * ((wdb[j] > 0.0f) ? 1.0f : -1.0f) : agn;
-                        agd = act ? agd + w : agd;
+                        agn = agn + w * ((wdb[j] > 0.0f) ? 1.0f : -1.0f);
+                        agd = agd + w;
                     }
                 }
             }
@@ -488,15 +486,16 @@ __global__ __launch_bounds__(kBlock) void des_score_wide_kernel(ScoreArgs a) {
         const float wn = wsum + w;
         const int wi = (int)wn;
         const float fac = (unit_w && wi < RT) ? (act ? exact_recip(wn) : 0.0f) : w / (act ? wn : 1.0f);
-        wsum = act ? wn : wsum;
+        // an inactive era (w = +0, gain = +0, factor 0) adds +-0 to every sum, which keeps its
+        // bits (no sum is ever -0): the reference's `continue`, with no selects
+        wsum = wn;
         const float delta = gain - mean;
         const float mean_n = mean + fac * delta;
-        const float M2_n = M2 + (w * delta) * (gain - mean_n);
-        mean = act ? mean_n : mean;
-        M2 = act ? M2_n : M2;
+        M2 = M2 + (w * delta) * (gain - mean_n);
+        mean = mean_n;
         if (use_dir) {
-            agn = act ? agn + w * (pos ? 1.0f : -1.0f) : agn;
-            agd = act ? agd + w : agd;
+            agn = agn + w * (pos ? 1.0f : -1.0f);
+            agd = agd + w;
         }
     };
 
@@ -767,7 +766,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
                 } else {
                     const float wn = wsum + w;
                     fac[j] = w / (act ? wn : 1.0f);
-                    wsum = act ? wn : wsum;
+                    wsum = wn;  // + (+0) when inactive
                 }
                 wv[j] = w;
                 actv[j] = act;
@@ -789,8 +788,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(3))) voi
                 mean = mean_n;
                 if (DIR) {
                     const float w = wv[j];
-                    agn = act ? agn + w * ((rec[j].w > 0.0f) ? 1.0f : -1.0f) : agn;
-                    agd = act ? agd + w : agd;
+                    agn = agn + w * ((rec[j].w > 0.0f) ? 1.0f : -1.0f);  // + (+-0) when inactive
+                    agd = agd + w;
                 }
             }
             if (bi + 1 < kBatches) {
@@ -1928,18 +1927,20 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(seg_wave
             } else {
                 fac = w / (act ? wn : 1.0f);
             }
-            wsum[j] = act ? wn : wsum[j];
+            // an inactive era has w = +0, gain = +0 and factor 0, so every sum below takes a +-0
+            // term and keeps its bits (none is ever -0: each starts at +0, and an IEEE sum is -0
+            // only when both terms are): the reference's `continue`, with no selects
+            wsum[j] = wn;
             const float delta = gain - mean[j];
             const float mean_n = mean[j] + fac * delta;
-            const float M2_n = M2[j] + (w * delta) * (gain - mean_n);
-            mean[j] = act ? mean_n : mean[j];
-            M2[j] = act ? M2_n : M2[j];
+            M2[j] = M2[j] + (w * delta) * (gain - mean_n);
+            mean[j] = mean_n;
             if (DIR) {
                 const float lv = -GL / dL;
                 const float rv = -GR / dR;
                 const bool pos = lv > rv;
-                agn[j] = act ? agn[j] + w * (pos ? 1.0f : -1.0f) : agn[j];
-                agd[j] = act ? agd[j] + w : agd[j];
+                agn[j] = agn[j] + w * (pos ? 1.0f : -1.0f);
+                agd[j] = agd[j] + w;
             }
         }
     }
