@@ -508,7 +508,47 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             if (k0 + kk == 0) emit(Digits{u, kk, 4}, run + m[4]);
         };
         constexpr int kMaxItems = 8;  // marginals a thread holds in registers
-        if (P == 2 && nb <= 8) {
+        if (P == 2 && NIB && vec5) {
+            // 5 bins, nibble columns: one thread per (node, pair), nodes fastest. It reads the pair's 25 joint
+            // cells once, as one batch, sums the rows of the 5 x 5 block (cell b1 * 5 + b2) into
+            // the first feature's marginals and its columns into the second's, and emits both.
+            // The lanes of a wavefront read consecutive nodes' blocks, 25 cells apart, which
+            // lands them on distinct LDS banks; a thread per (node, feature) read every cell
+            // twice, with the lanes of a node's features on one bank. (The uint8 instantiations
+            // keep that form: this one spills there at their register budget.)
+            const DivU16 div_un(Un);
+            for (int t = tx; t < Un * ng; t += BS) {
+                const int g = (int)div_un.div((uint32_t)t);
+                const int u = t - g * Un;
+                const unsigned long long* hc =
+                    lds + ((int64_t)g * words_group + (int64_t)u * cells_node * C);
+                unsigned long long m0[5], m1[5];
+                // the block's rows b1 = 0-2 (15 cells), then 3-4 (10), each as one batch of
+                // reads, within the register budget of every pair instantiation
+                {
+                    unsigned long long v[15];
+    #pragma unroll
+                    for (int j = 0; j < 15; ++j) v[j] = hc[j * C];
+    #pragma unroll
+                    for (int b = 0; b < 5; ++b) m1[b] = v[b] + v[5 + b] + v[10 + b];
+    #pragma unroll
+                    for (int r = 0; r < 3; ++r)
+                        m0[r] = v[r * 5] + v[r * 5 + 1] + v[r * 5 + 2] + v[r * 5 + 3] + v[r * 5 + 4];
+                }
+                {
+                    unsigned long long v[10];
+    #pragma unroll
+                    for (int j = 0; j < 10; ++j) v[j] = hc[(15 + j) * C];
+    #pragma unroll
+                    for (int b = 0; b < 5; ++b) m1[b] += v[b] + v[5 + b];
+    #pragma unroll
+                    for (int r = 0; r < 2; ++r)
+                        m0[3 + r] = v[r * 5] + v[r * 5 + 1] + v[r * 5 + 2] + v[r * 5 + 3] + v[r * 5 + 4];
+                }
+                emit5(u, 2 * g, m0);
+                if (2 * g + 1 < nf) emit5(u, 2 * g + 1, m1);  // the partner past the tile's end: none
+            }
+        } else if (P == 2 && nb <= 8) {
             // One thread per (node, feature) of a pair: it reads the pair's nb x nb joint cells
             // once, sums its feature's marginals (side 0 over rows of the cell block, side 1 over
             // columns), and emits the running sums. Every cell is read twice (once per side)
