@@ -596,6 +596,75 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 for (int q = 0; q < kEmitBatch; ++q)
                     if (it0 + q * BS < items) emit(dd[q], v[q]);
             }
+        } else if (P == 3 && NIB && vec5) {
+            // 5 bins, nibble columns, in two steps. (1) One thread per (node, group, plane b1 of
+            // the first feature), nodes fastest: it reads the plane's 25 cells (b2 * 5 + b3) once,
+            // in two batches, and forms the first feature's marginal at b1 (all 25), the second
+            // feature's partial marginals over this plane (rows, by b2) and the third's (columns,
+            // by b3). It writes those 11 sums over the plane's first words: no other thread reads
+            // the plane. (2) One thread per (node, feature) adds its 5 marginals from the 5
+            // planes' sums and emits them. Each cell is read once, where a thread per marginal
+            // element read it three times.
+            const int ng5 = ng * 5;
+            const DivU16 div_un(Un);
+            for (int t = tx; t < Un * ng5; t += BS) {
+                const int r = (int)div_un.div((uint32_t)t);
+                const int u = t - r * Un;
+                const int g = r / 5;
+                const int b1 = r - g * 5;
+                unsigned long long* pl =
+                    lds + ((int64_t)g * words_group + (int64_t)u * cells_node * C + (int64_t)b1 * 25 * C);
+                unsigned long long s2[5], s3[5];
+                {
+                    unsigned long long v[15];
+    #pragma unroll
+                    for (int j = 0; j < 15; ++j) v[j] = pl[j * C];
+    #pragma unroll
+                    for (int b = 0; b < 5; ++b) s3[b] = v[b] + v[5 + b] + v[10 + b];
+    #pragma unroll
+                    for (int q = 0; q < 3; ++q) s2[q] = v[q * 5] + v[q * 5 + 1] + v[q * 5 + 2] + v[q * 5 + 3] + v[q * 5 + 4];
+                }
+                {
+                    unsigned long long v[10];
+    #pragma unroll
+                    for (int j = 0; j < 10; ++j) v[j] = pl[(15 + j) * C];
+    #pragma unroll
+                    for (int b = 0; b < 5; ++b) s3[b] += v[b] + v[5 + b];
+    #pragma unroll
+                    for (int q = 0; q < 2; ++q)
+                        s2[3 + q] = v[q * 5] + v[q * 5 + 1] + v[q * 5 + 2] + v[q * 5 + 3] + v[q * 5 + 4];
+                }
+                pl[0] = s2[0] + s2[1] + s2[2] + s2[3] + s2[4];
+    #pragma unroll
+                for (int b = 0; b < 5; ++b) {
+                    pl[1 + b] = s2[b];
+                    pl[6 + b] = s3[b];
+                }
+            }
+            __syncthreads();
+            for (int t = tx; t < Un * nf; t += BS) {
+                const int u = (int)div_nf.div((uint32_t)t);
+                const int kk = t - u * nf;
+                const int g = kk / 3;
+                const int side = kk - g * 3;
+                const unsigned long long* pl0 =
+                    lds + ((int64_t)g * words_group + (int64_t)u * cells_node * C);
+                unsigned long long m[5];
+                if (side == 0) {  // plane bb's total
+    #pragma unroll
+                    for (int bb = 0; bb < 5; ++bb) m[bb] = pl0[bb * 25 * C];
+                } else {  // bin bb's partial sums of the 5 planes
+                    const int off = side == 1 ? 1 : 6;
+                    unsigned long long v[25];
+    #pragma unroll
+                    for (int p = 0; p < 5; ++p)
+    #pragma unroll
+                        for (int bb = 0; bb < 5; ++bb) v[p * 5 + bb] = pl0[p * 25 * C + off + bb];
+    #pragma unroll
+                    for (int bb = 0; bb < 5; ++bb) m[bb] = v[bb] + v[5 + bb] + v[10 + bb] + v[15 + bb] + v[20 + bb];
+                }
+                emit5(u, kk, m);
+            }
         } else if (items <= kMaxItems * BS) {
             // marginals into registers, then compact them over the (no longer needed) joint cells
             // and prefix from there: nb reads per element instead of (bb + 1) * nb
