@@ -509,8 +509,8 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         };
         constexpr int kMaxItems = 8;  // marginals a thread holds in registers
         if (P == 2 && NIB && vec5) {
-            // 5 bins, nibble columns: one thread per (node, pair), nodes fastest. It reads the pair's 25 joint
-            // cells once, as one batch, sums the rows of the 5 x 5 block (cell b1 * 5 + b2) into
+            // 5 bins, nibble columns: one thread per (node, pair), nodes fastest. It reads the
+            // pair's 25 joint cells once, sums the rows of the 5 x 5 block (cell b1 * 5 + b2) into
             // the first feature's marginals and its columns into the second's, and emits both.
             // The lanes of a wavefront read consecutive nodes' blocks, 25 cells apart, which
             // lands them on distinct LDS banks; a thread per (node, feature) read every cell
