@@ -396,8 +396,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None,
-                    help="timed rounds (default 20; config 4: 10, the rounds before its default learning "
-                         "rate x B = 6.4 diverges and the trees stop at the root)")
+                    help="timed rounds (default 100, the rounds configs 2 and 3 run; config 4: 10, the "
+                         "rounds before its default learning rate x B = 6.4 diverges and the trees stop "
+                         "at the root; config 5: 20 predict calls)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed rounds first (default 3; config 4: 1)")
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--rows", type=int, default=0, help="override row count (quick runs)")
@@ -428,7 +429,7 @@ def main() -> int:
     if args.rows:
         c["rows"] = args.rows
     if args.steps is None:
-        args.steps = 10 if args.config == 4 else 20
+        args.steps = {4: 10, 5: 20}.get(args.config, 100)  # config 5: predict calls
     if args.warmup is None:
         args.warmup = 1 if args.config == 4 else 3
     torch.cuda.set_device(0)
