@@ -36,6 +36,12 @@ CASES = [
     # one node x 128 bins x 20 features (config 1's first depth): single-feature tiles of 16
     # uint8 columns, the widest single-feature launch shape
     (10, 10000, 20, 10, 128, 1, 20, 20, 1.0, 0.5, 0.0, 0.0),
+    # 5 bins, 16 nodes: 16-feature pair tiles, the last one of 7 features (a pair whose second
+    # feature lies past the tile's end)
+    (11, 16000, 30, 9, 5, 16, 23, 5, 1e-6, 0.5, 0.0, 0.0),
+    # 5 bins, 8 nodes: 12-feature triple tiles over 1000 joint cells per group (the 40 KB
+    # budget), the last tile of one feature (a group with two partners past the tile's end)
+    (12, 12000, 20, 7, 5, 8, 13, 5, 1e-6, 0.5, 0.0, 0.0),
 ]
 
 
