@@ -300,7 +300,14 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         // consecutive addresses. Each element is the exact integer prefix (count | fixed-point
         // grad) over the feature's bins 0..bb, converted once: the count exactly, the grad as the
         // float32 rounding of the exact sum.
-        const double inv_scale = ldexp(1.0, -sh);
+        // A word's grad field w = Q * 2^kCountBits (count bits cleared) as a float: Q * 2^-sh
+        // rounded once. |Q| < 2^45, so high half * 2^32 + low half is exact in double (the fma
+        // has nothing to round) and the scaling by a power of two is exact: no 64-bit shift.
+        const int grad_exp = -kCountBits - sh;
+        auto grad_f32 = [&](unsigned long long word) -> float {
+            const uint32_t lo = (uint32_t)word & ~((1u << kCountBits) - 1u);
+            return (float)ldexp(fma((double)(int32_t)(uint32_t)(word >> 32), 0x1p32, (double)lo), grad_exp);
+        };
         // Element it = (u * nf + kk) * nb + bb. Its digits come from two exact multiply-high
         // divisions by the uniform nb and nf (a runtime integer division is a long VALU sequence
         // and the flush decodes every element).
@@ -469,8 +476,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         const int64_t row0 = ((int64_t)era * a.U + u0) * a.K + k0;  // (node u0, feature k0)
         auto emit = [&](const Digits& d, unsigned long long tot) {
             const uint32_t cnt = (uint32_t)(tot & ((1ull << kCountBits) - 1ull));
-            const long long Q = ((long long)(tot - cnt)) >> kCountBits;
-            const float gs = (float)((double)Q * inv_scale);
+            const float gs = grad_f32(tot);
             if (d.bb < pt) {
                 const int64_t o = (row0 + (int64_t)d.u * a.K + d.kk) * pt + d.bb;
                 if (a.out_cnt32)
@@ -500,7 +506,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
                 run += m[bb];
                 const uint32_t cnt = (uint32_t)(run & ((1ull << kCountBits) - 1ull));
                 cp[bb] = (uint16_t)cnt;
-                gp[bb] = (float)((double)(((long long)(run - cnt)) >> kCountBits) * inv_scale);
+                gp[bb] = grad_f32(run);
             }
             const int64_t o = (row0 + (int64_t)u * a.K + kk) * 4;
             *reinterpret_cast<ushort4*>(a.out_cnt + o) = cv;
