@@ -425,7 +425,9 @@ int hist_build(pb_ctx* c, const uint8_t* bins, int64_t ld_bytes, int32_t nibble,
     const int64_t per_group = cells_group * (int64_t(1) << clog2) * 8;
     while (groups > 1 && groups * per_group > 160 * 1024) groups /= 2;  // forced copies
     const int ftile = (int)groups * P;
-    const size_t lds_bytes = (size_t)(groups * per_group);
+    const size_t lds_bytes =
+        (size_t)groups * 8 *
+        (size_t)pb::hist_group_words((int)(per_group / 8), P, nb, 1 << clog2, (int)groups);
     if (lds_bytes > 160 * 1024)
         return fail(PB_ERR_UNSUPPORTED,
                     "pb_hist_build: one feature's node x bin histogram exceeds the 160 KiB LDS");

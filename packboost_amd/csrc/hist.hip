@@ -96,7 +96,7 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
     const int cells_node = (P == 3) ? nb * nb * nb : (P == 2) ? nb * nb : nb;  // joint cells/node
     const int C = 1 << a.clog2;
     const int UT = a.node_tile;                      // nodes held in LDS per work item
-    const int words_group = UT * cells_node * C;     // LDS words per group
+    const int words_group = hist_group_words(UT * cells_node * C, P, nb, C, G);  // LDS words per group
     const uint32_t copy = threadIdx.x & (C - 1);
     const uint32_t bin_shift = (uint32_t)a.clog2 + 3u;  // cell -> byte offset of its C copies
 
@@ -515,17 +515,26 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
         };
         constexpr int kMaxItems = 8;  // marginals a thread holds in registers
         if (P == 2 && NIB && vec5) {
-            // 5 bins, nibble columns: one thread per (node, pair), nodes fastest. It reads the
+            // 5 bins, nibble columns: one thread per (node, pair), pairs fastest. It reads the
             // pair's 25 joint cells once, sums the rows of the 5 x 5 block (cell b1 * 5 + b2) into
             // the first feature's marginals and its columns into the second's, and emits both.
-            // The lanes of a wavefront read consecutive nodes' blocks, 25 cells apart, which
-            // lands them on distinct LDS banks; a thread per (node, feature) read every cell
-            // twice, with the lanes of a node's features on one bank. (The uint8 instantiations
-            // keep that form: this one spills there at their register budget.)
-            const DivU16 div_un(Un);
+            // Consecutive lanes take one node's pairs, so a wavefront's plane stores cover a few
+            // whole runs of consecutive features instead of one 8- or 16-byte piece per node;
+            // the padded group stride (hist_group_words) keeps their cell reads on distinct LDS
+            // banks. A thread per (node, feature) read every cell twice. (The uint8
+            // instantiations keep that form: this one spills there at their register budget.)
+            // (Tiles of one or two pairs keep nodes fastest: their few groups gain little, and
+            // that order keeps the one-pair instantiation within its registers.)
+            const DivU16 div_ng(ng), div_un(Un);
             for (int t = tx; t < Un * ng; t += BS) {
-                const int g = (int)div_un.div((uint32_t)t);
-                const int u = t - g * Un;
+                int u, g;
+                if (G >= 4) {
+                    u = (int)div_ng.div((uint32_t)t);
+                    g = t - u * ng;
+                } else {
+                    g = (int)div_un.div((uint32_t)t);
+                    u = t - g * Un;
+                }
                 const unsigned long long* hc =
                     lds + ((int64_t)g * words_group + (int64_t)u * cells_node * C);
                 unsigned long long m0[5], m1[5];

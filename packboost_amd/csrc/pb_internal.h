@@ -86,6 +86,22 @@ __device__ __forceinline__ unsigned long long grad_addend(float g, float scale) 
     return ((unsigned long long)ahi << 32) | ((lo << kCountBits) | 1u);
 }
 
+// LDS words per feature group of hist_era_kernel: `cells` words (a group's joint cells over the
+// item's nodes, times the copies), padded for 5-bin pairs with one copy in tiles of 4 or more
+// groups. Their flush gives the lanes of a wavefront the groups of one node, then the next
+// node's (so that each node's plane stores are contiguous); a group stride that is an odd
+// multiple of 32 / groups words (groups rounded up to a power of two) puts the 32 lanes of a
+// half-wave, whose node offsets 25 u differ modulo 32 / groups, on distinct pairs of LDS banks.
+__host__ __device__ inline int hist_group_words(int cells, int P, int nb, int C, int groups) {
+    if (!(P == 2 && nb == 5 && C == 1 && groups >= 4)) return cells;
+    int g2 = 1;
+    while (g2 < groups) g2 *= 2;
+    const int q = 32 / (g2 < 32 ? g2 : 32);
+    int s = (cells + q - 1) / q * q;
+    if (((s / q) & 1) == 0) s += q;
+    return s;
+}
+
 // IEEE 1/n for an integer-valued float n in [1, 2^20]: the hardware reciprocal (within one ulp)
 // and one Newton step with fused multiply-adds give the correctly rounded value, checked bit for
 // bit against the IEEE division for every n in that range on gfx950. The scorers' unit-weight
