@@ -836,6 +836,11 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
                "segment round begin launch");
     }
     const int32_t fused_from = seg ? c->seg_from : c->d.max_depth;
+    // the last partition can take the round end's work when its vector accesses are aligned
+    const bool end_fusable = !(reinterpret_cast<uintptr_t>(b->preds_dev) & 15) &&
+                             !(reinterpret_cast<uintptr_t>(b->nid_dev) & 15) &&
+                             !(reinterpret_cast<uintptr_t>(b->tnode_dev) & 15) && b->pack_size >= 1 &&
+                             c->d.num_rows <= c->rows_padded;
     for (int d = 0; d < c->d.max_depth; ++d) {
         const int32_t m = max_nodes_at(c, d);
         const int32_t* f = feats + (int64_t)d * K;
@@ -884,13 +889,21 @@ int pb_grow_round(pb_ctx* c, const pb_fit_buffers* b, const int32_t* feats, int3
                    "segment partition launch");
             if (!last) c->seg_cur = 1 - i;
         }
-        // the plane path's row ids: every depth without segments (the last one leaves the
-        // leaves for pb_round_end), else while a later depth's histogram still reads them
-        if ((!seg || d + 1 < fused_from) &&
-            (rc = partition(c, bins, ld_bytes, nib, d, b->nid_dev, b->tnode_dev, stream)))
+        // the plane path's row ids: every depth without segments, else while a later depth's
+        // histogram still reads them. Without segments the last depth's partition also does
+        // the round end (each row's prediction from its final node, and the round header).
+        if (!seg && d + 1 == c->d.max_depth && end_fusable) {
+            PB_HIP(pb::launch_partition_end(bins, ld_bytes, nib, c->rows_padded, c->rules, c->st, d, b->nid_dev,
+                                            b->tnode_dev, b->values_dev, b->pack_size, b->learning_rate,
+                                            b->preds_dev, c->d.num_rows, header, (hipStream_t)stream),
+                   "partition + round end launch");
+        } else if ((!seg || d + 1 < fused_from) &&
+                   (rc = partition(c, bins, ld_bytes, nib, d, b->nid_dev, b->tnode_dev, stream))) {
             return rc;
+        }
         if ((rc = mark(4))) return rc;
     }
+    if (!seg && end_fusable) return PB_OK;
     // the round-end kernel also writes the round's header (its first workgroup)
     if (seg) {
         const pb::SegBuffers& cur = c->sb[c->seg_cur];

@@ -16,16 +16,42 @@ namespace {
 
 constexpr int kMaxRulesLds = 2048;
 
+// pb_round_end's inputs, for the round's last partition (partition_kernel<true>)
+struct RoundEndArgs {
+    const float* values;      // leaf value per TreeBuilder id
+    int32_t B;                // pack size
+    float lr;
+    float* preds;             // [N], 16-byte aligned
+    int64_t N;
+    pb_round_header* header;  // written by the first workgroup (may be null)
+};
+
+// One pack step of a row's prediction: its leaf value added B times in float32, times lr, added
+// to the prediction (the reference's pack aggregation, booster.py:585-597).
+__device__ __forceinline__ float pack_step(float p, float v, int32_t B, float lr) {
+    float s = 0.0f;
+    for (int t = 0; t < B; ++t) s = s + v;
+    const float tmp = lr * s;
+    return p + tmp;
+}
+
+// END: the round's last depth, which also does pb_round_end's work: every row's prediction
+// takes its final node's leaf value (rows whose node stopped at an earlier depth too), with
+// the same float operations as round_end_kernel, so the round needs no separate pass over the
+// rows' tree nodes and predictions.
+template <bool END>
 __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __restrict__ bins,
                                                        int64_t ld, int32_t nibble,
                                                        int64_t rows_padded,
                                                        const SplitRule* __restrict__ rules,
                                                        const Frontier* st, int32_t depth,
                                                        uint16_t* __restrict__ nid,
-                                                       uint16_t* __restrict__ tnode) {
+                                                       uint16_t* __restrict__ tnode,
+                                                       RoundEndArgs re) {
     __shared__ SplitRule s_rules[kMaxRulesLds];
     const int Ua = st->u_active[depth];
-    if (Ua <= 0) return;
+    if (END && re.header && blockIdx.x == 0) write_round_header(st, re.header);
+    if (!END && Ua <= 0) return;
     const bool in_lds = Ua <= kMaxRulesLds;
     // 8 rows per thread (rows_padded is a multiple of 16): one 16-byte load of their node ids and
     // one of their tree nodes, then their bin gathers all in flight before any result is needed.
@@ -42,23 +68,9 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
         for (int u = threadIdx.x; u < Ua; u += kBlock) s_rules[u] = rules[u];
         __syncthreads();
     }
-    for (; r < rows_padded; r += stride) {
-        if (r != ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8) {  // later groups
-            nn = *reinterpret_cast<const uint4*>(nid + r);
-            tt = *reinterpret_cast<const uint4*>(tnode + r);
-        }
-        uint32_t nw[4] = {nn.x, nn.y, nn.z, nn.w};
-        uint32_t n8[8];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            n8[q * 2] = nw[q] & 0xffffu;
-            n8[q * 2 + 1] = nw[q] >> 16;
-        }
-        bool any = false;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) any = any || n8[j] < (uint32_t)Ua;
-        if (!any) continue;  // PB_INACTIVE or stale rows only
-        uint32_t tw[4] = {tt.x, tt.y, tt.z, tt.w};
+    // the 8 rows of group r that sit in an active node move to their child (left iff bin <=
+    // threshold); their new ids are stored
+    auto split_rows = [&](int64_t r, uint32_t (&nw)[4], const uint32_t (&n8)[8], uint32_t (&tw)[4]) {
         SplitRule rr[8];
         uint32_t bin[8];
 #pragma unroll
@@ -94,6 +106,53 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
         }
         *reinterpret_cast<uint4*>(nid + r) = make_uint4(nw[0], nw[1], nw[2], nw[3]);
         *reinterpret_cast<uint4*>(tnode + r) = make_uint4(tw[0], tw[1], tw[2], tw[3]);
+    };
+    for (; r < rows_padded; r += stride) {
+        if (r != ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8) {  // later groups
+            nn = *reinterpret_cast<const uint4*>(nid + r);
+            tt = *reinterpret_cast<const uint4*>(tnode + r);
+        }
+        // END: the 8 rows' predictions, read with the ids (rows at or past N are not read)
+        float pr[8];
+        if (END) {
+            if (r + 8 <= re.N) {
+                const float4 p0 = *reinterpret_cast<const float4*>(re.preds + r);
+                const float4 p1 = *reinterpret_cast<const float4*>(re.preds + r + 4);
+                pr[0] = p0.x; pr[1] = p0.y; pr[2] = p0.z; pr[3] = p0.w;
+                pr[4] = p1.x; pr[5] = p1.y; pr[6] = p1.z; pr[7] = p1.w;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pr[j] = r + j < re.N ? re.preds[r + j] : 0.0f;
+            }
+        }
+        uint32_t nw[4] = {nn.x, nn.y, nn.z, nn.w};
+        uint32_t n8[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            n8[q * 2] = nw[q] & 0xffffu;
+            n8[q * 2 + 1] = nw[q] >> 16;
+        }
+        bool any = false;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) any = any || n8[j] < (uint32_t)Ua;
+        uint32_t tw[4] = {tt.x, tt.y, tt.z, tt.w};
+        if (any) split_rows(r, nw, n8, tw);  // else PB_INACTIVE or stale rows only
+        if (END) {
+            // each row's final node: its leaf value, added as in round_end_kernel
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t tv = (tw[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
+                pr[j] = pack_step(pr[j], re.values[tv], re.B, re.lr);
+            }
+            if (r + 8 <= re.N) {
+                *reinterpret_cast<float4*>(re.preds + r) = make_float4(pr[0], pr[1], pr[2], pr[3]);
+                *reinterpret_cast<float4*>(re.preds + r + 4) = make_float4(pr[4], pr[5], pr[6], pr[7]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (r + j < re.N) re.preds[r + j] = pr[j];
+            }
+        }
     }
 }
 
@@ -217,12 +276,6 @@ __global__ void select_subsets_kernel(const pb_round_header* prev, int32_t D, in
 // (torch: tmp = lr * pack_sum; preds += tmp). VEC: 4 rows per thread with one 8-byte tree-node
 // and one 16-byte prediction access (the host checks the alignment), the last N % 4 rows one by
 // one.
-__device__ __forceinline__ float pack_step(float p, float v, int32_t B, float lr) {
-    float s = 0.0f;
-    for (int t = 0; t < B; ++t) s = s + v;
-    const float tmp = lr * s;
-    return p + tmp;
-}
 
 template <bool VEC>
 __global__ __launch_bounds__(kBlock) void round_end_kernel(const uint16_t* __restrict__ tnode,
@@ -265,8 +318,20 @@ hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s) {
     const int grid = grid_for(rows_padded / 8, kBlock, 8192);
-    hipLaunchKernelGGL(partition_kernel, dim3(grid), dim3(kBlock), 0, s, bins, ld, nibble,
-                       rows_padded, rules, st, depth, nid, tnode);
+    hipLaunchKernelGGL(partition_kernel<false>, dim3(grid), dim3(kBlock), 0, s, bins, ld, nibble,
+                       rows_padded, rules, st, depth, nid, tnode, RoundEndArgs{});
+    return hipGetLastError();
+}
+
+hipError_t launch_partition_end(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
+                                const SplitRule* rules, const Frontier* st, int32_t depth, uint16_t* nid,
+                                uint16_t* tnode, const float* values, int32_t pack_size, float lr,
+                                float* preds, int64_t N, pb_round_header* header, hipStream_t s) {
+    if (!aligned(preds, 16) || N > rows_padded) return hipErrorInvalidValue;
+    const int grid = grid_for(rows_padded / 8, kBlock, 8192);
+    hipLaunchKernelGGL(partition_kernel<true>, dim3(grid), dim3(kBlock), 0, s, bins, ld, nibble,
+                       rows_padded, rules, st, depth, nid, tnode,
+                       RoundEndArgs{values, pack_size, lr, preds, N, header});
     return hipGetLastError();
 }
 

@@ -355,6 +355,12 @@ hipError_t launch_select_subsets(const pb_round_header* prev, int32_t D, int32_t
 hipError_t launch_partition(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
                             const SplitRule* rules, const Frontier* st, int32_t depth,
                             uint16_t* nid, uint16_t* tnode, hipStream_t s);
+// The round's last partition together with launch_round_end's work (preds 16-byte aligned,
+// N <= rows_padded; hipErrorInvalidValue otherwise, and nothing is launched).
+hipError_t launch_partition_end(const uint8_t* bins, int64_t ld, int32_t nibble, int64_t rows_padded,
+                                const SplitRule* rules, const Frontier* st, int32_t depth, uint16_t* nid,
+                                uint16_t* tnode, const float* values, int32_t pack_size, float lr,
+                                float* preds, int64_t N, pb_round_header* header, hipStream_t s);
 // Also writes win_sum [ceil(rows_padded / kGradWinRows)] (sum of |grad| per window) and
 // sh_era [E] (era_grad_scale of each era, eras at era_off [E+1]).
 hipError_t launch_round_begin(const float* preds, const float* y, float* grad, uint16_t* nid,
