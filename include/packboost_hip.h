@@ -249,9 +249,11 @@ typedef struct {
 
 /* One whole boosting round (booster.py:494-599) as a single asynchronous enqueue:
  * pb_round_begin, then for every depth pb_hist_build -> pb_des_score -> pb_decide ->
- * pb_partition, then pb_round_end. feats_dev: int32 [D][K] feature subsets (the host draws
- * them, booster.py:519, 787-792); decisions_dev: pb_decision [2^D - 1]; header_dev: the
- * round's pb_round_header. Depths whose frontier is empty run no work. */
+ * pb_partition, then pb_round_end (the last depth's partition and the round end run as one
+ * launch when preds, nid and tnode are 16-byte aligned; the results are the same). feats_dev:
+ * int32 [D][K] feature subsets (the host draws them, booster.py:519, 787-792); decisions_dev:
+ * pb_decision [2^D - 1]; header_dev: the round's pb_round_header. Depths whose frontier is
+ * empty run no work. */
 int pb_grow_round(pb_ctx* ctx, const pb_fit_buffers* buffers, const int32_t* feats_dev, int32_t K,
                   pb_decision* decisions_dev, pb_round_header* header_dev, void* stream);
 
