@@ -64,6 +64,20 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
         nn = *reinterpret_cast<const uint4*>(nid + r);
         tt = *reinterpret_cast<const uint4*>(tnode + r);
     }
+    // END: the 8 rows' predictions, read with their ids (rows at or past N are not read)
+    float pr[8];
+    auto load_preds = [&](int64_t r) {
+        if (r + 8 <= re.N) {
+            const float4 p0 = *reinterpret_cast<const float4*>(re.preds + r);
+            const float4 p1 = *reinterpret_cast<const float4*>(re.preds + r + 4);
+            pr[0] = p0.x; pr[1] = p0.y; pr[2] = p0.z; pr[3] = p0.w;
+            pr[4] = p1.x; pr[5] = p1.y; pr[6] = p1.z; pr[7] = p1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pr[j] = r + j < re.N ? re.preds[r + j] : 0.0f;
+        }
+    };
+    if (END) load_preds(r);
     if (in_lds) {
         for (int u = threadIdx.x; u < Ua; u += kBlock) s_rules[u] = rules[u];
         __syncthreads();
@@ -111,19 +125,7 @@ __global__ __launch_bounds__(kBlock) void partition_kernel(const uint8_t* __rest
         if (r != ((int64_t)blockIdx.x * kBlock + threadIdx.x) * 8) {  // later groups
             nn = *reinterpret_cast<const uint4*>(nid + r);
             tt = *reinterpret_cast<const uint4*>(tnode + r);
-        }
-        // END: the 8 rows' predictions, read with the ids (rows at or past N are not read)
-        float pr[8];
-        if (END) {
-            if (r + 8 <= re.N) {
-                const float4 p0 = *reinterpret_cast<const float4*>(re.preds + r);
-                const float4 p1 = *reinterpret_cast<const float4*>(re.preds + r + 4);
-                pr[0] = p0.x; pr[1] = p0.y; pr[2] = p0.z; pr[3] = p0.w;
-                pr[4] = p1.x; pr[5] = p1.y; pr[6] = p1.z; pr[7] = p1.w;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) pr[j] = r + j < re.N ? re.preds[r + j] : 0.0f;
-            }
+            if (END) load_preds(r);
         }
         uint32_t nw[4] = {nn.x, nn.y, nn.z, nn.w};
         uint32_t n8[8];
