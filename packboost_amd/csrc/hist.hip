@@ -613,20 +613,22 @@ void hist_era_kernel(HistArgs a, const int4* __restrict__ seg_info, const int32_
             }
         } else if (P == 3 && NIB && vec5) {
             // 5 bins, nibble columns, in two steps. (1) One thread per (node, group, plane b1 of
-            // the first feature), nodes fastest: it reads the plane's 25 cells (b2 * 5 + b3) once,
-            // in two batches, and forms the first feature's marginal at b1 (all 25), the second
-            // feature's partial marginals over this plane (rows, by b2) and the third's (columns,
-            // by b3). It writes those 11 sums over the plane's first words: no other thread reads
+            // the first feature), planes fastest, then nodes (a half-wave's plane and node
+            // offsets, 25 b1 + 125 u words, then fall on distinct LDS bank pairs at 2, 4 and 8
+            // nodes, where nodes fastest put two lanes on one bank pair). It reads the plane's
+            // 25 cells (b2 * 5 + b3) once, in two batches, and forms the first feature's marginal
+            // at b1 (all 25), the second feature's partial marginals over this plane (rows, by
+            // b2) and the third's (columns, by b3). It writes those 11 sums over the plane's first words: no other thread reads
             // the plane. (2) One thread per (node, feature) adds its 5 marginals from the 5
             // planes' sums and emits them. Each cell is read once, where a thread per marginal
             // element read it three times.
             const int ng5 = ng * 5;
             const DivU16 div_un(Un);
             for (int t = tx; t < Un * ng5; t += BS) {
-                const int r = (int)div_un.div((uint32_t)t);
-                const int u = t - r * Un;
-                const int g = r / 5;
-                const int b1 = r - g * 5;
+                const int q = t / 5;  // (node, group)
+                const int b1 = t - q * 5;
+                const int g = (int)div_un.div((uint32_t)q);
+                const int u = q - g * Un;
                 unsigned long long* pl =
                     lds + ((int64_t)g * words_group + (int64_t)u * cells_node * C + (int64_t)b1 * 25 * C);
                 unsigned long long s2[5], s3[5];
